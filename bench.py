@@ -1,0 +1,321 @@
+#!/usr/bin/env python
+"""Benchmark of the INT4 W4A16 dequant-matmul path on one MI355X.
+
+Workload: the seven linears of a Llama-3.1-8B
+decoder layer at M=1 (q/o 4096->4096, k/v 4096->1024, gate/up 4096->14336,
+down 14336->4096), INT4 g128 asymmetric RTN, fp16 activations ~N(0,1),
+weights ~N(0, 0.02), all seeded. One "step" runs those seven layers for all 32
+decoder layers, each with its own weights (3.5 GB of packed INT4), so every
+call streams its weights from HBM rather than from the 256 MB Infinity Cache.
+The step is captured once in a HIP graph and replayed.
+
+Printed JSON line: value = aggregate algorithmic HBM throughput (GB/s) of the
+step; "roofline" is that of the dominant kernel (the gate/up GEMV),
+"cpu_baseline" the reference's dequantize-on-the-fly path restated on the
+host CPU (oracle, timed on a bounded sample), "detail" per-layer µs / GB/s and
+the M=64 MFMA GEMM TFLOP/s.
+
+Algorithmic bytes per call: N*K/2 (INT4 codes) + N*G*(4 + 1) (fp32 scale +
+u8 zero, the format the kernels read) + M*K*2 (x) + M*N*2 (y); FLOPs 2*M*N*K.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "W4A16 layer µs + HBM GB/s (% peak) at M=1; TFLOP/s (% MFMA peak) at M=64"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+GS = 128
+N_LAYERS = 32
+LLAMA = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+         ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_bytes(N, K, M, scale_b=4, zero_b=1):
+    return N * K // 2 + N * (K // GS) * (scale_b + zero_b) + M * K * 2 + M * N * 2
+
+
+class Layer:
+    """Device buffers of one INT4 linear in the kernels' format."""
+
+    def __init__(self, name, N, K, seed, dev):
+        import torch
+
+        import pare_amd as P
+
+        self.name, self.N, self.K = name, N, K
+        g = torch.Generator(device=dev).manual_seed(seed)
+        w = torch.randn(N, K, generator=g, device=dev) * 0.02
+        packed, scale, zero = P.rtn_quantize(w, GS)
+        del w
+        self.w = P.repack_int4_for_kernel(packed, GS)
+        self.s = scale.reshape(N, K // GS).contiguous()
+        self.z = P.zeros_to_u8(zero)
+        del packed, scale, zero
+
+
+def launch(L, lay, x, y, M, stream):
+    from pare_amd import _lib
+
+    rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, lay.w.data_ptr(), lay.s.data_ptr(),
+                            lay.z.data_ptr(), _lib.PMI_U8, None, y.data_ptr(), _lib.PMI_F16,
+                            M, lay.N, lay.K, GS, stream)
+    if rc != 0:
+        raise RuntimeError(_lib.last_error())
+
+
+def capture(fn, stream):
+    """Captures fn() (a sequence of launches on `stream`) into a HIP graph."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn(torch.cuda.current_stream().cuda_stream)
+    return g
+
+
+def time_graph(g, reps, stream):
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps  # ms
+
+
+def cpu_baseline(max_threads=16):
+    """The reference's dequantize-on-the-fly forward on the host CPU, op for op
+    (oracle.dequant_path_forward_torch), on one decoder layer's seven linears at
+    M=1: 1 warmup + 3 timed passes per layer, median per layer."""
+    import numpy as np
+    import torch
+
+    from oracle import pare_oracle as O
+
+    threads = min(len(os.sched_getaffinity(0)), max_threads)
+    torch.set_num_threads(threads)
+    total_bytes, total_s = 0, 0.0
+    g = torch.Generator().manual_seed(1234)
+    for i, (name, N, K) in enumerate(LLAMA):
+        w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+        packed, s, z = O.rtn_quantize(w, GS)
+        tp, ts, tz = torch.from_numpy(packed), torch.from_numpy(s), torch.from_numpy(z)
+        x = torch.randn(1, K, generator=g).to(torch.float16)
+        O.dequant_path_forward_torch(x, tp, ts, tz)
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.dequant_path_forward_torch(x, tp, ts, tz)
+            times.append(time.perf_counter() - t0)
+        total_s += statistics.median(times)
+        total_bytes += layer_bytes(N, K, 1, 4, 4)
+    return {"value": round(total_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": "one Llama-3.1-8B decoder layer's 7 INT4 g128 linears at M=1 through the "
+                      "oracle's op-for-op restatement of the reference dequant path "
+                      "(unpack->float->(q-z)*s->fp16->F.linear) on the host CPU; median of 3 "
+                      "after 1 warmup per layer; bytes in the reference layout (fp32 s+z)",
+            "ms_per_layer_set": round(total_s * 1e3, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=N_LAYERS)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kernel-only", choices=["gate_m1", "gate_m64", "copy"], default=None,
+                    help="run only one kernel loop (for rocprofv3 counter passes)")
+    ap.add_argument("--sweep", action="store_true", help="also run the gate_proj M sweep")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only (the INT4 linear path has no "
+                                   "multi-GPU component); run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+
+    import pare_amd as P
+    from pare_amd import _lib
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    assert P.kernel_available(), "libpare_amd.so is not built or the device is not gfx950"
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    stream = torch.cuda.Stream(dev)
+
+    if args.kernel_only == "copy":
+        # plain copy of known size: calibrates the FETCH_SIZE / WRITE_SIZE counters
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(10):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copy: 10 x 256 MiB")
+        return
+
+    n_layers = args.layers
+    t0 = time.time()
+    layers = [[Layer(name, N, K, 1000 * l + i, dev) for i, (name, N, K) in enumerate(LLAMA)]
+              for l in range(n_layers)]
+    torch.cuda.synchronize()
+    log(f"setup: {n_layers} layers x 7 linears quantised on device in {time.time() - t0:.1f}s")
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    xh = torch.randn(64, 4096, generator=g, device=dev).to(torch.float16)
+    xf = torch.randn(64, 14336, generator=g, device=dev).to(torch.float16)
+    outs = {name: torch.empty(64, N, dtype=torch.float16, device=dev) for name, N, _ in LLAMA}
+
+    def step(s, M=1):
+        for lay_set in layers:
+            for lay in lay_set:
+                x = xf if lay.name == "down" else xh
+                launch(L, lay, x, outs[lay.name], M, s)
+
+    def gate_loop(s, M, copies):
+        for i in range(copies):
+            lay = layers[i % n_layers][4 + (i // n_layers) % 2]  # gate and up of all layers
+            launch(L, lay, xh, outs["gate"], M, s)
+
+    if args.kernel_only in ("gate_m1", "gate_m64"):
+        M = 1 if args.kernel_only == "gate_m1" else 64
+        with torch.cuda.stream(stream):
+            for _ in range(5):
+                gate_loop(stream.cuda_stream, M, 2 * n_layers)
+        torch.cuda.synchronize()
+        log(f"{args.kernel_only}: 5 x {2 * n_layers} launches")
+        return
+
+    # --- eager vs graph: same outputs -------------------------------------
+    with torch.cuda.stream(stream):
+        step(stream.cuda_stream)
+    torch.cuda.synchronize()
+    eager = {k: v[:1].clone() for k, v in outs.items()}
+    graph = capture(step, stream)
+    for k in outs:
+        outs[k].zero_()
+    for rep in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        for k in outs:
+            assert torch.equal(outs[k][:1], eager[k]), f"graph replay {rep} differs on {k}"
+    log("graph replay == eager outputs")
+
+    # --- timed region: K replays of the decode-layer-set step -------------
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms_step = time_graph(graph, args.steps, stream)
+    step_bytes = n_layers * sum(layer_bytes(N, K, 1) for _, N, K in LLAMA)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"step: {ms_step * 1e3:.1f} us for {n_layers}x7 linears, {value:.1f} GB/s")
+
+    # --- per-layer shape: graph of back-to-back launches over 32 copies ----
+    detail = {}
+    for i, (name, N, K) in enumerate(LLAMA):
+        def one(s, i=i, name=name):
+            for l in range(n_layers):
+                launch(L, layers[l][i], xf if name == "down" else xh, outs[name], 1, s)
+        gi = capture(one, stream)
+        for _ in range(2):
+            gi.replay()
+        us = time_graph(gi, 10, stream) * 1e3 / n_layers
+        gbs = layer_bytes(N, K, 1) / (us * 1e-6) / 1e9
+        detail[name] = {"N": N, "K": K, "us": round(us, 2), "GB/s": round(gbs, 1),
+                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
+                        "kernel": P.kernel_choice(1, N, K, GS)}
+        log(f"  {name:5s} {N:6d}x{K:6d} M=1: {us:7.2f} us {gbs:8.1f} GB/s")
+
+    # --- dominant kernel (gate/up GEMV) for the roofline --------------------
+    copies = 2 * n_layers
+    gg = capture(lambda s: gate_loop(s, 1, copies), stream)
+    for _ in range(2):
+        gg.replay()
+    gate_us = time_graph(gg, 10, stream) * 1e3 / copies
+    gate_bytes = layer_bytes(14336, 4096, 1)
+    gate_gbs = gate_bytes / (gate_us * 1e-6) / 1e9
+
+    # --- M = 64 MFMA GEMM on gate_proj --------------------------------------
+    gm = capture(lambda s: gate_loop(s, 64, copies), stream)
+    for _ in range(2):
+        gm.replay()
+    m64_us = time_graph(gm, 5, stream) * 1e3 / copies
+    m64_tflops = 2 * 64 * 14336 * 4096 / (m64_us * 1e-6) / 1e12
+    m64_gbs = layer_bytes(14336, 4096, 64) / (m64_us * 1e-6) / 1e9
+    detail["gate_m64"] = {"us": round(m64_us, 2), "TFLOP/s": round(m64_tflops, 1),
+                          "mfma_frac": round(m64_tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                          "GB/s": round(m64_gbs, 1), "kernel": P.kernel_choice(64, 14336, 4096, GS)}
+    log(f"  gate M=64: {m64_us:.2f} us {m64_tflops:.1f} TFLOP/s {m64_gbs:.1f} GB/s")
+
+    if args.sweep:
+        sweep = {}
+        for M in (1, 2, 4, 8, 16, 32, 64, 128):
+            gs_ = capture(lambda s, M=M: gate_loop(s, M, copies), stream)
+            gs_.replay()
+            us = time_graph(gs_, 5, stream) * 1e3 / copies
+            sweep[M] = {"us": round(us, 2),
+                        "GB/s": round(layer_bytes(14336, 4096, M) / (us * 1e-6) / 1e9, 1),
+                        "TFLOP/s": round(2 * M * 14336 * 4096 / (us * 1e-6) / 1e12, 2),
+                        "kernel": P.kernel_choice(M, 14336, 4096, GS)}
+            log(f"  sweep gate M={M:3d}: {sweep[M]}")
+        detail["gate_sweep"] = sweep
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_gemv_gate_m1.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded; weights N(0,0.02) RTN INT4 g128 asym, x N(0,1))",
+        "config": {"workload": f"Llama-3.1-8B decode linear set at M=1: {n_layers} layers x "
+                               "(q,k,v,o 4096/1024, gate/up 14336, down 14336->4096), INT4 g128",
+                   "M": 1, "group_size": GS, "layers": n_layers,
+                   "bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "w4a16_gemv (gate/up 4096->14336, M=1)",
+                     "avg_launch_us": round(gate_us, 3), "bytes_per_launch": gate_bytes},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

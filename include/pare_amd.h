@@ -1,0 +1,134 @@
+/*
+ * pare_amd.h — C ABI of the MI355X (gfx950) INT4 W4A16 dequant-matmul library
+ * (libpare_amd.so).
+ *
+ * This library is a drop-in for the kernel path of Pare's QuantizedLinear
+ * (use_kernel=True). Every entry point below names the reference interface it
+ * replaces, as /root/reference file:line.
+ *
+ * Conventions shared by all entry points
+ *  - Pointers are device pointers (HIP), except where noted. Shapes are int64.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream). All
+ *    work is enqueued asynchronously on it; nothing synchronises the host.
+ *  - Return value: PMI_OK (0) or a negative PMI_ERR_* code. On error a
+ *    message is available from pmi_last_error() (thread-local). Argument
+ *    validation happens on the host before anything is launched, so an
+ *    invalid call has no device side effects.
+ *  - No entry point allocates device memory.
+ *
+ * Data layouts (identical to the reference buffers)
+ *  - packed "storage" layout, u8 [N, K/2]: byte b of row n holds
+ *    q[n,2b] in bits 0-3 and q[n,2b+1] in bits 4-7      (pare/core/pack.py:29-48)
+ *  - packed "kernel" layout, u8 [N, K/2]: inside every group_size-wide tile
+ *    starting at column k0, byte j (0 <= j < gs/2) holds q[n,k0+j] in bits 0-3
+ *    and q[n,k0+gs/2+j] in bits 4-7                      (pare/core/pack.py:88-132)
+ *  - scales fp32 [N, G] with G = K / group_size            (pare/kernels/matmul_int4.py:219-228)
+ *  - zeros  fp32 [N, G] (integer values in [0,15]) or u8 [N, G]
+ *  - Dequantisation: w = (float(q) - zero) * scale in fp32  (pare/core/functional.py:78-91)
+ */
+#ifndef PARE_AMD_H
+#define PARE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PMI_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define PMI_API __attribute__((visibility("default")))
+#else
+#define PMI_API
+#endif
+
+/* status codes */
+#define PMI_OK               0
+#define PMI_ERR_INVALID     -1 /* bad argument (shape, dtype, alignment, null pointer) */
+#define PMI_ERR_UNSUPPORTED -2 /* well-formed but outside what the kernels implement   */
+#define PMI_ERR_HIP         -3 /* the HIP runtime reported an error                     */
+#define PMI_ERR_NO_DEVICE   -4 /* no usable gfx950 device                               */
+
+/* element types */
+#define PMI_F16  0
+#define PMI_BF16 1
+#define PMI_F32  2
+#define PMI_U8   3
+
+/* packed weight layouts */
+#define PMI_LAYOUT_STORAGE 0 /* pack_int4 order            */
+#define PMI_LAYOUT_KERNEL  1 /* repack_int4_for_kernel order */
+
+/* Library version (PMI_ABI_VERSION). No reference counterpart. */
+PMI_API int pmi_abi_version(void);
+
+/* Message of the last error on the calling thread ("" if none). Host-only. */
+PMI_API const char* pmi_last_error(void);
+
+/* 1 if `device` exists and is a gfx950 GPU, 0 if not, PMI_ERR_NO_DEVICE when
+ * no HIP device is present at all.
+ * Replaces: triton_available()                 pare/kernels/matmul_int4.py:246-248 */
+PMI_API int pmi_device_supported(int device);
+
+/* Storage layout -> kernel layout, one device pass.
+ * perm (nullable, int32 [K], a permutation of 0..K-1): when given, the
+ * output holds the columns in the order q[:, perm[0]], q[:, perm[1]], ...
+ * before the kernel-layout repack (used for act_order / g_idx layers).
+ * Requires K % group_size == 0, group_size % 32 == 0.
+ * Replaces: repack_int4_for_kernel(packed, group_size)  pare/core/pack.py:88-132 */
+PMI_API int pmi_repack_int4_for_kernel(const uint8_t* packed, uint8_t* out, const int32_t* perm,
+                               int64_t N, int64_t K, int64_t group_size, void* stream);
+
+/* fp32 zero points -> u8. Values must be integers in [0,15]; the number of
+ * elements that are not is added to *bad_count (device int32, nullable).
+ * Replaces: the per-call zeros.float() of _to_2d   pare/kernels/matmul_int4.py:219-228 */
+PMI_API int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count,
+                    int64_t count, void* stream);
+
+/* Y[M,N] = X[M,K] . dequant(W)^T with the dequantisation fused into the
+ * matmul. x: fp16 [M,K] row-major, 16-byte aligned; w: kernel layout;
+ * zeros: PMI_F32 or PMI_U8 [N,G]; perm (nullable, int32 [K]): act_order
+ * gather, X is read as X[:, perm[j]] for weight column j (w must then be
+ * repacked with the same perm); y: fp16 [M,N].
+ * Requires K % group_size == 0, group_size % 32 == 0, K % 32 == 0.
+ * Replaces: matmul_w4a16(x, packed_weight, scales, zeros, group_size)
+ *           pare/kernels/matmul_int4.py:183-243 (kernel :66-176) */
+PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
+                     const void* zeros, int zero_dtype, const int32_t* perm, void* y,
+                     int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                     void* stream);
+
+/* Full dequantised weight W_hat[N,K] in the original column order, cast to
+ * out_dtype (PMI_F16 / PMI_BF16 with round-to-nearest-even, or PMI_F32).
+ * layout PMI_LAYOUT_STORAGE: idx (nullable) is g_idx int32 [K], the group of
+ *   each column (default k / group_size).
+ * layout PMI_LAYOUT_KERNEL: idx (nullable) is the perm given to
+ *   pmi_repack_int4_for_kernel.
+ * Replaces: QuantizedLinear.dequantize().to(dtype)   pare/layers/linear.py:101-118,129
+ *           (unpack_int4 pare/core/pack.py:51-67, dequantize_tensor
+ *            pare/core/functional.py:78-91) */
+PMI_API int pmi_dequant_w4a16(const uint8_t* w, int layout, const float* scales, const void* zeros,
+                      int zero_dtype, const int32_t* idx, void* w_out, int out_dtype,
+                      int64_t N, int64_t K, int64_t group_size, void* stream);
+
+/* RTN INT4 quantisation of W[N,K] (fp32, fp16 or bf16) with per-group
+ * min/max scales: writes packed (storage layout, u8 [N,K/2]), scale and zero
+ * (fp32 [N, K/group_size]). sym=0: asymmetric; sym=1: the reference's
+ * symmetric rule on the unsigned grid. Use group_size = K for per-channel.
+ * Replaces: compute_scale(..., per_group) + quantize_tensor + pack_int4
+ *           pare/core/scale.py:24-137, pare/core/functional.py:46-75,
+ *           pare/core/pack.py:29-48, as called by pare/schemes/rtn.py:46-65 */
+PMI_API int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
+                     int64_t N, int64_t K, int64_t group_size, int sym, void* stream);
+
+/* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
+ * 2 = MFMA GEMM. Host-only; no reference counterpart (the reference has one
+ * Triton kernel). */
+PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PARE_AMD_H */

@@ -1,0 +1,212 @@
+"""CPU oracle for the INT4 W4A16 dequant-matmul path — TEST INFRASTRUCTURE ONLY.
+
+This module restates, on the CPU, the reference's algorithm for the
+``QuantizedLinear.use_kernel=True`` path and its dequantize-on-the-fly oracle.
+It is the checker, never the product: only ``tests/``, ``__graft_entry__.smoke``
+and the ``cpu_baseline`` leg of ``bench.py`` may import it. The shipped path
+(``pare_amd``) never calls into it and has no CPU fallback.
+
+Integer/byte work and the fp32 elementwise formulas are numpy (float32
+arithmetic, IEEE round-to-nearest-even, ``np.rint`` = round-half-to-even like
+``torch.round``). The fp16 matmul of the reference's dequant path is restated
+with torch on the CPU (``F.linear`` on fp16, as the reference runs it), which
+is also the CPU baseline timed by ``bench.py``.
+
+Each function cites the reference file:line it follows (paths relative to the
+reference repository root). Pinning of every function — by the reference's
+own known-answer tests, closed forms, invariants and brute force — lives in
+``tests/test_oracle.py``; no function here is "parity unpinned".
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+QMIN = 0   # INT4 is unsigned: pare/core/dtype.py:15-25,46
+QMAX = 15
+
+
+# ---------------------------------------------------------------------------
+# Packing (pare/core/pack.py)
+# ---------------------------------------------------------------------------
+
+def pack_int4(q: np.ndarray) -> np.ndarray:
+    """Even column -> low nibble, odd column -> high nibble (pack.py:29-48)."""
+    q = np.asarray(q)
+    if q.shape[-1] % 2 != 0:
+        raise ValueError(f"Last dimension must be even for INT4 packing, got {q.shape[-1]}")
+    q = q.astype(np.int32)
+    low = q[..., 0::2] & 0xF
+    high = (q[..., 1::2] & 0xF) << 4
+    return (low | high).astype(np.uint8)
+
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    """Inverse of pack_int4, int32 values in [0,15] (pack.py:51-67)."""
+    p = np.asarray(packed).astype(np.int32)
+    out = np.stack([p & 0xF, (p >> 4) & 0xF], axis=-1)
+    return out.reshape(*p.shape[:-1], -1)
+
+
+def repack_int4_for_kernel(packed: np.ndarray, group_size: int = 128) -> np.ndarray:
+    """Storage layout -> kernel layout (pack.py:88-132).
+
+    Inside each group_size-wide tile starting at column k0, byte j holds
+    q[k0 + j] (low nibble) and q[k0 + j + group_size/2] (high nibble).
+    """
+    N, K_half = packed.shape
+    K = 2 * K_half
+    assert K % group_size == 0, f"K={K} must be divisible by group_size={group_size}"
+    half = group_size // 2
+    q = unpack_int4(packed).reshape(N, K // group_size, group_size)
+    lo = q[:, :, :half]
+    hi = q[:, :, half:]
+    return (lo | (hi << 4)).astype(np.uint8).reshape(N, K_half)
+
+
+def permute_columns_packed(packed: np.ndarray, perm: np.ndarray) -> np.ndarray:
+    """Storage-layout weights with columns reordered as q[:, perm] (act_order
+    extension; the reference has no g_idx, see pare/schemes/gptq.py:196-201)."""
+    return pack_int4(unpack_int4(packed)[:, np.asarray(perm)])
+
+
+# ---------------------------------------------------------------------------
+# Scale / zero and quantize / dequantize (pare/core/scale.py, functional.py)
+# ---------------------------------------------------------------------------
+
+def _minmax_to_scale_zero(x_min, x_max, sym: bool):
+    """scale.py:65-91 with qmin=0, qmax=15, all in float32."""
+    f32 = np.float32
+    if sym:
+        abs_max = np.maximum(np.abs(x_min), np.abs(x_max))
+        abs_max = np.maximum(abs_max, f32(1e-8))
+        half = f32(max(abs(QMIN), abs(QMAX)))
+        scale = (abs_max / half).astype(f32)
+        zero = np.zeros_like(scale)
+    else:
+        x_min = np.minimum(x_min, f32(0.0))
+        x_max = np.maximum(x_max, f32(0.0))
+        scale = ((x_max - x_min) / f32(QMAX - QMIN)).astype(f32)
+        scale = np.maximum(scale, f32(1e-8))
+        zero = np.rint(-x_min / scale + f32(QMIN)).astype(f32)
+        zero = np.clip(zero, f32(QMIN), f32(QMAX))
+    return scale.astype(f32), zero.astype(f32)
+
+
+def compute_scale(w: np.ndarray, granularity: str = "per_group", group_size: int = 128,
+                  sym: bool = False):
+    """compute_scale for INT4 (scale.py:24-137). Shapes: per_group [N,G,1],
+    per_channel [N,1], per_tensor scalar."""
+    w = np.asarray(w, dtype=np.float32)
+    if granularity == "per_group":
+        if w.ndim != 2:
+            raise ValueError(f"per_group expects a 2-D weight matrix, got shape {w.shape}")
+        N, K = w.shape
+        if K % group_size != 0:
+            raise ValueError(f"in_features={K} is not divisible by group_size={group_size}")
+        g = w.reshape(N, K // group_size, group_size)
+        return _minmax_to_scale_zero(g.min(-1, keepdims=True), g.max(-1, keepdims=True), sym)
+    if granularity == "per_channel":
+        red = tuple(range(1, w.ndim))
+        return _minmax_to_scale_zero(w.min(red, keepdims=True), w.max(red, keepdims=True), sym)
+    if granularity == "per_tensor":
+        s, z = _minmax_to_scale_zero(w.min().reshape(1), w.max().reshape(1), sym)
+        return s.reshape(()), z.reshape(())
+    raise ValueError(f"Unknown granularity: {granularity!r}")
+
+
+def _align(x: np.ndarray, scale: np.ndarray):
+    """_align_shapes (functional.py:193-214): per_group reshapes x to [N,G,gs]."""
+    if scale.ndim == 3:
+        out, n_groups, _ = scale.shape
+        return x.reshape(out, n_groups, x.shape[-1] // n_groups)
+    return x
+
+
+def quantize_tensor(w: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+    """q = clamp(round(x / scale + zero), 0, 15) in float32 (functional.py:46-75)."""
+    x = _align(np.asarray(w, dtype=np.float32), scale)
+    q = np.clip(np.rint(x / scale + zero), QMIN, QMAX)
+    return q.astype(np.int32)
+
+
+def dequantize_tensor(q: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+    """(q.float() - zero) * scale in float32 (functional.py:78-91)."""
+    x = _align(np.asarray(q).astype(np.float32), scale)
+    return ((x - zero) * scale).astype(np.float32)
+
+
+def dequantize_packed(packed: np.ndarray, scale: np.ndarray, zero: np.ndarray) -> np.ndarray:
+    """QuantizedLinear.dequantize for INT4 (linear.py:101-118): fp32 [N, K]."""
+    N = packed.shape[0]
+    return dequantize_tensor(unpack_int4(packed), scale, zero).reshape(N, -1)
+
+
+def dequantize_gidx(q: np.ndarray, scale: np.ndarray, zero: np.ndarray,
+                    g_idx: np.ndarray) -> np.ndarray:
+    """act_order extension: w[n,k] = (q[n,k] - zero[n, g_idx[k]]) * scale[n, g_idx[k]].
+    With g_idx = k // group_size it is dequantize_tensor (functional.py:78-91)."""
+    s = scale.reshape(scale.shape[0], -1)[:, np.asarray(g_idx)]
+    z = zero.reshape(zero.shape[0], -1)[:, np.asarray(g_idx)]
+    return ((np.asarray(q).astype(np.float32) - z) * s).astype(np.float32)
+
+
+def rtn_quantize(w: np.ndarray, group_size: int = 128, sym: bool = False,
+                 granularity: str = "per_group"):
+    """RTN producer (pare/schemes/rtn.py:46-65 + QuantizedLinear.__init__
+    linear.py:74-89): returns (packed u8 [N,K/2], scale f32, zero f32)."""
+    w = np.asarray(w, dtype=np.float32)
+    scale, zero = compute_scale(w, granularity, group_size, sym)
+    q = quantize_tensor(w, scale, zero).reshape(w.shape)
+    return pack_int4(q), scale, zero
+
+
+def gidx_from_perm(perm: np.ndarray, group_size: int) -> np.ndarray:
+    """g_idx of a layer quantised in permuted column order P with contiguous
+    groups: column P[j] belongs to group j // group_size."""
+    perm = np.asarray(perm)
+    g = np.empty(perm.shape[0], dtype=np.int32)
+    g[perm] = np.arange(perm.shape[0], dtype=np.int32) // group_size
+    return g
+
+
+def rtn_quantize_act_order(w: np.ndarray, perm: np.ndarray, group_size: int = 128):
+    """Quantise W[:, P] with contiguous groups, return q in the original column
+    order plus g_idx (the layout of BASELINE config 4): (packed, scale, zero, g_idx)."""
+    w = np.asarray(w, dtype=np.float32)
+    perm = np.asarray(perm)
+    wp = w[:, perm]
+    scale, zero = compute_scale(wp, "per_group", group_size, False)
+    qp = quantize_tensor(wp, scale, zero).reshape(w.shape)
+    q = np.empty_like(qp)
+    q[:, perm] = qp
+    return pack_int4(q), scale, zero, gidx_from_perm(perm, group_size)
+
+
+# ---------------------------------------------------------------------------
+# Layer outputs
+# ---------------------------------------------------------------------------
+
+def linear_fp32(x: np.ndarray, w_hat: np.ndarray) -> np.ndarray:
+    """fp32-accumulated reference output x @ W^T, with the weights first
+    rounded to fp16 as the reference path does (linear.py:129)."""
+    w16 = np.asarray(w_hat, dtype=np.float32).astype(np.float16).astype(np.float32)
+    return np.asarray(x, dtype=np.float32) @ w16.T
+
+
+def dequant_path_forward_torch(x, packed, scale, zero, bias=None):
+    """The reference's dequantize-on-the-fly forward on the CPU, op for op
+    (linear.py:112-118,129,138 with pack.py:60-67 and functional.py:90-91):
+    unpack -> float -> (q - z) * s -> .to(x.dtype) -> F.linear.
+
+    Arguments are torch CPU tensors; used as the CPU baseline of bench.py."""
+    import torch
+    import torch.nn.functional as F
+
+    p = packed.to(torch.int32)
+    q = torch.stack([p & 0xF, (p >> 4) & 0xF], dim=-1).reshape(packed.shape[0], -1)
+    qf = q.float()
+    if scale.dim() == 3:
+        qf = qf.reshape(scale.shape[0], scale.shape[1], -1)
+    w = ((qf - zero) * scale).reshape(packed.shape[0], -1)
+    return F.linear(x, w.to(x.dtype), bias)

@@ -1,0 +1,21 @@
+"""pare_amd — MI355X (gfx950) INT4 W4A16 dequant-matmul, a drop-in for the
+``QuantizedLinear.use_kernel=True`` path of Pare.
+
+Operator API (mirrors pare.kernels.matmul_int4 and pare.core.pack):
+  matmul_w4a16, repack_int4_for_kernel, kernel_available / triton_available
+Module: QuantizedLinear (mirrors pare.layers.linear.QuantizedLinear)
+Producer: rtn_quantize (mirrors pare.schemes.rtn on the device)
+All compute runs in libpare_amd.so (hand-written HIP); there is no CPU fallback.
+"""
+
+from .config import QuantConfig, QuantDtype
+from .kernels import kernel_available, kernel_choice, matmul_w4a16, triton_available
+from .linear import QuantizedLinear
+from .pack import dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, zeros_to_u8
+from .quant import rtn_quantize
+
+__all__ = [
+    "QuantConfig", "QuantDtype", "QuantizedLinear", "dequantize_int4", "kernel_available",
+    "kernel_choice", "matmul_w4a16", "perm_from_g_idx", "repack_int4_for_kernel",
+    "rtn_quantize", "triton_available", "zeros_to_u8",
+]

@@ -1,0 +1,95 @@
+"""ctypes binding of libpare_amd.so (declarations: include/pare_amd.h).
+
+The library is loaded lazily from this package directory. A missing library is
+an error, never a silent fallback: every operator of the package raises when
+it cannot run on the HIP device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
+
+PMI_OK = 0
+PMI_ERR_INVALID = -1
+PMI_ERR_UNSUPPORTED = -2
+PMI_ERR_HIP = -3
+PMI_ERR_NO_DEVICE = -4
+
+PMI_F16, PMI_BF16, PMI_F32, PMI_U8 = 0, 1, 2, 3
+PMI_LAYOUT_STORAGE, PMI_LAYOUT_KERNEL = 0, 1
+
+_ERR_NAMES = {
+    PMI_ERR_INVALID: "PMI_ERR_INVALID",
+    PMI_ERR_UNSUPPORTED: "PMI_ERR_UNSUPPORTED",
+    PMI_ERR_HIP: "PMI_ERR_HIP",
+    PMI_ERR_NO_DEVICE: "PMI_ERR_NO_DEVICE",
+}
+
+_vp, _i, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+
+# name -> (restype, argtypes); must match include/pare_amd.h
+SIGNATURES = {
+    "pmi_abi_version": (_i, []),
+    "pmi_last_error": (ctypes.c_char_p, []),
+    "pmi_device_supported": (_i, [_i]),
+    "pmi_repack_int4_for_kernel": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "pmi_zeros_to_u8": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64, _vp]),
+    "pmi_dequant_w4a16": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _vp]),
+    "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),
+    "pmi_matmul_kernel_choice": (_i, [_i64, _i64, _i64, _i64]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class PmiError(RuntimeError):
+    """A libpare_amd entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, message: str):
+        self.code = code
+        super().__init__(f"{fn} failed ({_ERR_NAMES.get(code, code)}): {message}")
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            # torch first: its bundled HIP runtime carries the soname
+            # libamdhip64.so.7, so the library binds to that same runtime
+            # (torch's stream handles are then valid inside it).
+            import torch  # noqa: F401
+
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run `python -m pare_amd.build` "
+                    "(pare_amd has no CPU fallback)")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().pmi_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, fn: str) -> None:
+    if rc != PMI_OK:
+        raise PmiError(fn, rc, last_error())
+
+
+def call(fn: str, *args) -> None:
+    """Calls entry point `fn` and raises PmiError on a non-zero status."""
+    check(getattr(lib(), fn)(*args), fn)

@@ -1,0 +1,187 @@
+// C ABI of libpare_amd.so: host-side argument validation, error reporting and
+// kernel dispatch. Declarations and reference citations: include/pare_amd.h.
+#include "../../include/pare_amd.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "pmi_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return PMI_OK;
+}
+
+int from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(PMI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Shared shape rules of the packed INT4 format and the kernels' tiling.
+int check_shape(int64_t N, int64_t K, int64_t gs, const char* fn) {
+  if (N < 0 || K <= 0 || gs <= 0)
+    return fail(PMI_ERR_INVALID, "%s: need N >= 0, K > 0, group_size > 0 (N=%lld K=%lld gs=%lld)",
+                fn, (long long)N, (long long)K, (long long)gs);
+  if (K % gs != 0)
+    return fail(PMI_ERR_INVALID, "%s: K=%lld must be divisible by group_size=%lld", fn,
+                (long long)K, (long long)gs);
+  if (gs % 32 != 0)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: group_size=%lld must be a multiple of 32", fn,
+                (long long)gs);
+  if (K > (1ll << 30) || N > (1ll << 31) - 1)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: shape too large (N=%lld K=%lld)", fn, (long long)N,
+                (long long)K);
+  return PMI_OK;
+}
+
+int check_zero_dtype(int zero_dtype, const char* fn) {
+  if (zero_dtype != PMI_F32 && zero_dtype != PMI_U8)
+    return fail(PMI_ERR_INVALID, "%s: zero dtype must be PMI_F32 or PMI_U8 (got %d)", fn,
+                zero_dtype);
+  return PMI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pmi_abi_version(void) { return PMI_ABI_VERSION; }
+
+const char* pmi_last_error(void) { return g_err; }
+
+int pmi_device_supported(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return fail(PMI_ERR_NO_DEVICE, "pmi_device_supported: no HIP device");
+  if (device < 0 || device >= n) {
+    fail(PMI_OK, "pmi_device_supported: device %d out of range (count %d)", device, n);
+    return 0;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+    return fail(PMI_ERR_HIP, "pmi_device_supported: hipGetDeviceProperties failed");
+  ok();
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int pmi_repack_int4_for_kernel(const uint8_t* packed, uint8_t* out, const int32_t* perm,
+                               int64_t N, int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_repack_int4_for_kernel";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (N == 0) return ok();
+  if (!packed || !out) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (packed == out) return fail(PMI_ERR_INVALID, "%s: in-place repack is not supported", fn);
+  if (!aligned(out, 4)) return fail(PMI_ERR_INVALID, "%s: out must be 4-byte aligned", fn);
+  return from_hip(pmi::launch_repack(packed, out, perm, N, K, group_size, (hipStream_t)stream), fn);
+}
+
+int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count, int64_t count,
+                    void* stream) {
+  const char* fn = "pmi_zeros_to_u8";
+  if (count < 0) return fail(PMI_ERR_INVALID, "%s: count < 0", fn);
+  if (count == 0) return ok();
+  if (!zeros || !zeros_u8) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  return from_hip(pmi::launch_zeros_to_u8(zeros, zeros_u8, bad_count, count, (hipStream_t)stream),
+                  fn);
+}
+
+int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size) {
+  (void)N;
+  (void)K;
+  if (M <= 4) return 1;
+  return group_size % 128 == 0 ? 2 : 1;
+}
+
+int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
+                     const void* zeros, int zero_dtype, const int32_t* perm, void* y,
+                     int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                     void* stream) {
+  const char* fn = "pmi_matmul_w4a16";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (int rc = check_zero_dtype(zero_dtype, fn)) return rc;
+  if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
+  if (x_dtype != PMI_F16 || y_dtype != PMI_F16)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: x and y must be fp16 (got x=%d y=%d)", fn, x_dtype,
+                y_dtype);
+  if (M > (1ll << 31) - 1) return fail(PMI_ERR_UNSUPPORTED, "%s: M too large", fn);
+  if (M == 0 || N == 0) return ok();
+  if (!x || !w || !scales || !zeros || !y) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(x, 16)) return fail(PMI_ERR_INVALID, "%s: x must be 16-byte aligned", fn);
+  if (!aligned(w, 16)) return fail(PMI_ERR_INVALID, "%s: packed weight must be 16-byte aligned", fn);
+  if (!aligned(scales, 4)) return fail(PMI_ERR_INVALID, "%s: scales must be 4-byte aligned", fn);
+  if (zero_dtype == PMI_F32 && !aligned(zeros, 4))
+    return fail(PMI_ERR_INVALID, "%s: fp32 zeros must be 4-byte aligned", fn);
+  if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
+  if (perm && !aligned(perm, 4)) return fail(PMI_ERR_INVALID, "%s: perm must be 4-byte aligned", fn);
+
+  hipStream_t s = (hipStream_t)stream;
+  const int zu8 = zero_dtype == PMI_U8;
+  if (pmi_matmul_kernel_choice(M, N, K, group_size) == 2)
+    return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s), fn);
+  // GEMV, four activation rows per launch.
+  const uint16_t* xp = (const uint16_t*)x;
+  uint16_t* yp = (uint16_t*)y;
+  for (int64_t m = 0; m < M; m += 4) {
+    const int64_t mt = M - m < 4 ? M - m : 4;
+    hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, perm, yp + m * N, mt, N, K,
+                                    group_size, s);
+    if (e != hipSuccess) return from_hip(e, fn);
+  }
+  return ok();
+}
+
+int pmi_dequant_w4a16(const uint8_t* w, int layout, const float* scales, const void* zeros,
+                      int zero_dtype, const int32_t* idx, void* w_out, int out_dtype, int64_t N,
+                      int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_dequant_w4a16";
+  if (N < 0 || K <= 0 || group_size <= 0 || K % group_size != 0 || K % 2 != 0)
+    return fail(PMI_ERR_INVALID, "%s: need K even and divisible by group_size (N=%lld K=%lld gs=%lld)",
+                fn, (long long)N, (long long)K, (long long)group_size);
+  if (layout != PMI_LAYOUT_STORAGE && layout != PMI_LAYOUT_KERNEL)
+    return fail(PMI_ERR_INVALID, "%s: unknown layout %d", fn, layout);
+  if (layout == PMI_LAYOUT_KERNEL && group_size % 2 != 0)
+    return fail(PMI_ERR_INVALID, "%s: kernel layout needs an even group_size", fn);
+  if (int rc = check_zero_dtype(zero_dtype, fn)) return rc;
+  if (out_dtype != PMI_F16 && out_dtype != PMI_BF16 && out_dtype != PMI_F32)
+    return fail(PMI_ERR_INVALID, "%s: out dtype must be PMI_F16, PMI_BF16 or PMI_F32", fn);
+  if (N == 0) return ok();
+  if (!w || !scales || !zeros || !w_out) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  return from_hip(pmi::launch_dequant(w, layout, scales, zeros, zero_dtype == PMI_U8, idx, w_out,
+                                      out_dtype, N, K, group_size, (hipStream_t)stream),
+                  fn);
+}
+
+int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
+                     int64_t N, int64_t K, int64_t group_size, int sym, void* stream) {
+  const char* fn = "pmi_rtn_quantize";
+  if (N < 0 || K <= 0 || group_size <= 0 || K % group_size != 0)
+    return fail(PMI_ERR_INVALID, "%s: in_features=%lld is not divisible by group_size=%lld", fn,
+                (long long)K, (long long)group_size);
+  if (group_size % 2 != 0 || K % 2 != 0)
+    return fail(PMI_ERR_INVALID, "%s: INT4 packing needs an even group_size and K", fn);
+  if (w_dtype != PMI_F32 && w_dtype != PMI_F16 && w_dtype != PMI_BF16)
+    return fail(PMI_ERR_INVALID, "%s: weight dtype must be PMI_F32, PMI_F16 or PMI_BF16", fn);
+  if (sym != 0 && sym != 1) return fail(PMI_ERR_INVALID, "%s: sym must be 0 or 1", fn);
+  if (N == 0) return ok();
+  if (!w || !packed || !scale || !zero) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  return from_hip(pmi::launch_rtn(w, w_dtype, packed, scale, zero, N, K, group_size, sym,
+                                  (hipStream_t)stream),
+                  fn);
+}
+
+}  // extern "C"

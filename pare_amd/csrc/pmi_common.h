@@ -1,0 +1,62 @@
+// Shared device helpers for the gfx950 INT4 W4A16 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define PMI_DEV __device__ __forceinline__
+
+// fp16 bit pattern 0x6400 is 1024.0; OR-ing a nibble q into its mantissa gives
+// exactly 1024 + q. Two such halves per 32-bit word.
+#define PMI_MAGIC_X2 0x64006400u
+#define PMI_NIB_X2 0x000F000Fu
+
+PMI_DEV f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+PMI_DEV uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Packed -(1024 + z) in both halves, for an integer zero point z in [0, 15]:
+// 1024 + z has bit pattern 0x6400 | z, and the sign bit makes it 0xE400 | z.
+PMI_DEV uint32_t neg_magic_zero_x2(uint32_t z) { return (0xE400u | z) * 0x00010001u; }
+
+// Four half2 values (q - z) from one 32-bit word w of packed nibbles.
+// With bytes b0..b3 of w (byte i = lo_i | hi_i << 4) the results are
+//   d0 = (lo0, lo2), d1 = (lo1, lo3), d2 = (hi0, hi2), d3 = (hi1, hi3).
+// Every value is an integer in [-15, 15], so the fp16 subtraction is exact.
+PMI_DEV void unpack_word_minus_zero(uint32_t w, uint32_t nz, f16x2& d0, f16x2& d1,
+                                    f16x2& d2, f16x2& d3) {
+  const f16x2 z2 = as_f16x2(nz);
+  d0 = as_f16x2((w & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
+  d1 = as_f16x2(((w >> 8) & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
+  d2 = as_f16x2(((w >> 4) & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
+  d3 = as_f16x2(((w >> 12) & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
+}
+
+// (a.lo16, b.lo16) and (a.hi16, b.hi16) of two words holding consecutive
+// fp16 pairs: turns x[4i..4i+3] into the pairs (x0,x2) and (x1,x3) that
+// line up with d0/d1 (or d2/d3) above.
+PMI_DEV uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+PMI_DEV uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+PMI_DEV float dot2_acc(f16x2 a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(a, as_f16x2(b), c, false);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+PMI_DEV uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Loads a zero point for (row n, group g) as an integer 0..15.
+PMI_DEV uint32_t load_zero(const void* zeros, int zero_u8, int64_t idx) {
+  if (zero_u8) return (uint32_t)((const uint8_t*)zeros)[idx];
+  return (uint32_t)(int)((const float*)zeros)[idx];
+}

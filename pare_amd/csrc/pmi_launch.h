@@ -1,0 +1,49 @@
+// Host-side launchers shared between the kernel sources and the C ABI layer.
+// Every launcher assumes its arguments were validated by capi.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pmi {
+
+struct GemvConfig {
+  int rows_per_wave;  // R: weight rows one wave walks with one x slice in registers
+  int slice_waves;    // waves that split one row's K range (1 slice = 2048 columns)
+  int row_waves;      // waves that take different row blocks of the same slices
+  int n_slices;       // ceil(K / 2048)
+  int grid;           // workgroups
+};
+
+struct GemmConfig {
+  int m_tiles;  // 16-row MFMA tiles per workgroup (1, 2 or 4)
+  int n_tiles;  // 16-row weight tiles per wave (1 or 2)
+  int grid_n;
+  int grid_m;
+};
+
+GemvConfig gemv_config(int64_t M, int64_t N, int64_t K);
+GemmConfig gemm_config(int64_t M, int64_t N, int64_t K);
+
+hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
+                       int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
+                       int64_t K, int64_t gs, hipStream_t stream);
+
+hipError_t launch_gemm(const void* x, const uint8_t* w, const float* scales, const void* zeros,
+                       int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
+                       int64_t K, int64_t gs, hipStream_t stream);
+
+hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,
+                         int64_t K, int64_t gs, hipStream_t stream);
+
+hipError_t launch_zeros_to_u8(const float* zeros, uint8_t* out, int32_t* bad, int64_t count,
+                              hipStream_t stream);
+
+hipError_t launch_dequant(const uint8_t* w, int layout, const float* scales, const void* zeros,
+                          int zero_u8, const int32_t* idx, void* out, int out_dtype, int64_t N,
+                          int64_t K, int64_t gs, hipStream_t stream);
+
+hipError_t launch_rtn(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
+                      int64_t N, int64_t K, int64_t gs, int sym, hipStream_t stream);
+
+}  // namespace pmi

@@ -1,0 +1,256 @@
+// Layout and producer kernels around the INT4 matmul:
+//   repack   storage layout -> kernel layout (+ optional act_order permutation)
+//   zeros    fp32 zero points -> u8, counting values that are not integers in [0,15]
+//   dequant  packed INT4 -> fp16 / bf16 / fp32 weights (bit-exact with the reference)
+//   rtn      fp weights -> (packed, scale, zero) with per-group min/max RTN
+// All are integer/byte or elementwise work bound by HBM bandwidth; none uses LDS.
+#include "../../include/pare_amd.h"
+#include "pmi_common.h"
+#include "pmi_launch.h"
+
+namespace pmi {
+namespace {
+
+constexpr int kBlock = 256;
+
+PMI_DEV uint32_t nibble_at(const uint8_t* __restrict__ row, int64_t col) {
+  return (row[col >> 1] >> ((col & 1) * 4)) & 0xFu;
+}
+
+PMI_DEV int64_t safe_col(const int32_t* __restrict__ perm, int64_t k, int64_t K) {
+  if (!perm) return k;
+  const int32_t p = perm[k];
+  return (p >= 0 && p < K) ? (int64_t)p : k;
+}
+
+// Output byte j of a row holds, inside its group tile t (hgs = gs/2 bytes),
+// column t*gs + (j - t*hgs) in bits 0-3 and that column + hgs in bits 4-7
+// (pare/core/pack.py:123-130). One thread writes 4 consecutive output bytes.
+__global__ void repack_kernel(const uint8_t* __restrict__ packed, uint8_t* __restrict__ out,
+                              const int32_t* __restrict__ perm, int64_t N, int64_t K, int64_t gs) {
+  const int64_t row_bytes = K >> 1;
+  const int64_t words_per_row = row_bytes >> 2;
+  const int64_t hgs = gs >> 1;
+  const int64_t total = N * words_per_row;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = idx / words_per_row;
+    const int64_t jw = (idx - n * words_per_row) << 2;
+    const uint8_t* src = packed + n * row_bytes;
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int64_t j = jw + b;
+      const int64_t t = j / hgs;
+      const int64_t k_lo = t * gs + (j - t * hgs);
+      const uint32_t lo = nibble_at(src, safe_col(perm, k_lo, K));
+      const uint32_t hi = nibble_at(src, safe_col(perm, k_lo + hgs, K));
+      word |= (lo | (hi << 4)) << (8 * b);
+    }
+    *reinterpret_cast<uint32_t*>(out + n * row_bytes + jw) = word;
+  }
+}
+
+__global__ void zeros_to_u8_kernel(const float* __restrict__ zeros, uint8_t* __restrict__ out,
+                                   int32_t* __restrict__ bad, int64_t count) {
+  int local_bad = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float z = zeros[i];
+    const bool ok = z >= 0.f && z <= 15.f && z == rintf(z);  // false for NaN
+    local_bad += ok ? 0 : 1;
+    out[i] = ok ? (uint8_t)(int)z : (uint8_t)0;
+  }
+  if (bad && local_bad) atomicAdd(bad, local_bad);
+}
+
+// w_hat = (float(q) - zero) * scale in fp32, then one rounding to out dtype
+// (pare/core/functional.py:90-91, pare/layers/linear.py:129).
+template <int OUT>
+__global__ void dequant_kernel(const uint8_t* __restrict__ w, int layout,
+                               const float* __restrict__ scales, const void* __restrict__ zeros,
+                               int zero_u8, const int32_t* __restrict__ idx,
+                               void* __restrict__ out, int64_t N, int64_t K, int64_t gs) {
+  const int64_t row_bytes = K >> 1;
+  const int64_t hgs = gs >> 1;
+  const int64_t G = K / gs;
+  const int64_t total = N * K;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = e / K;
+    const int64_t j = e - n * K;
+    const uint8_t* row = w + n * row_bytes;
+    uint32_t q;
+    int64_t g, col;
+    if (layout == PMI_LAYOUT_KERNEL) {
+      const int64_t t = j / gs;
+      const int64_t r = j - t * gs;
+      const int64_t byte = t * hgs + (r < hgs ? r : r - hgs);
+      q = (row[byte] >> (r < hgs ? 0 : 4)) & 0xFu;
+      g = t;
+      col = safe_col(idx, j, K);
+    } else {
+      q = nibble_at(row, j);
+      g = idx ? (int64_t)idx[j] : j / gs;
+      col = j;
+    }
+    float v;
+    if (g < 0 || g >= G) {
+      v = __builtin_nanf("");
+    } else {
+      const int64_t sz = n * G + g;
+      const float z = zero_u8 ? (float)((const uint8_t*)zeros)[sz] : ((const float*)zeros)[sz];
+      v = ((float)q - z) * scales[sz];
+    }
+    const int64_t o = n * K + col;
+    if constexpr (OUT == PMI_F32) {
+      ((float*)out)[o] = v;
+    } else if constexpr (OUT == PMI_F16) {
+      ((f16*)out)[o] = (f16)v;
+    } else {
+      ((uint16_t*)out)[o] = f32_to_bf16_rne(v);
+    }
+  }
+}
+
+template <int IN>
+PMI_DEV float load_as_f32(const void* p, int64_t i) {
+  if constexpr (IN == PMI_F32) {
+    return ((const float*)p)[i];
+  } else if constexpr (IN == PMI_F16) {
+    return (float)((const f16*)p)[i];
+  } else {
+    return __builtin_bit_cast(float, (uint32_t)((const uint16_t*)p)[i] << 16);
+  }
+}
+
+PMI_DEV float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+PMI_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// One wave per (row, group): min/max -> (scale, zero) -> q -> packed bytes.
+// Formulas of pare/core/scale.py:73-91 and pare/core/functional.py:68-75 with
+// qmin = 0, qmax = 15 (unsigned INT4); rintf is round-half-to-even like
+// torch.round.
+template <int IN>
+__global__ void rtn_kernel(const void* __restrict__ w, uint8_t* __restrict__ packed,
+                           float* __restrict__ scale_out, float* __restrict__ zero_out, int64_t N,
+                           int64_t K, int64_t gs, int sym) {
+  const int lane = threadIdx.x & 63;
+  const int64_t G = K / gs;
+  const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (unit >= N * G) return;
+  const int64_t n = unit / G;
+  const int64_t g = unit - n * G;
+  const int64_t base = n * K + g * gs;
+  const int64_t pairs = gs >> 1;
+
+  float mn = __builtin_inff(), mx = -__builtin_inff();
+  for (int64_t p = lane; p < pairs; p += 64) {
+    const float a = load_as_f32<IN>(w, base + 2 * p);
+    const float b = load_as_f32<IN>(w, base + 2 * p + 1);
+    mn = fminf(mn, fminf(a, b));
+    mx = fmaxf(mx, fmaxf(a, b));
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+
+  float scale, zero;
+  if (sym) {
+    const float amax = fmaxf(fmaxf(fabsf(mn), fabsf(mx)), 1e-8f);
+    scale = amax / 15.0f;
+    zero = 0.0f;
+  } else {
+    mn = fminf(mn, 0.0f);
+    mx = fmaxf(mx, 0.0f);
+    scale = (mx - mn) / 15.0f;
+    scale = fmaxf(scale, 1e-8f);
+    zero = rintf(-mn / scale + 0.0f);
+    zero = fminf(fmaxf(zero, 0.0f), 15.0f);
+  }
+  if (lane == 0) {
+    scale_out[unit] = scale;
+    zero_out[unit] = zero;
+  }
+  for (int64_t p = lane; p < pairs; p += 64) {
+    const float a = load_as_f32<IN>(w, base + 2 * p);
+    const float b = load_as_f32<IN>(w, base + 2 * p + 1);
+    const float qa = fminf(fmaxf(rintf(a / scale + zero), 0.0f), 15.0f);
+    const float qb = fminf(fmaxf(rintf(b / scale + zero), 0.0f), 15.0f);
+    packed[(base >> 1) + p] = (uint8_t)((int)qa | ((int)qb << 4));
+  }
+}
+
+int grid_for(int64_t work, int per_thread = 1) {
+  int64_t blocks = (work / per_thread + kBlock - 1) / kBlock;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  return (int)blocks;
+}
+
+}  // namespace
+
+hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,
+                         int64_t K, int64_t gs, hipStream_t stream) {
+  hipLaunchKernelGGL(repack_kernel, dim3(grid_for(N * (K / 8))), dim3(kBlock), 0, stream, packed,
+                     out, perm, N, K, gs);
+  return hipGetLastError();
+}
+
+hipError_t launch_zeros_to_u8(const float* zeros, uint8_t* out, int32_t* bad, int64_t count,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL(zeros_to_u8_kernel, dim3(grid_for(count)), dim3(kBlock), 0, stream, zeros,
+                     out, bad, count);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(const uint8_t* w, int layout, const float* scales, const void* zeros,
+                          int zero_u8, const int32_t* idx, void* out, int out_dtype, int64_t N,
+                          int64_t K, int64_t gs, hipStream_t stream) {
+  const dim3 grid(grid_for(N * K)), block(kBlock);
+  switch (out_dtype) {
+    case PMI_F16:
+      hipLaunchKernelGGL(dequant_kernel<PMI_F16>, grid, block, 0, stream, w, layout, scales, zeros,
+                         zero_u8, idx, out, N, K, gs);
+      break;
+    case PMI_BF16:
+      hipLaunchKernelGGL(dequant_kernel<PMI_BF16>, grid, block, 0, stream, w, layout, scales,
+                         zeros, zero_u8, idx, out, N, K, gs);
+      break;
+    default:
+      hipLaunchKernelGGL(dequant_kernel<PMI_F32>, grid, block, 0, stream, w, layout, scales, zeros,
+                         zero_u8, idx, out, N, K, gs);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rtn(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
+                      int64_t N, int64_t K, int64_t gs, int sym, hipStream_t stream) {
+  const int64_t units = N * (K / gs);
+  const int waves_per_block = 4;
+  const dim3 grid((unsigned)((units + waves_per_block - 1) / waves_per_block));
+  const dim3 block(64 * waves_per_block);
+  switch (w_dtype) {
+    case PMI_F32:
+      hipLaunchKernelGGL(rtn_kernel<PMI_F32>, grid, block, 0, stream, w, packed, scale, zero, N, K,
+                         gs, sym);
+      break;
+    case PMI_F16:
+      hipLaunchKernelGGL(rtn_kernel<PMI_F16>, grid, block, 0, stream, w, packed, scale, zero, N, K,
+                         gs, sym);
+      break;
+    default:
+      hipLaunchKernelGGL(rtn_kernel<PMI_BF16>, grid, block, 0, stream, w, packed, scale, zero, N,
+                         K, gs, sym);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pmi

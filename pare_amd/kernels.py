@@ -1,0 +1,160 @@
+"""Fused INT4 W4A16 matmul on MI355X — the operator API of the kernel path.
+
+Mirrors pare/kernels/matmul_int4.py:183-248 (``matmul_w4a16``,
+``triton_available``) with the Triton kernel replaced by hand-written HIP
+kernels for gfx950 behind libpare_amd.so:
+  - M <= 4: split-K GEMV (w4a16_gemv.hip), HBM-bandwidth bound;
+  - M > 4 : MFMA GEMM (w4a16_gemm.hip) for group sizes that are multiples of
+    128, otherwise the GEMV four activation rows at a time.
+There is no CPU or PyTorch fallback: every call runs the HIP library or raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _DeviceGuard:
+    """Makes `device` the current HIP device for the duration of a launch."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.device.index is not None and self.device.index != cur:
+            self.prev = cur
+            torch.cuda.set_device(self.device)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def kernel_available() -> bool:
+    """True if libpare_amd.so is built and the current device is a gfx950 GPU
+    (the probe the reference calls ``triton_available``, matmul_int4.py:246-248)."""
+    try:
+        L = _lib.lib()
+    except (RuntimeError, OSError):
+        return False
+    if not torch.cuda.is_available():
+        return False
+    return L.pmi_device_supported(torch.cuda.current_device()) == 1
+
+
+# The reference's tests and callers probe the kernel with this name.
+triton_available = kernel_available
+
+
+def _to_2d(t: torch.Tensor) -> torch.Tensor:
+    """[N] -> [N,1], [N,G,1] -> [N,G] (matmul_int4.py:219-225)."""
+    if t.dim() == 1:
+        return t.unsqueeze(1)
+    if t.dim() == 3:
+        return t.squeeze(2)
+    if t.dim() == 0:
+        return t.reshape(1, 1)
+    return t
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _validated_zero_tensor(zeros: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """Zero points as the kernels read them: u8 as-is, anything else as fp32
+    after a one-time check (cached per tensor version) that every value is an
+    integer in [0, 15], the INT4 contract of pare/core/scale.py:89-90."""
+    if zeros.dtype == torch.uint8:
+        return zeros, _lib.PMI_U8
+    z = zeros.float()
+    stamp = (zeros.data_ptr(), zeros._version)
+    if getattr(zeros, "_pmi_checked", None) != stamp:
+        bad = ((z < 0) | (z > 15) | (z != torch.round(z))).any().item()
+        if bad:
+            raise ValueError("zeros must hold integers in [0, 15] for INT4 (asymmetric RTN/GPTQ/AWQ "
+                             "zero points); got values outside that set")
+        try:
+            zeros._pmi_checked = stamp
+        except (AttributeError, RuntimeError):
+            pass
+    return z, _lib.PMI_F32
+
+
+def matmul_w4a16(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    group_size: int,
+    *,
+    perm: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Y[M,N] = X[M,K] @ dequant(W)^T with the dequantisation fused (fp16 in, fp16 out).
+
+    Same arguments and errors as the reference (matmul_int4.py:183-217):
+      x:             [M, K] float16, contiguous, on a HIP device.
+      packed_weight: [N, K//2] uint8 in *kernel layout* (``repack_int4_for_kernel``).
+      scales:        [N], [N, G] or [N, G, 1], any float dtype (read as fp32).
+      zeros:         same shape as scales; fp32 integer values or uint8.
+      group_size:    quantisation group size; the K-tile of the kernel layout.
+    Extensions: ``perm`` (int32 [K]) for act_order layers whose weights were
+    repacked with the same permutation; ``out`` to write into a preallocated
+    [M, N] fp16 tensor.
+    Raises RuntimeError when x is not on a HIP device or the library is
+    missing; AssertionError on layout violations, like the reference.
+    """
+    L = _lib.lib()
+    if not x.is_cuda:
+        raise RuntimeError("matmul_w4a16 requires HIP (cuda) tensors.")
+    assert x.is_contiguous(), "x must be contiguous"
+    assert x.dtype == torch.float16, f"x must be float16, got {x.dtype}"
+    assert x.dim() == 2, f"x must be 2-D [M, K], got shape {tuple(x.shape)}"
+    M, K = x.shape
+    N, K_half = packed_weight.shape
+    assert K == K_half * 2, f"packed_weight has {K_half} columns, expected K//2={K // 2}"
+    assert packed_weight.dtype == torch.uint8, "packed_weight must be uint8"
+    assert K % group_size == 0, f"K={K} must be divisible by group_size={group_size}"
+    dev = x.device
+    for name, t in (("packed_weight", packed_weight), ("scales", scales), ("zeros", zeros)):
+        if t.device != dev:
+            raise RuntimeError(f"{name} is on {t.device}, x is on {dev}")
+    G = K // group_size
+    s2 = _to_2d(scales).float().contiguous()
+    z2, zdt = _validated_zero_tensor(_to_2d(zeros))
+    z2 = z2.contiguous()
+    assert tuple(s2.shape) == (N, G), f"scales must be [N, G]=[{N}, {G}], got {tuple(scales.shape)}"
+    assert tuple(z2.shape) == (N, G), f"zeros must be [N, G]=[{N}, {G}], got {tuple(zeros.shape)}"
+    w = _aligned16(packed_weight.contiguous())
+    xa = _aligned16(x)
+    if perm is not None:
+        assert perm.dtype == torch.int32 and perm.numel() == K and perm.device == dev, \
+            "perm must be an int32 [K] tensor on x's device"
+        perm = perm.contiguous()
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=torch.float16)
+    else:
+        assert out.dtype == torch.float16 and tuple(out.shape) == (M, N) and out.is_contiguous(), \
+            "out must be a contiguous [M, N] float16 tensor"
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16(
+            xa.data_ptr(), _lib.PMI_F16, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
+            perm.data_ptr() if perm is not None else None, out.data_ptr(), _lib.PMI_F16,
+            M, N, K, group_size, _stream_handle(dev)), "pmi_matmul_w4a16")
+    return out
+
+
+def kernel_choice(M: int, N: int, K: int, group_size: int) -> str:
+    """'gemv' or 'gemm': the kernel matmul_w4a16 runs for this shape."""
+    return "gemm" if _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size) == 2 else "gemv"

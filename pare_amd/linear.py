@@ -1,0 +1,142 @@
+"""QuantizedLinear for the INT4 W4A16 path on MI355X.
+
+Drop-in for pare/layers/linear.py:40-202 on its kernel path: the same buffers
+(``packed_weight`` uint8 [out, in//2] in pack_int4 order, ``scale`` and
+``zero`` fp32 [out, G, 1], optional ``bias``), the same ``use_kernel`` flag,
+``dequantize()`` and ``forward(x)``. Differences, all deliberate:
+  - Everything runs on the HIP device. A CPU input raises RuntimeError instead
+    of silently taking the reference's CPU dequant path (linear.py:121-127).
+  - ``use_kernel`` is read with getattr(..., False), so layers built by
+    ``from_tensors`` work (the reference never sets it there, linear.py:166-202).
+  - The kernel-layout cache is refreshed when the packed weight changes device
+    or contents (the reference caches forever, linear.py:148-151).
+  - Optional ``g_idx`` (int32 [in]) for act_order layers.
+  - ``quantize_inputs`` (SmoothQuant W8A8 fake-quant) is not part of this path.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .config import QuantConfig, is_int4, kernel_group_size
+from .kernels import matmul_w4a16
+from .pack import dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, zeros_to_u8
+
+
+class QuantizedLinear(nn.Module):
+    def __init__(self, packed_weight: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor,
+                 config, bias: torch.Tensor | None, in_features: int, out_features: int,
+                 use_kernel: bool = False, g_idx: torch.Tensor | None = None) -> None:
+        super().__init__()
+        if not is_int4(config):
+            raise ValueError("pare_amd.QuantizedLinear implements the INT4 path only")
+        if packed_weight.dtype != torch.uint8 or tuple(packed_weight.shape) != (out_features, in_features // 2):
+            raise ValueError(f"packed_weight must be uint8 [{out_features}, {in_features // 2}]")
+        self.config = config
+        self.in_features = in_features
+        self.out_features = out_features
+        self.use_kernel = use_kernel
+        self.quantize_inputs = False
+        self.register_buffer("packed_weight", packed_weight)
+        self.register_buffer("q_weight", None)
+        self.register_buffer("scale", scale.float())
+        self.register_buffer("zero", zero.float())
+        self.register_buffer("g_idx", g_idx.to(torch.int32) if g_idx is not None else None)
+        self.bias = nn.Parameter(bias.detach().clone()) if bias is not None else None
+
+    # ------------------------------------------------------------------
+    # Constructors
+    # ------------------------------------------------------------------
+
+    @classmethod
+    def from_tensors(cls, packed_weight, q_weight, scale, zero, config, bias, in_features,
+                     out_features, quantize_inputs: bool = False, g_idx=None) -> "QuantizedLinear":
+        """Same signature as pare/layers/linear.py:166-177 (used by load paths)."""
+        if quantize_inputs:
+            raise NotImplementedError("quantize_inputs (SmoothQuant W8A8) is not part of the INT4 path")
+        if packed_weight is None:
+            raise ValueError("the INT4 path needs packed_weight (q_weight is for 8-bit layers)")
+        return cls(packed_weight, scale, zero, config, bias, in_features, out_features,
+                   g_idx=g_idx)
+
+    @classmethod
+    def from_reference(cls, ref: nn.Module, use_kernel: bool = True) -> "QuantizedLinear":
+        """Takes over the buffers of a reference pare QuantizedLinear (INT4)."""
+        return cls(ref.packed_weight, ref.scale, ref.zero, ref.config, ref.bias,
+                   ref.in_features, ref.out_features, use_kernel=use_kernel,
+                   g_idx=getattr(ref, "g_idx", None))
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, config=None) -> "QuantizedLinear":
+        """RTN-quantise an nn.Linear (pare/layers/linear.py:205-268, INT4 branch)
+        with the HIP producer. A CPU layer is quantised on the current HIP device
+        and the buffers are returned on the layer's device."""
+        from .quant import rtn_quantize
+
+        config = config or QuantConfig(bits=4, scheme="rtn")
+        if not is_int4(config):
+            raise ValueError("pare_amd.QuantizedLinear implements the INT4 path only")
+        w = linear.weight.detach()
+        home = w.device
+        if not w.is_cuda:
+            w = w.to("cuda")
+        packed, scale, zero = rtn_quantize(w.float(), config.group_size, config.sym,
+                                           config.granularity)
+        return cls(packed.to(home), scale.to(home), zero.to(home), config, linear.bias,
+                   linear.in_features, linear.out_features)
+
+    # ------------------------------------------------------------------
+    # Forward
+    # ------------------------------------------------------------------
+
+    def _group_size(self) -> int:
+        return kernel_group_size(self.config, self.in_features)
+
+    def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """Full weight [out, in] = (q - zero) * scale (pare/layers/linear.py:101-118),
+        cast once to ``dtype``."""
+        return dequantize_int4(self.packed_weight, self.scale, self.zero, self._group_size(),
+                               dtype=dtype, layout="storage", g_idx=self.g_idx)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError("pare_amd.QuantizedLinear runs on the HIP device only "
+                               "(no CPU fallback); move the module and input to cuda")
+        if getattr(self, "use_kernel", False):
+            return self._forward_kernel(x)
+        weight = self.dequantize(dtype=x.dtype)
+        return F.linear(x, weight, self.bias)
+
+    def _kernel_buffers(self):
+        """Kernel-layout weight, u8 zeros and act_order permutation, built once
+        per (device, weight contents) like linear.py:148-151."""
+        stamp = (self.packed_weight.device, self.packed_weight.data_ptr(),
+                 self.packed_weight._version, self.zero._version)
+        cache = getattr(self, "_kernel_cache", None)
+        if cache is None or cache[0] != stamp:
+            gs = self._group_size()
+            perm = None
+            if self.g_idx is not None:
+                perm = perm_from_g_idx(self.g_idx.to(self.packed_weight.device), gs)
+            self._packed_weight_kernel = repack_int4_for_kernel(self.packed_weight, gs, perm=perm)
+            cache = (stamp, zeros_to_u8(self.zero), perm)
+            self._kernel_cache = cache
+        return self._packed_weight_kernel, cache[1], cache[2]
+
+    def _forward_kernel(self, x: torch.Tensor) -> torch.Tensor:
+        """pare/layers/linear.py:140-159 with the HIP kernels."""
+        w_k, zero_u8, perm = self._kernel_buffers()
+        orig_shape = x.shape
+        x_2d = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm)
+        y = y.to(x.dtype)
+        if self.bias is not None:
+            y = y + self.bias
+        return y.reshape(*orig_shape[:-1], self.out_features)
+
+    def extra_repr(self) -> str:
+        return (f"in={self.in_features}, out={self.out_features}, dtype=INT4, "
+                f"scheme={self.config.scheme}, granularity={self.config.granularity}, "
+                f"use_kernel={getattr(self, 'use_kernel', False)}")

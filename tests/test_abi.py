@@ -1,0 +1,133 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/pare_amd.h declares with the arity the ctypes binding uses, and the
+host-side validation rejects malformed calls before anything is launched
+(pare/kernels/matmul_int4.py:208-217 and pare/core/pack.py:113 raise there)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from pare_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "pare_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    decls = {}
+    for m in re.finditer(r"PMI_API\s+[\w\s\*]+?\b(pmi_\w+)\s*\(([^)]*)\)", text, re.S):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return decls
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def test_header_declares_entry_points():
+    d = _declared()
+    assert {"pmi_matmul_w4a16", "pmi_repack_int4_for_kernel", "pmi_dequant_w4a16",
+            "pmi_rtn_quantize", "pmi_zeros_to_u8", "pmi_last_error"} <= set(d)
+
+
+def test_every_declared_symbol_is_exported_and_bound(L):
+    for name, arity in _declared().items():
+        assert hasattr(L, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+        assert len(_lib.SIGNATURES[name][1]) == arity, f"{name}: arity mismatch"
+
+
+def test_version(L):
+    assert L.pmi_abi_version() == 1
+
+
+def test_kernel_choice(L):
+    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
+    assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128) == 1
+    assert L.pmi_matmul_kernel_choice(16, 4096, 4096, 128) == 2
+    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
+    assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1
+
+
+FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid calls
+
+
+def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.PMI_F32,
+        perm=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16):
+    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, y, ydt, M, N, K, gs, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(K=200), _lib.PMI_ERR_INVALID, "divisible"),
+    (dict(gs=48, K=96), _lib.PMI_ERR_UNSUPPORTED, "multiple of 32"),
+    (dict(gs=0), _lib.PMI_ERR_INVALID, "group_size > 0"),
+    (dict(M=-1), _lib.PMI_ERR_INVALID, "M < 0"),
+    (dict(xdt=_lib.PMI_F32), _lib.PMI_ERR_UNSUPPORTED, "fp16"),
+    (dict(zdt=_lib.PMI_F16), _lib.PMI_ERR_INVALID, "zero dtype"),
+    (dict(x=None), _lib.PMI_ERR_INVALID, "null"),
+    (dict(s=None), _lib.PMI_ERR_INVALID, "null"),
+    (dict(x=FAKE + 2), _lib.PMI_ERR_INVALID, "x must be 16-byte aligned"),
+    (dict(w=FAKE + 4), _lib.PMI_ERR_INVALID, "weight must be 16-byte aligned"),
+    (dict(z=FAKE + 1), _lib.PMI_ERR_INVALID, "fp32 zeros"),
+])
+def test_matmul_validation(L, kw, code, msg):
+    rc = _mm(L, **kw)
+    assert rc == code
+    assert msg in _lib.last_error()
+
+
+def test_matmul_empty_is_noop(L):
+    assert _mm(L, M=0, x=None, w=None, s=None, z=None, y=None) == _lib.PMI_OK
+    assert _mm(L, N=0, x=None, w=None, s=None, z=None, y=None) == _lib.PMI_OK
+    assert _lib.last_error() == ""
+
+
+def test_repack_validation(L):
+    rc = L.pmi_repack_int4_for_kernel(FAKE, FAKE * 2, None, 8, 200, 128, None)
+    assert rc == _lib.PMI_ERR_INVALID and "divisible" in _lib.last_error()
+    rc = L.pmi_repack_int4_for_kernel(FAKE, FAKE, None, 8, 256, 128, None)
+    assert rc == _lib.PMI_ERR_INVALID and "in-place" in _lib.last_error()
+    assert L.pmi_repack_int4_for_kernel(None, None, None, 0, 256, 128, None) == _lib.PMI_OK
+
+
+def test_dequant_validation(L):
+    rc = L.pmi_dequant_w4a16(FAKE, 7, FAKE, FAKE, _lib.PMI_F32, None, FAKE, _lib.PMI_F16,
+                             4, 256, 128, None)
+    assert rc == _lib.PMI_ERR_INVALID and "layout" in _lib.last_error()
+    rc = L.pmi_dequant_w4a16(FAKE, 0, FAKE, FAKE, _lib.PMI_F32, None, FAKE, _lib.PMI_U8,
+                             4, 256, 128, None)
+    assert rc == _lib.PMI_ERR_INVALID and "out dtype" in _lib.last_error()
+
+
+def test_rtn_validation(L):
+    rc = L.pmi_rtn_quantize(FAKE, _lib.PMI_F32, FAKE, FAKE, FAKE, 4, 100, 128, 0, None)
+    assert rc == _lib.PMI_ERR_INVALID and "divisible" in _lib.last_error()
+    rc = L.pmi_rtn_quantize(FAKE, _lib.PMI_F32, FAKE, FAKE, FAKE, 4, 256, 128, 2, None)
+    assert rc == _lib.PMI_ERR_INVALID and "sym" in _lib.last_error()
+
+
+def test_error_message_is_thread_local(L):
+    import threading
+
+    _mm(L, K=200)
+    seen = {}
+
+    def other():
+        seen["msg"] = _lib.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "divisible" in _lib.last_error()
+
+
+def test_pmi_error_maps_to_runtime_error():
+    with pytest.raises(RuntimeError, match="PMI_ERR_INVALID"):
+        _lib.call("pmi_repack_int4_for_kernel", FAKE, FAKE * 2, None, 8, 200, 128, None)

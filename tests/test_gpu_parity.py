@@ -1,0 +1,441 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bars:
+  - integer/byte work (repack, RTN codes, zero conversion): bit-exact;
+  - dequantised weights: bit-exact with the reference dequant path in fp32,
+    fp16 and bf16;
+  - layer outputs: |y - y_ref| <= atol + rtol * |y_ref| with rtol = atol = 1e-2
+    in fp16 against the fp32-accumulated oracle; max-abs error is printed.
+Mirrors the reference's kernel tests (pare tests/test_triton_kernel.py:108-245)
+and widens them to the BASELINE shapes, group sizes and act_order.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import pare_amd as P
+from oracle import pare_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-2
+ATOL = 1e-2
+KAT = json.loads((Path(__file__).parent / "golden" / "kat_int4.json").read_text())
+DEV = "cuda"
+
+
+def _w(N, K, seed, std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(N, K, generator=g) * std).numpy().astype(np.float32)
+
+
+def _x(M, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).to(torch.float16)
+
+
+def _layer(N, K, gs, seed):
+    w = _w(N, K, seed)
+    packed, s, z = O.rtn_quantize(w, gs)
+    return packed, s, z
+
+
+def _cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _check_out(y_gpu, y_ref, what):
+    y = y_gpu.float().cpu().numpy()
+    err = np.abs(y - y_ref)
+    bound = ATOL + RTOL * np.abs(y_ref)
+    print(f"[parity] {what}: max_abs={err.max():.3e} max_rel_excess={(err - bound).max():.3e}",
+          flush=True)
+    assert np.isfinite(y).all(), f"{what}: non-finite output"
+    assert (err <= bound).all(), f"{what}: max_abs={err.max():.4e}"
+
+
+def _matmul_case(M, N, K, gs, seed, zero_u8=False):
+    packed, s, z = _layer(N, K, gs, seed)
+    x = _x(M, K, seed + 1000)
+    w_k = P.repack_int4_for_kernel(_cuda(packed), gs)
+    zz = _cuda(z)
+    if zero_u8:
+        zz = P.zeros_to_u8(zz)
+    y = P.matmul_w4a16(x.to(DEV), w_k, _cuda(s), zz, gs)
+    torch.cuda.synchronize()
+    ref = O.linear_fp32(x.float().numpy(), O.dequantize_packed(packed, s, z))
+    _check_out(y, ref, f"M={M} N={N} K={K} gs={gs} u8={zero_u8} kernel={P.kernel_choice(M, N, K, gs)}")
+
+
+def test_device_is_supported():
+    assert P.kernel_available(), "libpare_amd.so did not load or the device is not gfx950"
+
+
+# ---------------------------------------------------------------------------
+# integer / byte work: bit-exact
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K,gs", [(8, 256, 128), (16, 4096, 128), (7, 512, 32),
+                                    (5, 512, 64), (3, 1024, 256), (4, 384, 384)])
+def test_repack_bitexact(N, K, gs):
+    q = np.random.default_rng(N * K + gs).integers(0, 16, (N, K))
+    packed = O.pack_int4(q)
+    got = P.repack_int4_for_kernel(_cuda(packed), gs).cpu().numpy()
+    assert (got == O.repack_int4_for_kernel(packed, gs)).all()
+
+
+def test_repack_golden_pattern():
+    k = KAT["repack_pattern"]
+    got = P.repack_int4_for_kernel(_cuda(np.array(k["storage"], dtype=np.uint8)), k["group_size"])
+    assert got.cpu().tolist() == k["kernel"]
+
+
+def test_repack_with_perm_bitexact():
+    rng = np.random.default_rng(11)
+    N, K, gs = 6, 512, 128
+    q = rng.integers(0, 16, (N, K))
+    perm = rng.permutation(K).astype(np.int32)
+    packed = O.pack_int4(q)
+    got = P.repack_int4_for_kernel(_cuda(packed), gs, perm=_cuda(perm)).cpu().numpy()
+    want = O.repack_int4_for_kernel(O.permute_columns_packed(packed, perm), gs)
+    assert (got == want).all()
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128, 256, "channel"])
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_rtn_producer_bitexact(gs, wdtype):
+    N, K = 48, 512
+    w = torch.from_numpy(_w(N, K, 21)).to(wdtype)
+    wf = w.float().numpy()
+    if gs == "channel":
+        packed, s, z = P.rtn_quantize(w.to(DEV), granularity="per_channel")
+        rp, rs, rz = O.rtn_quantize(wf, granularity="per_channel")
+    else:
+        packed, s, z = P.rtn_quantize(w.to(DEV), gs)
+        rp, rs, rz = O.rtn_quantize(wf, gs)
+    assert (packed.cpu().numpy() == rp).all()
+    assert (s.cpu().numpy().view(np.uint32) == rs.view(np.uint32)).all()
+    assert (z.cpu().numpy() == rz).all()
+
+
+def test_rtn_producer_sym_bitexact():
+    w = _w(16, 256, 5)
+    packed, s, z = P.rtn_quantize(_cuda(w), 128, sym=True)
+    rp, rs, rz = O.rtn_quantize(w, 128, sym=True)
+    assert (packed.cpu().numpy() == rp).all()
+    assert (s.cpu().numpy().view(np.uint32) == rs.view(np.uint32)).all()
+    assert (z.cpu().numpy() == 0).all()
+
+
+@pytest.mark.parametrize("name", ["scale_zero_asym", "scale_zero_neg", "scale_zero_flat"])
+def test_rtn_golden(name):
+    k = KAT[name]
+    w = np.array(k["w"], dtype=np.float32)
+    packed, s, z = P.rtn_quantize(_cuda(w), k["group_size"])
+    assert s.item() == np.float32(k["scale"]) and z.item() == k["zero"]
+    q = O.unpack_int4(packed.cpu().numpy())
+    if "q" in k:
+        assert q.tolist() == k["q"]
+    else:
+        assert q.reshape(-1)[-1] == k["q_last"]
+
+
+def test_rtn_golden_sym_quirk():
+    k = KAT["sym_unsigned_quirk"]
+    packed, s, z = P.rtn_quantize(_cuda(np.array(k["w"], dtype=np.float32)), 128, sym=True)
+    assert s.item() == np.float32(k["scale"])
+    assert O.unpack_int4(packed.cpu().numpy()).reshape(-1)[:4].tolist() == k["q_head"]
+
+
+def test_zeros_to_u8():
+    z = np.random.default_rng(3).integers(0, 16, (64, 8, 1)).astype(np.float32)
+    got = P.zeros_to_u8(_cuda(z)).cpu().numpy()
+    assert got.dtype == np.uint8 and (got == z.reshape(64, 8)).all()
+    bad = z.copy()
+    bad[0, 0, 0] = 3.5
+    bad[1, 1, 0] = 16.0
+    with pytest.raises(ValueError, match="2 zero points"):
+        P.zeros_to_u8(_cuda(bad))
+
+
+# ---------------------------------------------------------------------------
+# dequantised weights: bit-exact
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("layout", ["storage", "kernel"])
+@pytest.mark.parametrize("gs", [32, 128, 256])
+def test_dequant_bitexact(layout, gs):
+    N, K = 40, 1024
+    packed, s, z = _layer(N, K, gs, 31)
+    ref32 = O.dequantize_packed(packed, s, z)
+    src = _cuda(packed) if layout == "storage" else P.repack_int4_for_kernel(_cuda(packed), gs)
+    for dt, view in ((torch.float32, np.uint32), (torch.float16, np.uint16)):
+        got = P.dequantize_int4(src, _cuda(s), _cuda(z), gs, dtype=dt, layout=layout).cpu()
+        want = ref32 if dt == torch.float32 else ref32.astype(np.float16)
+        assert (got.numpy().view(view) == want.view(view)).all(), f"{layout} {dt}"
+    got = P.dequantize_int4(src, _cuda(s), _cuda(z), gs, dtype=torch.bfloat16, layout=layout).cpu()
+    want = torch.from_numpy(ref32).to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_dequant_pow2_golden():
+    k = KAT["dequant_pow2"]
+    packed = O.pack_int4(np.array(k["q"], dtype=np.int32))
+    N, K = 1, 4
+    # one group of 4 columns is below the 32-column kernel tiling, so pad K to 128
+    q = np.zeros((1, 128), dtype=np.int32)
+    q[0, :4] = k["q"]
+    packed = O.pack_int4(q)
+    s = np.full((1, 1, 1), k["scale"], dtype=np.float32)
+    z = np.full((1, 1, 1), k["zero"], dtype=np.float32)
+    got = P.dequantize_int4(_cuda(packed), _cuda(s), _cuda(z), 128, dtype=torch.float16)
+    assert got.float().cpu().numpy()[0, :4].tolist() == k["w"][0]
+
+
+def test_dequant_gidx_bitexact():
+    rng = np.random.default_rng(41)
+    N, K, gs = 24, 768, 128
+    w = _w(N, K, 41)
+    perm = rng.permutation(K)
+    packed, s, z, g = O.rtn_quantize_act_order(w, perm, gs)
+    ref = O.dequantize_gidx(O.unpack_int4(packed), s, z, g)
+    got = P.dequantize_int4(_cuda(packed), _cuda(s), _cuda(z), gs, g_idx=_cuda(g)).cpu().numpy()
+    assert (got.view(np.uint32) == ref.view(np.uint32)).all()
+    # kernel layout with the permutation derived from g_idx reproduces the same weights
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+    got_k = P.dequantize_int4(wk, _cuda(s), _cuda(z), gs, layout="kernel", perm=pm).cpu().numpy()
+    assert (got_k.view(np.uint32) == ref.view(np.uint32)).all()
+
+
+# ---------------------------------------------------------------------------
+# matmul: tolerance vs fp32-accumulated oracle
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m", [1, 4, 16, 64])
+def test_matches_dequant_on_the_fly_256(m):
+    """test_triton_kernel.py:127-143 shape, stricter tolerance."""
+    _matmul_case(m, 256, 256, 128, 1)
+
+
+def test_non_divisible_m():
+    """test_triton_kernel.py:154-167."""
+    for m in [1, 3, 7, 31]:
+        _matmul_case(m, 256, 256, 128, 7)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 16, 17, 32, 33, 64, 65, 128])
+def test_matmul_m_sweep(M):
+    _matmul_case(M, 1040, 1024, 128, 100 + M)
+
+
+@pytest.mark.parametrize("N,K", [(1024, 4096), (4096, 4096), (520, 3584), (96, 18944),
+                                 (4096, 14336)])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_matmul_shapes(M, N, K):
+    _matmul_case(M, N, K, 128, N + K + M)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256, "channel"])
+@pytest.mark.parametrize("M", [1, 3, 20])
+def test_matmul_group_sizes(gs, M):
+    K = 1024
+    _matmul_case(M, 272, K, K if gs == "channel" else gs, 7 * M)
+
+
+@pytest.mark.parametrize("M", [1, 2, 16, 64])
+def test_matmul_u8_zeros(M):
+    _matmul_case(M, 512, 2048, 128, 3 + M, zero_u8=True)
+
+
+def test_zero_input_gives_zero_output():
+    packed, s, z = _layer(128, 256, 128, 2)
+    w = P.repack_int4_for_kernel(_cuda(packed), 128)
+    for m in (1, 8):
+        y = P.matmul_w4a16(torch.zeros(m, 256, dtype=torch.float16, device=DEV), w, _cuda(s),
+                           _cuda(z), 128)
+        assert y.abs().max().item() == 0.0
+
+
+def test_deterministic():
+    packed, s, z = _layer(4096, 4096, 128, 9)
+    w = P.repack_int4_for_kernel(_cuda(packed), 128)
+    for m in (1, 64):
+        x = _x(m, 4096, 10).to(DEV)
+        a = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
+        b = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_scales_shapes_accepted():
+    packed, s, z = _layer(64, 256, 128, 12)
+    w = P.repack_int4_for_kernel(_cuda(packed), 128)
+    x = _x(2, 256, 13).to(DEV)
+    y3 = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
+    y2 = P.matmul_w4a16(x, w, _cuda(s.reshape(64, 2)), _cuda(z.reshape(64, 2)), 128)
+    assert torch.equal(y3, y2)
+
+
+def test_matmul_rejects_bad_zeros():
+    packed, s, z = _layer(64, 256, 128, 12)
+    w = P.repack_int4_for_kernel(_cuda(packed), 128)
+    zb = z.copy()
+    zb[3, 1, 0] = 2.5
+    with pytest.raises(ValueError, match="integers"):
+        P.matmul_w4a16(_x(1, 256, 1).to(DEV), w, _cuda(s), _cuda(zb), 128)
+
+
+def test_matmul_reference_errors():
+    packed, s, z = _layer(64, 256, 128, 12)
+    w = P.repack_int4_for_kernel(_cuda(packed), 128)
+    with pytest.raises(RuntimeError):
+        P.matmul_w4a16(_x(1, 256, 1), w, _cuda(s), _cuda(z), 128)  # CPU x
+    with pytest.raises(AssertionError):
+        P.matmul_w4a16(_x(1, 256, 1).to(DEV).float(), w, _cuda(s), _cuda(z), 128)
+    with pytest.raises(AssertionError):
+        P.matmul_w4a16(_x(2, 512, 1).to(DEV)[:, ::2], w, _cuda(s), _cuda(z), 128)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("N,K", [(512, 3584), (3584, 3584), (200, 18944)])
+def test_matmul_act_order(M, N, K):
+    """Qwen2.5-7B-style act_order: g_idx from a seeded permutation."""
+    gs = 128
+    rng = np.random.default_rng(N + K)
+    w = _w(N, K, N + K)
+    perm_np = rng.permutation(K)
+    packed, s, z, g = O.rtn_quantize_act_order(w, perm_np, gs)
+    x = _x(M, K, 5)
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+    y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), _cuda(z), gs, perm=pm)
+    ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
+    _check_out(y, ref, f"act_order M={M} N={N} K={K}")
+
+
+# ---------------------------------------------------------------------------
+# QuantizedLinear integration (test_triton_kernel.py:174-245)
+# ---------------------------------------------------------------------------
+
+def _ql(N, K, seed=0, bias=False):
+    torch.manual_seed(seed)
+    lin = torch.nn.Linear(K, N, bias=bias)
+    return P.QuantizedLinear.from_linear(lin, P.QuantConfig(bits=4, scheme="rtn", group_size=128)), lin
+
+
+def test_from_linear_buffers_match_oracle():
+    ql, lin = _ql(64, 256)
+    rp, rs, rz = O.rtn_quantize(lin.weight.detach().numpy(), 128)
+    assert (ql.packed_weight.cpu().numpy() == rp).all()
+    assert (ql.scale.cpu().numpy() == rs).all() and (ql.zero.cpu().numpy() == rz).all()
+    assert ql.packed_weight.shape == (64, 128) and ql.packed_weight.dtype == torch.uint8
+
+
+def test_use_kernel_flag_and_matches_dequant_path():
+    ql, _ = _ql(256, 256, seed=3)
+    ql = ql.cuda()
+    x = torch.randn(8, 256, device=DEV, dtype=torch.float16)
+    with torch.no_grad():
+        y_std = ql(x).float()
+        ql.use_kernel = True
+        y_k = ql(x).float()
+    assert y_k.shape == (8, 256) and not y_k.isnan().any()
+    assert (y_std - y_k).abs().max().item() < 0.05
+
+
+def test_module_dequantize_bitexact():
+    ql, _ = _ql(128, 512, seed=4)
+    ql = ql.cuda()
+    ref = O.dequantize_packed(ql.packed_weight.cpu().numpy(), ql.scale.cpu().numpy(),
+                              ql.zero.cpu().numpy())
+    got = ql.dequantize().cpu().numpy()
+    assert (got.view(np.uint32) == ref.view(np.uint32)).all()
+
+
+def test_lazy_repack_cached():
+    ql, _ = _ql(128, 256)
+    ql.use_kernel = True
+    ql = ql.cuda()
+    x = torch.randn(2, 256, device=DEV, dtype=torch.float16)
+    assert not hasattr(ql, "_packed_weight_kernel")
+    with torch.no_grad():
+        ql(x)
+    assert hasattr(ql, "_packed_weight_kernel")
+    buf = id(ql._packed_weight_kernel)
+    with torch.no_grad():
+        ql(x)
+    assert id(ql._packed_weight_kernel) == buf
+
+
+def test_3d_input_and_bias():
+    ql, lin = _ql(256, 256, bias=True)
+    ql.use_kernel = True
+    ql = ql.cuda()
+    x = torch.randn(2, 64, 256, device=DEV, dtype=torch.float16)
+    with torch.no_grad():
+        y = ql(x)
+    assert y.shape == (2, 64, 256)
+    w16 = ql.dequantize(torch.float16).float()
+    ref = x.float() @ w16.T + ql.bias.float()
+    assert (y.float() - ref).abs().max().item() < 0.05
+
+
+def test_bf16_input_round_trip_dtype():
+    ql, _ = _ql(128, 256)
+    ql.use_kernel = True
+    ql = ql.cuda()
+    x = torch.randn(3, 256, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        y = ql(x)
+    assert y.dtype == torch.bfloat16
+    ref = x.to(torch.float16).float() @ ql.dequantize(torch.float16).float().T
+    assert (y.float() - ref).abs().max().item() < 0.05
+
+
+def test_cpu_input_raises_instead_of_fallback():
+    ql, _ = _ql(64, 128)
+    ql.use_kernel = True
+    with pytest.raises(RuntimeError, match="HIP device"):
+        ql(torch.randn(4, 128))
+
+
+def test_from_tensors_without_use_kernel_attr():
+    ql, _ = _ql(64, 256)
+    ql2 = P.QuantizedLinear.from_tensors(ql.packed_weight, None, ql.scale, ql.zero, ql.config,
+                                         None, 256, 64).cuda()
+    del ql2.use_kernel  # a layer object that never had the flag (linear.py:166-202)
+    with torch.no_grad():
+        y = ql2(torch.randn(2, 256, device=DEV, dtype=torch.float16))
+    assert y.shape == (2, 64)
+
+
+def test_act_order_module():
+    rng = np.random.default_rng(8)
+    N, K, gs = 96, 512, 128
+    w = _w(N, K, 8)
+    perm = rng.permutation(K)
+    packed, s, z, g = O.rtn_quantize_act_order(w, perm, gs)
+    ql = P.QuantizedLinear(_cuda(packed), _cuda(s), _cuda(z), P.QuantConfig(group_size=gs), None,
+                           K, N, use_kernel=True, g_idx=_cuda(g))
+    x = _x(4, K, 2)
+    with torch.no_grad():
+        y = ql(x.to(DEV))
+    ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
+    _check_out(y, ref, "act_order module")
+
+
+# ---------------------------------------------------------------------------
+# BASELINE full sizes
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+def test_llama_decode_layers_full_size(N, K):
+    """Llama-3.1-8B decode layers at M=1 (and the M=64 crossover side)."""
+    for M in (1, 64):
+        _matmul_case(M, N, K, 128, 10 + N // 1024 + M)
