@@ -90,16 +90,18 @@ def capture(fn, stream):
 
 
 def time_graph(g, reps, stream):
+    """ms per replay; the replays and both events are on `stream`."""
     import torch
 
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(reps):
-        g.replay()
-    end.record(stream)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            g.replay()
+        end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / reps  # ms
+    return start.elapsed_time(end) / reps
 
 
 def cpu_baseline(max_threads=16):
@@ -216,15 +218,17 @@ def main():
     for k in outs:
         outs[k].zero_()
     for rep in range(2):
-        graph.replay()
+        with torch.cuda.stream(stream):
+            graph.replay()
         torch.cuda.synchronize()
         for k in outs:
             assert torch.equal(outs[k][:1], eager[k]), f"graph replay {rep} differs on {k}"
     log("graph replay == eager outputs")
 
     # --- timed region: K replays of the decode-layer-set step -------------
-    for _ in range(args.warmup):
-        graph.replay()
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            graph.replay()
     torch.cuda.synchronize()
     ms_step = time_graph(graph, args.steps, stream)
     step_bytes = n_layers * sum(layer_bytes(N, K, 1) for _, N, K in LLAMA)

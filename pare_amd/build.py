@@ -31,6 +31,10 @@ HIPCC_FLAGS = [
     # Packed fp32 arithmetic is kept out of the generated code on purpose.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fvisibility=hidden",
+    # No implicit contraction: hipcc would otherwise fold (f16)(a * b) into one
+    # v_fma_mixlo_f16 (a single rounding) where the reference rounds to fp32
+    # first and then to fp16. Wanted fusions are written as fmaf().
+    "-ffp-contract=off",
 ]
 
 

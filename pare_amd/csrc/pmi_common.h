@@ -12,10 +12,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define PMI_DEV __device__ __forceinline__
 
-// fp16 bit pattern 0x6400 is 1024.0; OR-ing a nibble q into its mantissa gives
-// exactly 1024 + q. Two such halves per 32-bit word.
-#define PMI_MAGIC_X2 0x64006400u
-#define PMI_NIB_X2 0x000F000Fu
+// fp16 bit pattern 0x6400 is 1024.0; a nibble q in its low mantissa bits
+// gives exactly 1024 + q.
 
 PMI_DEV f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 PMI_DEV uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -27,14 +25,20 @@ PMI_DEV uint32_t neg_magic_zero_x2(uint32_t z) { return (0xE400u | z) * 0x000100
 // Four half2 values (q - z) from one 32-bit word w of packed nibbles.
 // With bytes b0..b3 of w (byte i = lo_i | hi_i << 4) the results are
 //   d0 = (lo0, lo2), d1 = (lo1, lo3), d2 = (hi0, hi2), d3 = (hi1, hi3).
-// Every value is an integer in [-15, 15], so the fp16 subtraction is exact.
+// The nibbles are first spread to one per byte; v_perm_b32 then places each
+// nibble under a 0x64 high byte, giving the fp16 value 1024 + q. Every
+// result is an integer in [-15, 15], so the fp16 subtraction is exact.
+// 7 bit ops + 4 packed-fp16 subtracts per word.
 PMI_DEV void unpack_word_minus_zero(uint32_t w, uint32_t nz, f16x2& d0, f16x2& d1,
                                     f16x2& d2, f16x2& d3) {
   const f16x2 z2 = as_f16x2(nz);
-  d0 = as_f16x2((w & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
-  d1 = as_f16x2(((w >> 8) & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
-  d2 = as_f16x2(((w >> 4) & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
-  d3 = as_f16x2(((w >> 12) & PMI_NIB_X2) | PMI_MAGIC_X2) + z2;
+  const uint32_t lo = w & 0x0F0F0F0Fu;
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+  // selector bytes 0..3 pick from the second operand, 4 picks 0x64
+  d0 = as_f16x2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04020400u)) + z2;
+  d1 = as_f16x2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030401u)) + z2;
+  d2 = as_f16x2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04020400u)) + z2;
+  d3 = as_f16x2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030401u)) + z2;
 }
 
 // (a.lo16, b.lo16) and (a.hi16, b.hi16) of two words holding consecutive
@@ -45,6 +49,16 @@ PMI_DEV uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(
 
 PMI_DEV float dot2_acc(f16x2 a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(a, as_f16x2(b), c, false);
+}
+
+// fp32 -> fp16, round to nearest even, from a materialised fp32 value. The
+// empty asm keeps the backend from folding the producer of v into the
+// conversion: (f16)(a * b) would otherwise become one v_fma_mixlo_f16 that
+// rounds the exact product once, where the reference rounds to fp32 first
+// and then to fp16 (they differ when the fp32 product is an fp16 tie).
+PMI_DEV f16 f32_to_f16_rne(float v) {
+  asm volatile("" : "+v"(v));
+  return (f16)v;
 }
 
 // fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
@@ -59,4 +73,11 @@ PMI_DEV uint16_t f32_to_bf16_rne(float f) {
 PMI_DEV uint32_t load_zero(const void* zeros, int zero_u8, int64_t idx) {
   if (zero_u8) return (uint32_t)((const uint8_t*)zeros)[idx];
   return (uint32_t)(int)((const float*)zeros)[idx];
+}
+
+// Column index read from a caller-supplied permutation, clamped into [0, K)
+// so a malformed permutation cannot make a kernel read outside the row.
+PMI_DEV int perm_col(const int32_t* __restrict__ perm, int k, int K) {
+  const int p = perm[k];
+  return (unsigned)p < (unsigned)K ? p : 0;
 }

@@ -8,11 +8,13 @@
 namespace pmi {
 
 struct GemvConfig {
-  int rows_per_wave;  // R: weight rows one wave walks with one x slice in registers
-  int slice_waves;    // waves that split one row's K range (1 slice = 2048 columns)
-  int row_waves;      // waves that take different row blocks of the same slices
-  int n_slices;       // ceil(K / 2048)
-  int grid;           // workgroups
+  int rows_per_wave;    // U: rows per batch of one wave (x stays in registers)
+  int slices_per_wave;  // 1, or 2 when K needs more than 8 slices
+  int slice_waves;      // waves that split one row's K range (1 slice = 2048 columns)
+  int row_waves;        // waves that take different rows of the same slices
+  int n_slices;         // ceil(K / 2048)
+  int rows_per_wg;      // contiguous rows owned by one workgroup
+  int grid;             // workgroups
 };
 
 struct GemmConfig {

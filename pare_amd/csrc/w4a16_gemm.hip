@@ -97,10 +97,15 @@ w4a16_gemm_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         if (m0 + m < M) {
           const int64_t xr = (int64_t)(m0 + m) * K;
           if constexpr (PERM) {
-            l0 = (uint32_t)xs[xr + perm[kk]] | ((uint32_t)xs[xr + perm[kk + 1]] << 16);
-            l1 = (uint32_t)xs[xr + perm[kk + 2]] | ((uint32_t)xs[xr + perm[kk + 3]] << 16);
-            h0 = (uint32_t)xs[xr + perm[kk + hgs]] | ((uint32_t)xs[xr + perm[kk + hgs + 1]] << 16);
-            h1 = (uint32_t)xs[xr + perm[kk + hgs + 2]] | ((uint32_t)xs[xr + perm[kk + hgs + 3]] << 16);
+            const uint16_t* xrow = xs + xr;
+            l0 = (uint32_t)xrow[perm_col(perm, kk, K)] |
+                 ((uint32_t)xrow[perm_col(perm, kk + 1, K)] << 16);
+            l1 = (uint32_t)xrow[perm_col(perm, kk + 2, K)] |
+                 ((uint32_t)xrow[perm_col(perm, kk + 3, K)] << 16);
+            h0 = (uint32_t)xrow[perm_col(perm, kk + hgs, K)] |
+                 ((uint32_t)xrow[perm_col(perm, kk + hgs + 1, K)] << 16);
+            h1 = (uint32_t)xrow[perm_col(perm, kk + hgs + 2, K)] |
+                 ((uint32_t)xrow[perm_col(perm, kk + hgs + 3, K)] << 16);
           } else {
             const uint2 lo = *reinterpret_cast<const uint2*>(xs + xr + kk);
             const uint2 hi = *reinterpret_cast<const uint2*>(xs + xr + kk + hgs);
@@ -148,7 +153,7 @@ w4a16_gemm_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = m0 + 16 * i + 4 * lg + v;
-        if (m < M && n < N) y[(int64_t)m * N + n] = (f16)acc[i][nb][v];
+        if (m < M && n < N) y[(int64_t)m * N + n] = f32_to_f16_rne(acc[i][nb][v]);
       }
     }
 }

@@ -1,20 +1,30 @@
 // Split-K INT4 W4A16 GEMV for decode (M = 1..4), gfx950.
 //
 // Work layout. A packed weight row (kernel layout, K/2 bytes) is cut into
-// 16-byte chunks; 64 consecutive chunks (2048 columns) form a "slice", the
-// K range one wave covers with one 128-bit load per lane. Because the kernel
-// layout keeps each 16-byte chunk inside one quantisation group, lane l of a
-// wave always needs the same 32 activation values for every row: it loads
-// them once, reorders them into fp16 pairs that line up with the nibble
-// unpack, and keeps them in registers while the wave walks R weight rows.
-// Per row and lane: one 16-byte weight load, one scale and one zero load,
-// 4 x (7 bit ops + 4 packed-fp16 subtracts + 4 v_dot2_f32_f16), one fp32 FMA
-// with the group scale (the scale is factored out of the group sum).
+// 16-byte chunks; 64 consecutive chunks (2048 columns) form a "slice", the K
+// range one wave covers with one 128-bit load per lane. The kernel layout keeps
+// every 16-byte chunk inside one quantisation group, so lane l of a wave needs
+// the same 32 activations for every weight row: it loads them once, reorders
+// them into fp16 pairs that line up with the nibble unpack, and keeps them in
+// registers for the life of the wave, together with their sum Sx.
 //
-// A workgroup is slice_waves x row_waves waves. The partial sums of a row
-// are reduced across the 64 lanes with a transpose-style butterfly, then
-// across the slice waves through LDS in a fixed order, so results are
-// deterministic and no workspace or atomics are needed.
+// Arithmetic. A nibble zero-extended into an fp16 half is the subnormal
+// q * 2^-24, exact. v_dot2_f32_f16 on those halves and the activation pairs
+// gives sum x*q * 2^-24 with exact products and fp32 sums, and the group term
+// is s * (2^24 * sum x*q - z * Sx) = s * sum x*(q - z). Per 32-bit word of
+// nibbles: 7 bit ops + 4 v_dot2_f32_f16; per row two FMAs per activation row.
+//
+// Pipeline. A workgroup is slice_waves x row_waves waves and owns a contiguous
+// range of rows. Each wave walks its rows in batches of U with a two-deep
+// software pipeline: buffer loads of batch i+1 (row offsets in SGPRs, so no
+// address VALU) are in flight while batch i is unpacked and reduced. Every
+// load is unconditional, so the compiler waits for exactly the older batch.
+//
+// Reduction. Partial sums of a batch are reduced across the 64 lanes with a
+// transpose butterfly (v_permlane32_swap / v_permlane16_swap for the two wide
+// steps, DPP row_mirror / row_half_mirror / quad_perm for the rest), then
+// across the slice waves through LDS in a fixed order: results are
+// deterministic and no workspace or atomics are used.
 //
 // Semantics follow the reference Triton kernel (pare/kernels/matmul_int4.py:
 // 105-176): w = (q - zero) * scale per group, fp32 accumulation, fp16 output.
@@ -25,6 +35,7 @@ namespace pmi {
 namespace {
 
 constexpr int kSliceChunks = 64;  // 16-byte chunks per slice (one per lane)
+constexpr int kMaxWaves = 8;      // waves per workgroup
 
 template <int V>
 struct Pow2Ceil {
@@ -45,12 +56,11 @@ struct Log2<1> {
 };
 
 // The 32 activations of one row that match this lane's chunk: columns
-// k_lo..k_lo+15 (low nibbles) and k_hi..k_hi+15 (high nibbles), reordered so
-// xp[4i+c] pairs with d_c of weight word i (see unpack_word_minus_zero).
+// k_lo..k_lo+15 (low nibbles) and k_hi..k_hi+15 (high nibbles), as raw
+// consecutive pairs a[i] = (x[k_lo+2i], x[k_lo+2i+1]), b[i] likewise at k_hi.
 template <bool PERM>
-PMI_DEV void load_x_pairs(const f16* __restrict__ xrow, const int32_t* __restrict__ perm,
-                          int k_lo, int k_hi, uint32_t (&xp)[16]) {
-  uint32_t a[8], b[8];
+PMI_DEV void load_x_raw(const f16* __restrict__ xrow, const int32_t* __restrict__ perm, int k_lo,
+                        int k_hi, int K, uint32_t (&a)[8], uint32_t (&b)[8]) {
   if constexpr (!PERM) {
     const u32x4* pa = reinterpret_cast<const u32x4*>(xrow + k_lo);
     const u32x4* pb = reinterpret_cast<const u32x4*>(xrow + k_hi);
@@ -63,10 +73,17 @@ PMI_DEV void load_x_pairs(const f16* __restrict__ xrow, const int32_t* __restric
     const uint16_t* xs = reinterpret_cast<const uint16_t*>(xrow);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      a[i] = (uint32_t)xs[perm[k_lo + 2 * i]] | ((uint32_t)xs[perm[k_lo + 2 * i + 1]] << 16);
-      b[i] = (uint32_t)xs[perm[k_hi + 2 * i]] | ((uint32_t)xs[perm[k_hi + 2 * i + 1]] << 16);
+      a[i] = (uint32_t)xs[perm_col(perm, k_lo + 2 * i, K)] |
+             ((uint32_t)xs[perm_col(perm, k_lo + 2 * i + 1, K)] << 16);
+      b[i] = (uint32_t)xs[perm_col(perm, k_hi + 2 * i, K)] |
+             ((uint32_t)xs[perm_col(perm, k_hi + 2 * i + 1, K)] << 16);
     }
   }
+}
+
+// Reorders the raw pairs so xp[4i+c] lines up with nibble pair c of weight
+// word i: (x0,x2), (x1,x3) from the low half, the same from the high half.
+PMI_DEV void pair_x(const uint32_t (&a)[8], const uint32_t (&b)[8], uint32_t (&xp)[16]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     xp[4 * i + 0] = pair_lo(a[2 * i], a[2 * i + 1]);
@@ -76,167 +93,348 @@ PMI_DEV void load_x_pairs(const f16* __restrict__ xrow, const int32_t* __restric
   }
 }
 
-// Reduces VP values per lane across the wave. Afterwards every lane holds the
-// wave-wide sum of value index (lane >> (6 - log2 VP)) in v[0].
-template <int VP>
-PMI_DEV void wave_transpose_reduce(float (&v)[VP], int lane) {
+// dst = keep + (value of `send` in the partner lane), partner given by a DPP
+// control that pairs lanes differing in the step's lane bit.
+template <int CTRL>
+PMI_DEV float dpp_add(float keep, float send) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), CTRL, 0xf, 0xf,
+                                                false);
+  return keep + __builtin_bit_cast(float, moved);
+}
+
+// One transpose step with partner lane^o for o = 32 or 16. After
+// v_permlane{32,16}_swap_b32 a, b the pair (a, b) holds, per lane, the own
+// and the partner value of one index, so a + b is the pair sum of index i on
+// the lower lane and of index i + half on the upper lane. Written as inline
+// asm on two tied registers: the compiler builtin's two results were read
+// back as the same register when summed (hipcc 7.2), doubling the own value.
+// The s_nops cover the VALU-write -> permlane-read hazard on both sides.
+template <int O>
+PMI_DEV float swap_add(float lo, float hi) {
+  uint32_t a = __builtin_bit_cast(uint32_t, lo), b = __builtin_bit_cast(uint32_t, hi);
+  if constexpr (O == 32)
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  else
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+// DPP partner controls for lane bits 3, 2, 1, 0: row_mirror (l <-> 15-l),
+// row_half_mirror (l <-> 7-l), quad_perm [2,3,0,1], quad_perm [1,0,3,2]. The
+// mirrors also flip lower lane bits, which is harmless because the steps run
+// from the high bit down and lower bits have not split the values yet.
+template <int STEP>
+struct DppCtrl;
+template <> struct DppCtrl<2> { static constexpr int v = 0x140; };
+template <> struct DppCtrl<3> { static constexpr int v = 0x141; };
+template <> struct DppCtrl<4> { static constexpr int v = 0x4E; };
+template <> struct DppCtrl<5> { static constexpr int v = 0xB1; };
+
+template <int VP, int STEP>
+PMI_DEV void reduce_step(float (&v)[VP], int lane) {
+  constexpr int o = 32 >> STEP;
+  constexpr int cnt = VP >> STEP;  // values still held per lane
+  if constexpr (STEP < 2) {
+    if constexpr (cnt > 1) {
 #pragma unroll
-  for (int step = 0; step < 6; ++step) {
-    const int o = 32 >> step;
-    const int cnt = VP >> step;  // values still held per lane
-    if (cnt > 1) {
-      const int half = cnt / 2;
+      for (int i = 0; i < cnt / 2; ++i) v[i] = swap_add<o>(v[i], v[i + cnt / 2]);
+    } else {
+      v[0] = swap_add<o>(v[0], v[0]);
+    }
+  } else {
+    if constexpr (cnt > 1) {
       const bool upper = (lane & o) != 0;
 #pragma unroll
-      for (int i = 0; i < half; ++i) {
-        const float send = upper ? v[i] : v[i + half];
-        const float keep = upper ? v[i + half] : v[i];
-        v[i] = keep + __shfl_xor(send, o, 64);
+      for (int i = 0; i < cnt / 2; ++i) {
+        const float send = upper ? v[i] : v[i + cnt / 2];
+        const float keep = upper ? v[i + cnt / 2] : v[i];
+        v[i] = dpp_add<DppCtrl<STEP>::v>(keep, send);
       }
     } else {
-      v[0] += __shfl_xor(v[0], o, 64);
+      v[0] = dpp_add<DppCtrl<STEP>::v>(v[0], v[0]);
     }
   }
 }
 
-template <int MT, int R, bool PERM>
-__global__ void __launch_bounds__(512)
-w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
-                  const float* __restrict__ scales, const void* __restrict__ zeros, int zero_u8,
-                  const int32_t* __restrict__ perm, f16* __restrict__ y, int N, int K, int gs,
-                  int n_slices, int slice_waves, int row_waves) {
-  constexpr int V = R * MT;
-  constexpr int VP = Pow2Ceil<V>::value;
-  constexpr int LOGV = Log2<VP>::value;
-  extern __shared__ float red[];  // [row_waves][slice_waves][V]
+// Reduces VP values per lane across the wave. Afterwards every lane holds the
+// wave-wide sum of value index (lane >> (6 - log2 VP)) in v[0].
+template <int VP>
+PMI_DEV void wave_transpose_reduce(float (&v)[VP], int lane) {
+  reduce_step<VP, 0>(v, lane);
+  reduce_step<VP, 1>(v, lane);
+  reduce_step<VP, 2>(v, lane);
+  reduce_step<VP, 3>(v, lane);
+  reduce_step<VP, 4>(v, lane);
+  reduce_step<VP, 5>(v, lane);
+}
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int ws = wave % slice_waves;
-  const int wr = wave / slice_waves;
-  const int row_chunks = K >> 5;
-  const int hgs = gs >> 1;  // bytes per group tile
-  const int G = K / gs;
-  const int64_t row_bytes = K >> 1;
-  const int n0 = (blockIdx.x * row_waves + wr) * R;
+// One batch of U weight rows for the SPW slices a lane covers. z holds the raw
+// zero point (u8 value or fp32 bits) and is converted only when used.
+template <int U, int SPW>
+struct Batch {
+  u32x4 w[SPW][U];
+  float s[SPW][U];
+  uint32_t z[SPW][U];
+};
 
-  float acc[R][MT];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+struct Rsrc {
+  __amdgpu_buffer_rsrc_t w, s, z;
+};
 
-  for (int s = ws; s < n_slices; s += slice_waves) {
-    const int chunk = s * kSliceChunks + lane;
-    if (chunk < row_chunks) {
-      const int b = chunk << 4;  // byte offset inside the row
-      const int t = b / hgs;     // group (tile) index
-      const int j = b - t * hgs;
-      const int k_lo = t * gs + j;
-      const int k_hi = k_lo + hgs;
+// Raw buffer resource over `bytes` bytes (untyped dword access).
+PMI_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 
-      u32x4 wv[R];
-      float sc[R];
-      uint32_t nz[R];
+// Every load is unconditional: rows past the workgroup's range re-read its
+// last row (their results are never written) and inactive lanes read byte
+// offset 0 (their activations are zero). Row offsets are wave-uniform and go
+// in the SGPR offset of the buffer load; lane offsets are fixed per wave.
+template <int U, int SPW, bool ZU8>
+PMI_DEV void load_batch(Batch<U, SPW>& bt, const Rsrc& rs, int first_row, int row_last,
+                        int row_bytes, int G, const int (&boff)[SPW], const int (&grp)[SPW]) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int n = n0 + r;
-        if (n < N) {
-          wv[r] = *reinterpret_cast<const u32x4*>(w + (int64_t)n * row_bytes + b);
-          sc[r] = scales[(int64_t)n * G + t];
-          nz[r] = neg_magic_zero_x2(load_zero(zeros, zero_u8, (int64_t)n * G + t));
-        } else {
-          wv[r] = u32x4{0u, 0u, 0u, 0u};
-          sc[r] = 0.f;
-          nz[r] = neg_magic_zero_x2(0u);
-        }
-      }
-
-      uint32_t xp[MT][16];
+  for (int u = 0; u < U; ++u) {
+    const int n = min(first_row + u, row_last);
 #pragma unroll
-      for (int m = 0; m < MT; ++m) load_x_pairs<PERM>(x + (int64_t)m * K, perm, k_lo, k_hi, xp[m]);
-
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float p[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) p[m] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f16x2 d0, d1, d2, d3;
-          unpack_word_minus_zero(wv[r][i], nz[r], d0, d1, d2, d3);
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            p[m] = dot2_acc(d0, xp[m][4 * i + 0], p[m]);
-            p[m] = dot2_acc(d1, xp[m][4 * i + 1], p[m]);
-            p[m] = dot2_acc(d2, xp[m][4 * i + 2], p[m]);
-            p[m] = dot2_acc(d3, xp[m][4 * i + 3], p[m]);
-          }
-        }
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = fmaf(p[m], sc[r], acc[r][m]);
-      }
+    for (int sp = 0; sp < SPW; ++sp) {
+      const u32x4 wv = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, boff[sp], n * row_bytes, 0));
+      bt.w[sp][u] = wv;
+      bt.s[sp][u] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs.s, grp[sp] * 4, n * G * 4, 0));
+      if constexpr (ZU8)
+        bt.z[sp][u] = __builtin_amdgcn_raw_buffer_load_b8(rs.z, grp[sp], n * G, 0);
+      else
+        bt.z[sp][u] = __builtin_amdgcn_raw_buffer_load_b32(rs.z, grp[sp] * 4, n * G * 4, 0);
     }
   }
+}
 
+template <bool ZU8>
+PMI_DEV float zero_value(uint32_t raw) {
+  if constexpr (ZU8) return (float)raw;
+  return __builtin_bit_cast(float, raw);
+}
+
+// Unpacks and reduces one batch, then writes its U x MT outputs.
+template <int MT, int U, int SPW, bool ZU8>
+PMI_DEV void finish_batch(const Batch<U, SPW>& bt, const uint32_t (&xp)[SPW][MT][16],
+                          const float (&sx)[SPW][MT], float* __restrict__ red,
+                          f16* __restrict__ y, int lane, int wave, int wr, int slice_waves,
+                          int row_waves, int batch_row0, int row_lim, int N) {
+  constexpr int V = U * MT;
+  constexpr int VP = Pow2Ceil<V>::value;
+  constexpr int LOGV = Log2<VP>::value;
   float v[VP];
 #pragma unroll
   for (int i = 0; i < VP; ++i) v[i] = 0.f;
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int u = 0; u < U; ++u) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) v[r * MT + m] = acc[r][m];
+    for (int sp = 0; sp < SPW; ++sp) {
+      float p[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) p[m] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t wd = bt.w[sp][u][i];
+        const uint32_t w4 = wd >> 4;
+        // (lo0,lo2) (lo1,lo3) (hi0,hi2) (hi1,hi3) as fp16 subnormals q * 2^-24
+        const f16x2 h0 = as_f16x2(wd & 0x000F000Fu);
+        const f16x2 h1 = as_f16x2((wd >> 8) & 0x000F000Fu);
+        const f16x2 h2 = as_f16x2(w4 & 0x000F000Fu);
+        const f16x2 h3 = as_f16x2((w4 >> 8) & 0x000F000Fu);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          p[m] = dot2_acc(h0, xp[sp][m][4 * i + 0], p[m]);
+          p[m] = dot2_acc(h1, xp[sp][m][4 * i + 1], p[m]);
+          p[m] = dot2_acc(h2, xp[sp][m][4 * i + 2], p[m]);
+          p[m] = dot2_acc(h3, xp[sp][m][4 * i + 3], p[m]);
+        }
+      }
+      const float sc = bt.s[sp][u];
+      const float s24 = sc * 16777216.0f;               // s * 2^24, exact
+      const float sz = -sc * zero_value<ZU8>(bt.z[sp][u]);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        v[u * MT + m] = fmaf(p[m], s24, v[u * MT + m]);
+        v[u * MT + m] = fmaf(sz, sx[sp][m], v[u * MT + m]);
+      }
+    }
+  }
   wave_transpose_reduce<VP>(v, lane);
 
   const int idx = LOGV == 0 ? 0 : (lane >> (6 - LOGV));
   const bool writer = (lane & ((64 >> LOGV) - 1)) == 0 && idx < V;
   if (slice_waves == 1) {
     if (writer) {
-      const int r = idx / MT, m = idx - (idx / MT) * MT;
-      const int n = n0 + r;
-      if (n < N) y[(int64_t)m * N + n] = (f16)v[0];
+      const int u = idx / MT, m = idx - (idx / MT) * MT;
+      const int n = batch_row0 + wr * U + u;
+      if (n < row_lim) y[(int64_t)m * N + n] = f32_to_f16_rne(v[0]);
     }
     return;
   }
-  if (writer) red[(wr * slice_waves + ws) * V + idx] = v[0];
+  if (writer) red[wave * V + idx] = v[0];
   __syncthreads();
   for (int e = threadIdx.x; e < row_waves * V; e += blockDim.x) {
     const int wr2 = e / V, id2 = e - (e / V) * V;
     float s = 0.f;
     for (int q = 0; q < slice_waves; ++q) s += red[(wr2 * slice_waves + q) * V + id2];
-    const int r = id2 / MT, m = id2 - (id2 / MT) * MT;
-    const int n = (blockIdx.x * row_waves + wr2) * R + r;
-    if (n < N) y[(int64_t)m * N + n] = (f16)s;
+    const int u = id2 / MT, m = id2 - (id2 / MT) * MT;
+    const int n = batch_row0 + wr2 * U + u;
+    if (n < row_lim) y[(int64_t)m * N + n] = f32_to_f16_rne(s);
   }
 }
 
-template <int MT, int R>
-hipError_t launch_mt_r(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
-                       const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                       int gs, hipStream_t stream) {
+template <int MT, int U, int SPW, bool PERM, bool ZU8>
+__global__ void __launch_bounds__(kMaxWaves * 64)
+w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+                  const float* __restrict__ scales, const void* __restrict__ zeros,
+                  const int32_t* __restrict__ perm, f16* __restrict__ y, int N, int K, int gs,
+                  int n_slices, int slice_waves, int row_waves, int rows_per_wg) {
+  constexpr int VP = Pow2Ceil<U * MT>::value;
+  // Double-buffered by batch parity: one barrier per batch suffices, because
+  // a wave cannot rewrite a buffer before every wave has passed the barrier
+  // of the batch in between.
+  __shared__ float red[2][kMaxWaves * VP];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ws = wave % slice_waves;
+  const int wr = wave / slice_waves;
+  const int row_chunks = K >> 5;
+  const int hgs = gs >> 1;  // bytes per group tile
+  const int G = K / gs;
+  const int row_bytes = K >> 1;
+  const int row0 = blockIdx.x * rows_per_wg;
+  const int row_lim = min(N, row0 + rows_per_wg);
+  const int stride = row_waves * U;
+  const int n_batches = (rows_per_wg + stride - 1) / stride;
+
+  Rsrc rs;
+  rs.w = make_rsrc(w, (uint32_t)N * (uint32_t)row_bytes);
+  rs.s = make_rsrc(scales, (uint32_t)N * (uint32_t)G * 4u);
+  rs.z = make_rsrc(zeros, (uint32_t)N * (uint32_t)G * (ZU8 ? 1u : 4u));
+
+  // Issue order matters: activation loads, then the first weight batch, and
+  // only then wait for the activations, so the HBM stream starts at once.
+  // sched_barrier keeps the scheduler from sinking loads below the waits.
+  int boff[SPW], grp[SPW];
+  bool act[SPW];
+  uint32_t xa[SPW][MT][8], xb[SPW][MT][8];
+#pragma unroll
+  for (int sp = 0; sp < SPW; ++sp) {
+    const int s = ws + sp * slice_waves;
+    const int chunk = s * kSliceChunks + lane;
+    act[sp] = s < n_slices && chunk < row_chunks;
+    const int b = act[sp] ? chunk << 4 : 0;
+    const int t = b / hgs;
+    const int j = b - t * hgs;
+    boff[sp] = b;
+    grp[sp] = t;
+    const int k_lo = t * gs + j;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      load_x_raw<PERM>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
+  }
+
+  Batch<U, SPW> a, b;
+  const int my_row0 = row0 + wr * U;
+  const int row_last = row_lim - 1;
+  load_batch<U, SPW, ZU8>(a, rs, my_row0, row_last, row_bytes, G, boff, grp);
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t xp[SPW][MT][16];
+  float sx[SPW][MT];
+#pragma unroll
+  for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      pair_x(xa[sp][m], xb[sp][m], xp[sp][m]);
+      if (!act[sp]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xp[sp][m][i] = 0u;
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc = dot2_acc(as_f16x2(0x3C003C00u), xp[sp][m][i], acc);
+      sx[sp][m] = acc;  // sum of the lane's 32 activations
+    }
+
+  // Steady state: batch i+1 loads while batch i computes. The tail is
+  // peeled so that every path issues a fixed number of loads (static
+  // vmcnt waits) and no load past the last batch is made.
+  int i = 0;
+  for (; i + 2 < n_batches; i += 2) {
+    load_batch<U, SPW, ZU8>(b, rs, my_row0 + (i + 1) * stride, row_last, row_bytes, G, boff, grp);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_batch<MT, U, SPW, ZU8>(a, xp, sx, red[0], y, lane, wave, wr, slice_waves, row_waves,
+                                  row0 + i * stride, row_lim, N);
+    load_batch<U, SPW, ZU8>(a, rs, my_row0 + (i + 2) * stride, row_last, row_bytes, G, boff, grp);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_batch<MT, U, SPW, ZU8>(b, xp, sx, red[1], y, lane, wave, wr, slice_waves, row_waves,
+                                  row0 + (i + 1) * stride, row_lim, N);
+  }
+  if (i + 1 < n_batches) {
+    load_batch<U, SPW, ZU8>(b, rs, my_row0 + (i + 1) * stride, row_last, row_bytes, G, boff, grp);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_batch<MT, U, SPW, ZU8>(a, xp, sx, red[0], y, lane, wave, wr, slice_waves, row_waves,
+                                  row0 + i * stride, row_lim, N);
+    finish_batch<MT, U, SPW, ZU8>(b, xp, sx, red[1], y, lane, wave, wr, slice_waves, row_waves,
+                                  row0 + (i + 1) * stride, row_lim, N);
+  } else {
+    finish_batch<MT, U, SPW, ZU8>(a, xp, sx, red[0], y, lane, wave, wr, slice_waves, row_waves,
+                                  row0 + i * stride, row_lim, N);
+  }
+}
+
+template <int MT, int U, int SPW, bool ZU8>
+hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
+                      const void* zeros, const int32_t* perm, void* y, int N, int K, int gs,
+                      hipStream_t stream) {
   const dim3 block(64 * c.slice_waves * c.row_waves);
-  const size_t lds = c.slice_waves > 1 ? sizeof(float) * c.row_waves * c.slice_waves * R * MT : 0;
   if (perm)
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MT, R, true>), dim3(c.grid), block, lds, stream,
-                       (const f16*)x, w, scales, zeros, zero_u8, perm, (f16*)y, N, K, gs,
-                       c.n_slices, c.slice_waves, c.row_waves);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, SPW, true, ZU8>), dim3(c.grid), block, 0, stream,
+                       (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,
+                       c.slice_waves, c.row_waves, c.rows_per_wg);
   else
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MT, R, false>), dim3(c.grid), block, lds, stream,
-                       (const f16*)x, w, scales, zeros, zero_u8, perm, (f16*)y, N, K, gs,
-                       c.n_slices, c.slice_waves, c.row_waves);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, SPW, false, ZU8>), dim3(c.grid), block, 0,
+                       stream, (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs,
+                       c.n_slices, c.slice_waves, c.row_waves, c.rows_per_wg);
   return hipGetLastError();
+}
+
+template <int MT, int U, int SPW>
+hipError_t launch_z(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
+                    const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
+                    int gs, hipStream_t stream) {
+  if (zero_u8) return launch_cfg<MT, U, SPW, true>(c, x, w, scales, zeros, perm, y, N, K, gs, stream);
+  return launch_cfg<MT, U, SPW, false>(c, x, w, scales, zeros, perm, y, N, K, gs, stream);
+}
+
+template <int MT, int SPW>
+hipError_t launch_u(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
+                    const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
+                    int gs, hipStream_t stream) {
+  // Register budget: with more than four activation-row slices per lane a
+  // batch of one row is the most that fits without spilling.
+  if constexpr (MT * SPW > 4) {
+    return launch_z<MT, 1, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+  } else {
+    if (c.rows_per_wave <= 2)
+      return launch_z<MT, 2, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+    return launch_z<MT, 4, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+  }
 }
 
 template <int MT>
 hipError_t launch_mt(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
                      int gs, hipStream_t stream) {
-  switch (c.rows_per_wave) {
-    case 1: return launch_mt_r<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-    case 2: return launch_mt_r<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-    case 4: return launch_mt_r<MT, 4>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-    default: return launch_mt_r<MT, 8>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-  }
+  if (c.slices_per_wave == 2)
+    return launch_u<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+  return launch_u<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
 }
 
 int env_int(const char* name, int dflt) {
@@ -244,25 +442,42 @@ int env_int(const char* name, int dflt) {
   return (s && *s) ? atoi(s) : dflt;
 }
 
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
 }  // namespace
 
 GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
-  (void)M;
   GemvConfig c;
   const int64_t row_chunks = K / 32;
   c.n_slices = (int)((row_chunks + kSliceChunks - 1) / kSliceChunks);
-  // At most 8 waves per workgroup (512 threads) so a wave may use 256 VGPRs.
-  c.slice_waves = c.n_slices < 8 ? c.n_slices : 8;
-  c.row_waves = 8 / c.slice_waves;
+  // At most 8 waves per workgroup; more than 8 slices -> two slices per wave.
+  c.slices_per_wave = c.n_slices > kMaxWaves ? 2 : 1;
+  c.slice_waves = (c.n_slices + c.slices_per_wave - 1) / c.slices_per_wave;
+  c.row_waves = kMaxWaves / c.slice_waves;
   // Tuning overrides (benchmark sweeps only).
-  static const int env_r = env_int("PMI_GEMV_R", 0);
+  static const int env_u = env_int("PMI_GEMV_U", 0);
   static const int env_wr = env_int("PMI_GEMV_ROW_WAVES", 0);
-  if (env_wr > 0 && env_wr * c.slice_waves <= 8) c.row_waves = env_wr;
-  int R = 8;
-  while (R > 1 && (N + (int64_t)c.row_waves * R - 1) / ((int64_t)c.row_waves * R) < 512) R /= 2;
-  if (env_r == 1 || env_r == 2 || env_r == 4 || env_r == 8) R = env_r;
-  c.rows_per_wave = R;
-  c.grid = (int)((N + (int64_t)c.row_waves * R - 1) / ((int64_t)c.row_waves * R));
+  static const int env_wpc = env_int("PMI_GEMV_WG_PER_CU", 0);
+  if (env_wr > 0 && env_wr * c.slice_waves <= kMaxWaves) c.row_waves = env_wr;
+  c.rows_per_wave = M * c.slices_per_wave > 4 ? 1 : 4;
+  if (M * c.slices_per_wave <= 4 && (env_u == 2 || env_u == 4)) c.rows_per_wave = env_u;
+  const int64_t target = (int64_t)device_cus() * (env_wpc > 0 ? env_wpc : 2);
+  const int64_t stride = (int64_t)c.row_waves * c.rows_per_wave;
+  int64_t rows = (N + target - 1) / target;
+  if (rows < stride) rows = stride;  // every wave of a workgroup gets rows
+  c.rows_per_wg = (int)rows;
+  c.grid = (int)((N + rows - 1) / rows);
   return c;
 }
 
@@ -270,11 +485,12 @@ hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, con
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream) {
   const GemvConfig c = gemv_config(M, N, K);
+  const int n = (int)N, k = (int)K, g = (int)gs;
   switch (M) {
-    case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, (int)N, (int)K, (int)gs, stream);
-    case 2: return launch_mt<2>(c, x, w, scales, zeros, zero_u8, perm, y, (int)N, (int)K, (int)gs, stream);
-    case 3: return launch_mt<3>(c, x, w, scales, zeros, zero_u8, perm, y, (int)N, (int)K, (int)gs, stream);
-    case 4: return launch_mt<4>(c, x, w, scales, zeros, zero_u8, perm, y, (int)N, (int)K, (int)gs, stream);
+    case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
+    case 2: return launch_mt<2>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
+    case 3: return launch_mt<3>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
+    case 4: return launch_mt<4>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -106,7 +106,7 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, int layout,
     if constexpr (OUT == PMI_F32) {
       ((float*)out)[o] = v;
     } else if constexpr (OUT == PMI_F16) {
-      ((f16*)out)[o] = (f16)v;
+      ((f16*)out)[o] = f32_to_f16_rne(v);
     } else {
       ((uint16_t*)out)[o] = f32_to_bf16_rne(v);
     }

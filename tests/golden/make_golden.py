@@ -34,6 +34,15 @@ sym_unsigned_quirk sym=True on the unsigned grid (scale.py:73-82): scale =
                    value quantises to 0 (functional.py:70-74 clamps at qmin = 0).
 dequant_pow2       (q - z) * s with s = 0.5, z = 8 (functional.py:91): q = 0 -> -4.0,
                    q = 15 -> 3.5, q = 8 -> 0.0, q = 3 -> -2.5; exact in fp32 and fp16.
+dequant_f16_ties   scales s (given as fp32 bit patterns) and d = q - z for which
+                   the fp32 product s * d is exactly half-way between two fp16
+                   values while the exact product is not. The reference computes
+                   the product in fp32 and then casts (linear.py:129), i.e. rounds
+                   twice: "w16" is numpy's round-to-nearest-even fp16 of the fp32
+                   product; "single" is the fp16 of the exact product (one
+                   rounding), which a fused multiply-convert would produce
+                   instead. Found by a seeded random search over s in
+                   [0.001, 0.01]; listed literally.
 """
 
 from __future__ import annotations
@@ -73,6 +82,14 @@ def main() -> None:
                                "scale": 0.2, "zero": 0.0, "q_head": [0, 0, 0, 15]},
         "dequant_pow2": {"q": [[0, 15, 8, 3]], "scale": 0.5, "zero": 8.0,
                          "w": [[-4.0, 3.5, 0.0, -2.5]]},
+        "dequant_f16_ties": [
+            {"scale_bits": 994753468, "d": 15, "w16": 10736, "single": 10737},
+            {"scale_bits": 995537211, "d": 13, "w16": 10612, "single": 10611},
+            {"scale_bits": 1006722526, "d": 15, "w16": 12180, "single": 12181},
+            {"scale_bits": 1007874867, "d": 5, "w16": 10686, "single": 10685},
+            {"scale_bits": 1007874867, "d": 10, "w16": 11710, "single": 11709},
+            {"scale_bits": 1008682780, "d": 9, "w16": 11674, "single": 11673},
+        ],
     }
     OUT.write_text(json.dumps(kat, indent=1))
     print(f"wrote {OUT}")

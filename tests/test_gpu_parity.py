@@ -186,16 +186,34 @@ def test_dequant_bitexact(layout, gs):
 
 def test_dequant_pow2_golden():
     k = KAT["dequant_pow2"]
-    packed = O.pack_int4(np.array(k["q"], dtype=np.int32))
-    N, K = 1, 4
-    # one group of 4 columns is below the 32-column kernel tiling, so pad K to 128
+    # pad the 4 golden columns to one 128-column group
     q = np.zeros((1, 128), dtype=np.int32)
-    q[0, :4] = k["q"]
+    q[0, :4] = k["q"][0]
     packed = O.pack_int4(q)
     s = np.full((1, 1, 1), k["scale"], dtype=np.float32)
     z = np.full((1, 1, 1), k["zero"], dtype=np.float32)
     got = P.dequantize_int4(_cuda(packed), _cuda(s), _cuda(z), 128, dtype=torch.float16)
     assert got.float().cpu().numpy()[0, :4].tolist() == k["w"][0]
+
+
+@pytest.mark.parametrize("layout", ["storage", "kernel"])
+def test_dequant_f16_double_rounding_ties(layout):
+    """fp32 product then fp16 cast (two roundings), not one fused rounding."""
+    cases = KAT["dequant_f16_ties"]
+    n = len(cases)
+    q = np.zeros((2 * n, 128), dtype=np.int32)
+    s = np.zeros((2 * n, 1, 1), dtype=np.float32)
+    z = np.zeros((2 * n, 1, 1), dtype=np.float32)
+    want = np.zeros(2 * n, dtype=np.uint16)
+    for i, c in enumerate(cases):
+        sv = np.array([c["scale_bits"]], dtype=np.uint32).view(np.float32)[0]
+        q[2 * i, 0], s[2 * i], z[2 * i], want[2 * i] = c["d"], sv, 0, c["w16"]
+        q[2 * i + 1, 0], s[2 * i + 1], z[2 * i + 1] = 15 - c["d"], sv, 15
+        want[2 * i + 1] = c["w16"] | 0x8000
+    packed = O.pack_int4(q)
+    src = _cuda(packed) if layout == "storage" else P.repack_int4_for_kernel(_cuda(packed), 128)
+    got = P.dequantize_int4(src, _cuda(s), _cuda(z), 128, dtype=torch.float16, layout=layout)
+    assert (got.cpu().numpy()[:, 0].view(np.uint16) == want).all()
 
 
 def test_dequant_gidx_bitexact():

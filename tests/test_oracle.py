@@ -212,6 +212,19 @@ class TestDequant:
         assert got.tolist() == k["w"]
         assert got.astype(np.float16).astype(np.float32).tolist() == k["w"]
 
+    def test_f16_double_rounding_ties(self):
+        # each case: one group whose first column dequantises to +s*d (q=d, z=0)
+        # and a second row to -s*d (q=15-d, z=15)
+        for c in KAT["dequant_f16_ties"]:
+            s_ = np.array([c["scale_bits"]], dtype=np.uint32).view(np.float32).reshape(1, 1, 1)
+            q = np.zeros((1, 128), dtype=np.int32)
+            q[0, 0] = c["d"]
+            w = O.dequantize_tensor(q, s_, np.zeros((1, 1, 1), np.float32)).reshape(-1)[0]
+            assert int(np.float16(w).view(np.uint16)) == c["w16"]
+            q[0, 0] = 15 - c["d"]
+            w = O.dequantize_tensor(q, s_, np.full((1, 1, 1), 15, np.float32)).reshape(-1)[0]
+            assert int(np.float16(w).view(np.uint16)) == c["w16"] | 0x8000
+
     def test_sub_then_mul_not_fma(self):
         # (q - z) * s has one rounding (the subtraction is exact); q*s - z*s
         # rounds twice and differs for s = 0.1f, q = 3, z = 7: pins the order.
