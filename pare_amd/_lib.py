@@ -42,6 +42,7 @@ SIGNATURES = {
     "pmi_dequant_w4a16": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _vp]),
     "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),
     "pmi_matmul_kernel_choice": (_i, [_i64, _i64, _i64, _i64]),
+    "pmi_set_kernel_override": (_i, [_i]),
 }
 
 _lock = threading.Lock()

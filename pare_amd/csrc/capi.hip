@@ -6,11 +6,14 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "pmi_launch.h"
 
 namespace {
 
 thread_local char g_err[512] = "";
+std::atomic<int> g_kernel_override{0};
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -43,7 +46,7 @@ int check_shape(int64_t N, int64_t K, int64_t gs, const char* fn) {
   if (gs % 32 != 0)
     return fail(PMI_ERR_UNSUPPORTED, "%s: group_size=%lld must be a multiple of 32", fn,
                 (long long)gs);
-  if (K > (1ll << 30) || N > (1ll << 31) - 1)
+  if (K > (1ll << 30) || N > (1ll << 31) - 1 || N * (K / 2) >= (1ll << 31))
     return fail(PMI_ERR_UNSUPPORTED, "%s: shape too large (N=%lld K=%lld)", fn, (long long)N,
                 (long long)K);
   return PMI_OK;
@@ -100,10 +103,18 @@ int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count, i
                   fn);
 }
 
+int pmi_set_kernel_override(int kernel) {
+  if (kernel < 0 || kernel > 3)
+    return fail(PMI_ERR_INVALID, "pmi_set_kernel_override: unknown kernel %d", kernel);
+  ok();
+  return g_kernel_override.exchange(kernel);
+}
+
 int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size) {
-  (void)N;
-  (void)K;
+  const int forced = g_kernel_override.load();
+  if (forced) return forced;
   if (M <= 4) return 1;
+  if (pmi::skinny_supported(M, N, K, group_size)) return 3;
   return group_size % 128 == 0 ? 2 : 1;
 }
 
@@ -131,7 +142,16 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
 
   hipStream_t s = (hipStream_t)stream;
   const int zu8 = zero_dtype == PMI_U8;
-  if (pmi_matmul_kernel_choice(M, N, K, group_size) == 2)
+  const int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
+  if (choice == 3 && !pmi::skinny_supported(M, N, K, group_size))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: forced skinny kernel needs M <= 16, group_size %% 128 "
+                "== 0 and the activations within 64 KiB of LDS", fn);
+  if (choice == 2 && group_size % 128 != 0)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: forced MFMA GEMM needs group_size %% 128 == 0", fn);
+  if (choice == 3)
+    return from_hip(pmi::launch_skinny(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s),
+                    fn);
+  if (choice == 2)
     return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s), fn);
   // GEMV, four activation rows per launch.
   const uint16_t* xp = (const uint16_t*)x;

@@ -24,7 +24,21 @@ struct GemmConfig {
   int grid_m;
 };
 
+struct SkinnyConfig {
+  int k_waves;         // waves of a workgroup splitting the K groups
+  int n_waves;         // waves of a workgroup taking different weight tiles
+  int tiles_per_wave;  // 16-row weight tiles per wave (NB)
+  int grid;            // workgroups
+  size_t lds;          // dynamic LDS bytes
+};
+
 GemvConfig gemv_config(int64_t M, int64_t N, int64_t K);
+bool skinny_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
+SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
+
+hipError_t launch_skinny(const void* x, const uint8_t* w, const float* scales, const void* zeros,
+                         int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
+                         int64_t K, int64_t gs, hipStream_t stream);
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K);
 
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,

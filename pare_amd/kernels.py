@@ -4,8 +4,10 @@ Mirrors pare/kernels/matmul_int4.py:183-248 (``matmul_w4a16``,
 ``triton_available``) with the Triton kernel replaced by hand-written HIP
 kernels for gfx950 behind libpare_amd.so:
   - M <= 4: split-K GEMV (w4a16_gemv.hip), HBM-bandwidth bound;
-  - M > 4 : MFMA GEMM (w4a16_gemm.hip) for group sizes that are multiples of
-    128, otherwise the GEMV four activation rows at a time.
+  - M <= 16 with the activations within 64 KiB of LDS and group size % 128 == 0:
+    the skinny MFMA kernel (w4a16_skinny.hip);
+  - otherwise: MFMA GEMM (w4a16_gemm.hip) for group sizes that are multiples
+    of 128, or the GEMV four activation rows at a time.
 There is no CPU or PyTorch fallback: every call runs the HIP library or raises.
 """
 
@@ -155,6 +157,27 @@ def matmul_w4a16(
     return out
 
 
+_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3}
+
+
+class force_kernel:
+    """Context manager pinning matmul_w4a16 to one kernel ('gemv', 'gemm',
+    'skinny'; 'auto' for the automatic choice) — for tests and benchmarks."""
+
+    def __init__(self, name: str):
+        self.id = _KERNEL_IDS[name]
+        self.prev = 0
+
+    def __enter__(self):
+        self.prev = _lib.lib().pmi_set_kernel_override(self.id)
+        return self
+
+    def __exit__(self, *exc):
+        _lib.lib().pmi_set_kernel_override(self.prev)
+        return False
+
+
 def kernel_choice(M: int, N: int, K: int, group_size: int) -> str:
-    """'gemv' or 'gemm': the kernel matmul_w4a16 runs for this shape."""
-    return "gemm" if _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size) == 2 else "gemv"
+    """'gemv', 'gemm' or 'skinny': the kernel matmul_w4a16 runs for this shape."""
+    c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size)
+    return {1: "gemv", 2: "gemm", 3: "skinny"}[c]

@@ -48,11 +48,32 @@ def test_version(L):
 
 
 def test_kernel_choice(L):
+    # GEMV for M <= 4; skinny MFMA kernel up to M = 16 while the activations fit the LDS budget
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
     assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128) == 1
-    assert L.pmi_matmul_kernel_choice(16, 4096, 4096, 128) == 2
+    assert L.pmi_matmul_kernel_choice(8, 4096, 3072, 128) == 3
+    assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128) == 2   # 64.1 KiB of padded activations
+    assert L.pmi_matmul_kernel_choice(8, 4096, 18944, 128) == 2   # 296 KiB of activations
+    assert L.pmi_matmul_kernel_choice(16, 4096, 4096, 128) == 2   # 128 KiB of activations
+    assert L.pmi_matmul_kernel_choice(4, 4096, 14336, 128) == 1   # GEMV
+    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 64) == 1     # group size not % 128
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1
+
+
+def test_kernel_override(L):
+    try:
+        assert L.pmi_set_kernel_override(1) == 0
+        assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
+        assert L.pmi_set_kernel_override(7) == _lib.PMI_ERR_INVALID
+        assert "unknown kernel" in _lib.last_error()
+        assert L.pmi_set_kernel_override(3) == 1
+        # forced skinny on a shape it cannot run: rejected before any launch
+        assert _mm(L, M=32, N=256, K=256) == _lib.PMI_ERR_UNSUPPORTED
+        assert "skinny" in _lib.last_error()
+    finally:
+        L.pmi_set_kernel_override(0)
+    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
 
 
 FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid calls

@@ -21,6 +21,9 @@ import torch
 
 import pare_amd as P
 from oracle import pare_oracle as O
+from pare_amd.kernels import force_kernel
+
+
 
 pytestmark = pytest.mark.gpu
 
@@ -60,17 +63,20 @@ def _check_out(y_gpu, y_ref, what):
     assert (err <= bound).all(), f"{what}: max_abs={err.max():.4e}"
 
 
-def _matmul_case(M, N, K, gs, seed, zero_u8=False):
+def _matmul_case(M, N, K, gs, seed, zero_u8=False, kernel="auto"):
     packed, s, z = _layer(N, K, gs, seed)
     x = _x(M, K, seed + 1000)
     w_k = P.repack_int4_for_kernel(_cuda(packed), gs)
     zz = _cuda(z)
     if zero_u8:
         zz = P.zeros_to_u8(zz)
-    y = P.matmul_w4a16(x.to(DEV), w_k, _cuda(s), zz, gs)
+    with force_kernel(kernel):
+        name = P.kernel_choice(M, N, K, gs)
+        print(f"[case] M={M} N={N} K={K} gs={gs} u8={zero_u8} kernel={name}", flush=True)
+        y = P.matmul_w4a16(x.to(DEV), w_k, _cuda(s), zz, gs)
     torch.cuda.synchronize()
     ref = O.linear_fp32(x.float().numpy(), O.dequantize_packed(packed, s, z))
-    _check_out(y, ref, f"M={M} N={N} K={K} gs={gs} u8={zero_u8} kernel={P.kernel_choice(M, N, K, gs)}")
+    _check_out(y, ref, f"M={M} N={N} K={K} gs={gs} u8={zero_u8} kernel={name}")
 
 
 def test_device_is_supported():
@@ -267,6 +273,30 @@ def test_matmul_group_sizes(gs, M):
     _matmul_case(M, 272, K, K if gs == "channel" else gs, 7 * M)
 
 
+# Every kernel on the shapes it supports, forced explicitly (the automatic
+# choice sends most small-M shapes to the skinny kernel).
+KERNEL_CASES = [
+    ("gemv", 1, 4096, 4096, 128), ("gemv", 3, 520, 3584, 128), ("gemv", 4, 96, 18944, 128),
+    ("gemv", 2, 272, 1024, 64), ("gemv", 6, 300, 2048, 128),
+    ("skinny", 1, 4096, 4096, 128), ("skinny", 2, 1040, 1024, 128), ("skinny", 4, 520, 3584, 128),
+    ("skinny", 5, 272, 2048, 256), ("skinny", 13, 400, 1024, 128), ("skinny", 16, 272, 1024, 128),
+    ("skinny", 1, 200, 18944, 128), ("skinny", 1, 1024, 14336, 128), ("skinny", 3, 64, 512, 512),
+    ("gemm", 5, 1040, 1024, 128), ("gemm", 16, 4096, 4096, 128), ("gemm", 64, 520, 3584, 128),
+    ("gemm", 17, 272, 2048, 256),
+]
+
+
+@pytest.mark.parametrize("kernel,M,N,K,gs", KERNEL_CASES)
+def test_each_kernel(kernel, M, N, K, gs):
+    _matmul_case(M, N, K, gs, M * 131 + N + K, kernel=kernel)
+
+
+@pytest.mark.parametrize("kernel", ["gemv", "skinny"])
+@pytest.mark.parametrize("M", [1, 4])
+def test_each_kernel_u8_zeros(kernel, M):
+    _matmul_case(M, 1024, 4096, 128, 77 + M, zero_u8=True, kernel=kernel)
+
+
 @pytest.mark.parametrize("M", [1, 2, 16, 64])
 def test_matmul_u8_zeros(M):
     _matmul_case(M, 512, 2048, 128, 3 + M, zero_u8=True)
@@ -281,13 +311,15 @@ def test_zero_input_gives_zero_output():
         assert y.abs().max().item() == 0.0
 
 
-def test_deterministic():
+@pytest.mark.parametrize("kernel", ["auto", "gemv", "gemm", "skinny"])
+def test_deterministic(kernel):
     packed, s, z = _layer(4096, 4096, 128, 9)
     w = P.repack_int4_for_kernel(_cuda(packed), 128)
-    for m in (1, 64):
+    for m in ((1, 4) if kernel in ("gemv", "skinny") else (1, 64)):
         x = _x(m, 4096, 10).to(DEV)
-        a = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
-        b = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
+        with force_kernel(kernel):
+            a = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
+            b = P.matmul_w4a16(x, w, _cuda(s), _cuda(z), 128)
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
@@ -320,9 +352,10 @@ def test_matmul_reference_errors():
         P.matmul_w4a16(_x(2, 512, 1).to(DEV)[:, ::2], w, _cuda(s), _cuda(z), 128)
 
 
+@pytest.mark.parametrize("kernel", ["auto", "gemv"])
 @pytest.mark.parametrize("M", [1, 16])
 @pytest.mark.parametrize("N,K", [(512, 3584), (3584, 3584), (200, 18944)])
-def test_matmul_act_order(M, N, K):
+def test_matmul_act_order(M, N, K, kernel):
     """Qwen2.5-7B-style act_order: g_idx from a seeded permutation."""
     gs = 128
     rng = np.random.default_rng(N + K)
@@ -332,9 +365,11 @@ def test_matmul_act_order(M, N, K):
     x = _x(M, K, 5)
     pm = P.perm_from_g_idx(_cuda(g), gs)
     wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
-    y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), _cuda(z), gs, perm=pm)
+    with force_kernel(kernel):
+        name = P.kernel_choice(M, N, K, gs)
+        y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), _cuda(z), gs, perm=pm)
     ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
-    _check_out(y, ref, f"act_order M={M} N={N} K={K}")
+    _check_out(y, ref, f"act_order M={M} N={N} K={K} kernel={name}")
 
 
 # ---------------------------------------------------------------------------
