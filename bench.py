@@ -69,12 +69,16 @@ class Layer:
         del packed, scale, zero
 
 
+WORKSPACE = []  # one zero-filled scratch buffer shared by every (stream-ordered) launch
+
+
 def launch(L, lay, x, y, M, stream):
     from pare_amd import _lib
 
+    ws = WORKSPACE[0]
     rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, lay.w.data_ptr(), lay.s.data_ptr(),
                             lay.z.data_ptr(), _lib.PMI_U8, None, y.data_ptr(), _lib.PMI_F16,
-                            M, lay.N, lay.K, GS, stream)
+                            M, lay.N, lay.K, GS, ws.data_ptr(), ws.numel(), stream)
     if rc != 0:
         raise RuntimeError(_lib.last_error())
 
@@ -176,6 +180,10 @@ def main():
         torch.cuda.synchronize()
         log("copy: 10 x 256 MiB")
         return
+
+    ws_bytes = max(L.pmi_matmul_workspace_bytes(M, N, K, GS, 0)
+                   for M in (1, 2, 4, 8, 16, 32, 64, 128) for _, N, K in LLAMA)
+    WORKSPACE.append(torch.zeros(max(ws_bytes, 1 << 20), dtype=torch.uint8, device=dev))
 
     n_layers = args.layers
     t0 = time.time()

@@ -92,13 +92,26 @@ PMI_API int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_
  * zeros: PMI_F32 or PMI_U8 [N,G]; perm (nullable, int32 [K]): act_order
  * gather, X is read as X[:, perm[j]] for weight column j (w must then be
  * repacked with the same perm); y: fp16 [M,N].
+ * workspace (nullable when workspace_bytes == 0): device scratch of
+ * pmi_matmul_workspace_bytes() bytes, 256-byte aligned, zero-filled before
+ * its first use; every call leaves it zero-filled again (it holds split-K
+ * counters, partial tiles and the act_order gather of X). A smaller or null
+ * workspace is accepted: the GEMM then runs without split-K, and act_order
+ * shapes fall back to the GEMV. Calls that may run concurrently (other
+ * streams) must not share a workspace.
  * Requires K % group_size == 0, group_size % 32 == 0, K % 32 == 0.
  * Replaces: matmul_w4a16(x, packed_weight, scales, zeros, group_size)
  *           pare/kernels/matmul_int4.py:183-243 (kernel :66-176) */
 PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_dtype, const int32_t* perm, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
-                     void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes pmi_matmul_w4a16 uses at full speed for this shape (0 when
+ * the chosen kernel needs none). Host-only. No reference counterpart: the
+ * Triton kernel allocates nothing besides Y (pare/kernels/matmul_int4.py:230). */
+PMI_API size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                  int has_perm);
 
 /* Full dequantised weight W_hat[N,K] in the original column order, cast to
  * out_dtype (PMI_F16 / PMI_BF16 with round-to-nearest-even, or PMI_F32).

@@ -35,6 +35,9 @@ HIPCC_FLAGS = [
     # v_fma_mixlo_f16 (a single rounding) where the reference rounds to fp32
     # first and then to fp16. Wanted fusions are written as fmaf().
     "-ffp-contract=off",
+    # MFMA results in ordinary VGPRs: the accumulators feed VALU every group,
+    # and AGPR operands would cost one v_accvgpr_read per value.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

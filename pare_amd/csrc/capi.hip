@@ -118,10 +118,17 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   return group_size % 128 == 0 ? 2 : 1;
 }
 
+size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                  int has_perm) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
+  if (pmi_matmul_kernel_choice(M, N, K, group_size) != 2 || group_size % 128 != 0) return 0;
+  return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
+}
+
 int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_dtype, const int32_t* perm, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
-                     void* stream) {
+                     void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "pmi_matmul_w4a16";
   if (int rc = check_shape(N, K, group_size, fn)) return rc;
   if (int rc = check_zero_dtype(zero_dtype, fn)) return rc;
@@ -139,10 +146,23 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     return fail(PMI_ERR_INVALID, "%s: fp32 zeros must be 4-byte aligned", fn);
   if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
   if (perm && !aligned(perm, 4)) return fail(PMI_ERR_INVALID, "%s: perm must be 4-byte aligned", fn);
+  if (workspace_bytes && (!workspace || !aligned(workspace, 256)))
+    return fail(PMI_ERR_INVALID, "%s: workspace must be non-null and 256-byte aligned", fn);
 
   hipStream_t s = (hipStream_t)stream;
   const int zu8 = zero_dtype == PMI_U8;
-  const int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
+  const int forced = g_kernel_override.load();
+  int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
+  // act_order on the GEMM gathers X[:, perm] into the workspace; without one
+  // the automatic choice falls back to the GEMV.
+  const bool perm_fits = !perm || group_size % 128 != 0 ||
+                         workspace_bytes >= pmi::gemm_workspace_bytes(M, N, K, group_size, true) -
+                                                pmi::gemm_config(M, N, K, group_size, true).ws_split;
+  if (choice == 2 && !perm_fits) {
+    if (forced) return fail(PMI_ERR_UNSUPPORTED, "%s: forced MFMA GEMM with perm needs a workspace "
+                            "of pmi_matmul_workspace_bytes() bytes", fn);
+    choice = 1;
+  }
   if (choice == 3 && !pmi::skinny_supported(M, N, K, group_size))
     return fail(PMI_ERR_UNSUPPORTED, "%s: forced skinny kernel needs M <= 16, group_size %% 128 "
                 "== 0 and the activations within 64 KiB of LDS", fn);
@@ -152,7 +172,8 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     return from_hip(pmi::launch_skinny(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s),
                     fn);
   if (choice == 2)
-    return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s), fn);
+    return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size,
+                                     workspace, workspace_bytes, s), fn);
   // GEMV, four activation rows per launch.
   const uint16_t* xp = (const uint16_t*)x;
   uint16_t* yp = (uint16_t*)y;

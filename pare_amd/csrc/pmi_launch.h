@@ -18,10 +18,13 @@ struct GemvConfig {
 };
 
 struct GemmConfig {
-  int m_tiles;  // 16-row MFMA tiles per workgroup (1, 2 or 4)
-  int n_tiles;  // 16-row weight tiles per wave (1 or 2)
-  int grid_n;
-  int grid_m;
+  int m_tiles;      // 16-row MFMA activation tiles per workgroup (1, 2 or 4)
+  int n_tiles;      // 128-row weight tiles
+  int grid_m;       // activation row blocks of 16 * m_tiles
+  int splits;       // workgroups sharing one tile's K range
+  int grid;         // workgroups
+  size_t ws_split;  // workspace bytes for the partial tiles (splits > 1)
+  size_t ws_perm;   // workspace bytes for X[:, perm] (act_order)
 };
 
 struct SkinnyConfig {
@@ -39,15 +42,20 @@ SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
 hipError_t launch_skinny(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                          int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                          int64_t K, int64_t gs, hipStream_t stream);
-GemmConfig gemm_config(int64_t M, int64_t N, int64_t K);
+GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream);
 
+// workspace: zero-filled before first use, left zeroed; may be smaller than
+// gemm_workspace_bytes() (then unsplit) but must hold the counter block and
+// ws_perm when perm is set.
 hipError_t launch_gemm(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
-                       int64_t K, int64_t gs, hipStream_t stream);
+                       int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
+                       hipStream_t stream);
 
 hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,
                          int64_t K, int64_t gs, hipStream_t stream);

@@ -93,6 +93,23 @@ def _validated_zero_tensor(zeros: torch.Tensor) -> tuple[torch.Tensor, int]:
     return z, _lib.PMI_F32
 
 
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    """Zero-filled scratch for the GEMM's split-K counters/partials and the
+    act_order gather, one per (device, stream): launches on one stream are
+    ordered, so they can share it (each call leaves it zero-filled again)."""
+    if nbytes == 0:
+        return None
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def matmul_w4a16(
     x: torch.Tensor,
     packed_weight: torch.Tensor,
@@ -150,10 +167,14 @@ def matmul_w4a16(
         assert out.dtype == torch.float16 and tuple(out.shape) == (M, N) and out.is_contiguous(), \
             "out must be a contiguous [M, N] float16 tensor"
     with _DeviceGuard(dev):
+        stream = _stream_handle(dev)
+        nbytes = L.pmi_matmul_workspace_bytes(M, N, K, group_size, int(perm is not None))
+        ws = _workspace(dev, stream, nbytes)
         _lib.check(L.pmi_matmul_w4a16(
             xa.data_ptr(), _lib.PMI_F16, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
             perm.data_ptr() if perm is not None else None, out.data_ptr(), _lib.PMI_F16,
-            M, N, K, group_size, _stream_handle(dev)), "pmi_matmul_w4a16")
+            M, N, K, group_size, ws.data_ptr() if ws is not None else None,
+            ws.numel() if ws is not None else 0, stream), "pmi_matmul_w4a16")
     return out
 
 

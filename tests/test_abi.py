@@ -81,7 +81,7 @@ FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid
 
 def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.PMI_F32,
         perm=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16):
-    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, y, ydt, M, N, K, gs, None)
+    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, y, ydt, M, N, K, gs, None, 0, None)
 
 
 @pytest.mark.parametrize("kw,code,msg", [

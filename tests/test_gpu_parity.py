@@ -21,6 +21,7 @@ import torch
 
 import pare_amd as P
 from oracle import pare_oracle as O
+from pare_amd import _lib
 from pare_amd.kernels import force_kernel
 
 
@@ -352,7 +353,7 @@ def test_matmul_reference_errors():
         P.matmul_w4a16(_x(2, 512, 1).to(DEV)[:, ::2], w, _cuda(s), _cuda(z), 128)
 
 
-@pytest.mark.parametrize("kernel", ["auto", "gemv"])
+@pytest.mark.parametrize("kernel", ["auto", "gemv", "gemm"])
 @pytest.mark.parametrize("M", [1, 16])
 @pytest.mark.parametrize("N,K", [(512, 3584), (3584, 3584), (200, 18944)])
 def test_matmul_act_order(M, N, K, kernel):
@@ -370,6 +371,49 @@ def test_matmul_act_order(M, N, K, kernel):
         y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), _cuda(z), gs, perm=pm)
     ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
     _check_out(y, ref, f"act_order M={M} N={N} K={K} kernel={name}")
+
+
+def test_gemm_workspace_reused_across_shapes():
+    """One workspace serves split-K GEMMs of different tile counts and act_order
+    gathers in any order; each result matches the oracle and the split-K
+    counter block is zero again after every call."""
+    L = _lib.lib()
+    gs = 128
+    cases = [(64, 14336, 4096, False), (16, 512, 3584, True), (48, 4096, 4096, False),
+             (64, 3584, 3584, True), (17, 1024, 4096, False), (128, 2048, 4096, False)]
+    need = max(L.pmi_matmul_workspace_bytes(M, N, K, gs, int(pm)) for M, N, K, pm in cases)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    for rep in range(2):
+        for i, (M, N, K, use_perm) in enumerate(cases):
+            seed = 50 + i
+            w = _w(N, K, seed)
+            if use_perm:
+                perm_np = np.random.default_rng(seed).permutation(K)
+                packed, s, z, g = O.rtn_quantize_act_order(w, perm_np, gs)
+                pm = P.perm_from_g_idx(_cuda(g), gs)
+                ref_w = O.dequantize_gidx(O.unpack_int4(packed), s, z, g)
+            else:
+                packed, s, z = O.rtn_quantize(w, gs)
+                pm = None
+                ref_w = O.dequantize_packed(packed, s, z)
+            wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+            x = _x(M, K, seed + 1)
+            xd = x.to(DEV)
+            sd = _cuda(s).reshape(N, K // gs).contiguous()
+            zd = P.zeros_to_u8(_cuda(z))
+            y = torch.empty(M, N, dtype=torch.float16, device=DEV)
+            with force_kernel("gemm"):
+                rc = L.pmi_matmul_w4a16(xd.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
+                                        zd.data_ptr(), _lib.PMI_U8,
+                                        pm.data_ptr() if pm is not None else None,
+                                        y.data_ptr(), _lib.PMI_F16, M, N, K, gs, ws.data_ptr(),
+                                        ws.numel(), stream)
+            assert rc == 0, _lib.last_error()
+            torch.cuda.synchronize()
+            assert int(ws[:65536].count_nonzero()) == 0, "split-K counters not reset"
+            _check_out(y, O.linear_fp32(x.float().numpy(), ref_w),
+                       f"shared workspace rep={rep} M={M} N={N} K={K} perm={use_perm}")
 
 
 # ---------------------------------------------------------------------------
