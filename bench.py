@@ -4,16 +4,21 @@
 Workload: the seven linears of a Llama-3.1-8B
 decoder layer at M=1 (q/o 4096->4096, k/v 4096->1024, gate/up 4096->14336,
 down 14336->4096), INT4 g128 asymmetric RTN, fp16 activations ~N(0,1),
-weights ~N(0, 0.02), all seeded. One "step" runs those seven layers for all 32
+weights ~N(0, 0.02), all seeded. One "step" runs those linears for all 32
 decoder layers, each with its own weights (3.5 GB of packed INT4), so every
 call streams its weights from HBM rather than from the 256 MB Infinity Cache.
 The step is captured once in a HIP graph and replayed.
 
+The step runs the layer set as a model does with FusedQuantizedLinear: q/k/v
+as one launch (N=6144) and gate/up as one launch (N=28672), then o and down:
+four launches per decoder layer over exactly the bytes of the seven linears.
+The seven-launch step (one launch per QuantizedLinear) is reported beside it.
+
 Printed JSON line: value = aggregate algorithmic HBM throughput (GB/s) of the
-step; "roofline" is that of the dominant kernel (the gate/up GEMV),
+step; "roofline" is that of the dominant kernel (the fused gate/up GEMV),
 "cpu_baseline" the reference's dequantize-on-the-fly path restated on the
-host CPU (oracle, timed on a bounded sample), "detail" per-layer µs / GB/s and
-the M=64 MFMA GEMM TFLOP/s.
+host CPU (oracle, timed on a bounded sample), "detail" per-shape µs / GB/s, the
+seven-launch step and the M=64 MFMA GEMM TFLOP/s.
 
 Algorithmic bytes per call: N*K/2 (INT4 codes) + N*G*(4 + 1) (fp32 scale +
 u8 zero, the format the kernels read) + M*K*2 (x) + M*N*2 (y); FLOPs 2*M*N*K.
@@ -40,6 +45,7 @@ GS = 128
 N_LAYERS = 32
 LLAMA = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
          ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+FUSED = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
 
 
 def log(*a):
@@ -50,35 +56,61 @@ def layer_bytes(N, K, M, scale_b=4, zero_b=1):
     return N * K // 2 + N * (K // GS) * (scale_b + zero_b) + M * K * 2 + M * N * 2
 
 
-class Layer:
-    """Device buffers of one INT4 linear in the kernels' format."""
+class Buf:
+    """Device buffers of one INT4 launch in the kernels' format: kernel-layout
+    codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]."""
 
-    def __init__(self, name, N, K, seed, dev):
-        import torch
+    def __init__(self, name, w, s, z):
+        self.name, self.w, self.s, self.z = name, w, s, z
+        self.N, self.K = w.shape[0], w.shape[1] * 2
 
-        import pare_amd as P
 
-        self.name, self.N, self.K = name, N, K
-        g = torch.Generator(device=dev).manual_seed(seed)
+def make_decoder_layer(seed, dev):
+    """One decoder layer's seven linears, RTN-quantised on the device, stored as
+    the four fused launches; the seven single-linear buffers are row-block
+    views into them (the same bytes)."""
+    import torch
+
+    import pare_amd as P
+
+    single = {}
+    for i, (name, N, K) in enumerate(LLAMA):
+        g = torch.Generator(device=dev).manual_seed(seed + i)
         w = torch.randn(N, K, generator=g, device=dev) * 0.02
         packed, scale, zero = P.rtn_quantize(w, GS)
         del w
-        self.w = P.repack_int4_for_kernel(packed, GS)
-        self.s = scale.reshape(N, K // GS).contiguous()
-        self.z = P.zeros_to_u8(zero)
-        del packed, scale, zero
+        single[name] = (P.repack_int4_for_kernel(packed, GS), scale.reshape(N, K // GS),
+                        P.zeros_to_u8(zero).reshape(N, K // GS))
+    fused, views = [], {}
+    for fname, parts in FUSED:
+        w = torch.cat([single[p][0] for p in parts]).contiguous()
+        s = torch.cat([single[p][1] for p in parts]).contiguous()
+        z = torch.cat([single[p][2] for p in parts]).contiguous()
+        fused.append(Buf(fname, w, s, z))
+        r0 = 0
+        for p in parts:
+            n = single[p][0].shape[0]
+            views[p] = Buf(p, w[r0:r0 + n], s[r0:r0 + n], z[r0:r0 + n])
+            r0 += n
+    return fused, [views[name] for name, _, _ in LLAMA]
 
 
 WORKSPACE = []  # one zero-filled scratch buffer shared by every (stream-ordered) launch
 
 
-def launch(L, lay, x, y, M, stream):
+M_MAX = 128  # largest activation row count any leg launches
+
+
+def launch(L, buf, x, y, M, stream):
     from pare_amd import _lib
 
+    # the kernels trust their shapes: check them here, before any launch
+    assert x.shape[0] >= M and x.shape[1] == buf.K and x.is_contiguous(), "x too small for M"
+    assert y.shape[0] >= M and y.shape[1] == buf.N and y.is_contiguous(), "y too small for M"
     ws = WORKSPACE[0]
-    rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, lay.w.data_ptr(), lay.s.data_ptr(),
-                            lay.z.data_ptr(), _lib.PMI_U8, None, y.data_ptr(), _lib.PMI_F16,
-                            M, lay.N, lay.K, GS, ws.data_ptr(), ws.numel(), stream)
+    rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, buf.w.data_ptr(), buf.s.data_ptr(),
+                            buf.z.data_ptr(), _lib.PMI_U8, None, y.data_ptr(), _lib.PMI_F16,
+                            M, buf.N, buf.K, GS, ws.data_ptr(), ws.numel(), stream)
     if rc != 0:
         raise RuntimeError(_lib.last_error())
 
@@ -112,7 +144,6 @@ def cpu_baseline(max_threads=16):
     """The reference's dequantize-on-the-fly forward on the host CPU, op for op
     (oracle.dequant_path_forward_torch), on one decoder layer's seven linears at
     M=1: 1 warmup + 3 timed passes per layer, median per layer."""
-    import numpy as np
     import torch
 
     from oracle import pare_oracle as O
@@ -121,7 +152,7 @@ def cpu_baseline(max_threads=16):
     torch.set_num_threads(threads)
     total_bytes, total_s = 0, 0.0
     g = torch.Generator().manual_seed(1234)
-    for i, (name, N, K) in enumerate(LLAMA):
+    for name, N, K in LLAMA:
         w = (torch.randn(N, K, generator=g) * 0.02).numpy()
         packed, s, z = O.rtn_quantize(w, GS)
         tp, ts, tz = torch.from_numpy(packed), torch.from_numpy(s), torch.from_numpy(z)
@@ -150,7 +181,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--kernel-only", choices=["gate_m1", "gate_m64", "copy"], default=None,
+    ap.add_argument("--kernel-only", choices=["gate_up_m1", "gate_m64", "copy"], default=None,
                     help="run only one kernel loop (for rocprofv3 counter passes)")
     ap.add_argument("--sweep", action="store_true", help="also run the gate_proj M sweep")
     args = ap.parse_args()
@@ -181,40 +212,58 @@ def main():
         log("copy: 10 x 256 MiB")
         return
 
+    shapes = [(N, K) for _, N, K in LLAMA] + [(6144, 4096), (28672, 4096)]
     ws_bytes = max(L.pmi_matmul_workspace_bytes(M, N, K, GS, 0)
-                   for M in (1, 2, 4, 8, 16, 32, 64, 128) for _, N, K in LLAMA)
+                   for M in (1, 2, 4, 8, 16, 32, 64, M_MAX) for N, K in shapes)
     WORKSPACE.append(torch.zeros(max(ws_bytes, 1 << 20), dtype=torch.uint8, device=dev))
 
     n_layers = args.layers
     t0 = time.time()
-    layers = [[Layer(name, N, K, 1000 * l + i, dev) for i, (name, N, K) in enumerate(LLAMA)]
-              for l in range(n_layers)]
+    fused, single = [], []
+    for l in range(n_layers):
+        f, s = make_decoder_layer(1000 * l, dev)
+        fused.append(f)
+        single.append(s)
     torch.cuda.synchronize()
-    log(f"setup: {n_layers} layers x 7 linears quantised on device in {time.time() - t0:.1f}s")
+    log(f"setup: {n_layers} decoder layers quantised on device in {time.time() - t0:.1f}s")
 
     g = torch.Generator(device=dev).manual_seed(1)
-    xh = torch.randn(64, 4096, generator=g, device=dev).to(torch.float16)
-    xf = torch.randn(64, 14336, generator=g, device=dev).to(torch.float16)
-    outs = {name: torch.empty(64, N, dtype=torch.float16, device=dev) for name, N, _ in LLAMA}
+    xh = torch.randn(M_MAX, 4096, generator=g, device=dev).to(torch.float16)
+    xf = torch.randn(M_MAX, 14336, generator=g, device=dev).to(torch.float16)
+    outs = {name: torch.empty(M_MAX, N, dtype=torch.float16, device=dev) for name, N, _ in LLAMA}
+    outs.update({"qkv": torch.empty(M_MAX, 6144, dtype=torch.float16, device=dev),
+                 "gate_up": torch.empty(M_MAX, 28672, dtype=torch.float16, device=dev)})
+
+    def run(s, bufs, M=1):
+        for buf in bufs:
+            launch(L, buf, xf if buf.name == "down" else xh, outs[buf.name], M, s)
 
     def step(s, M=1):
-        for lay_set in layers:
-            for lay in lay_set:
-                x = xf if lay.name == "down" else xh
-                launch(L, lay, x, outs[lay.name], M, s)
+        for f in fused:
+            run(s, f, M)
+
+    def step_single(s, M=1):
+        for sgl in single:
+            run(s, sgl, M)
+
+    def gate_up_loop(s, M, passes=2):
+        for _ in range(passes):
+            for f in fused:
+                run(s, [f[2]], M)
 
     def gate_loop(s, M, copies):
         for i in range(copies):
-            lay = layers[i % n_layers][4 + (i // n_layers) % 2]  # gate and up of all layers
-            launch(L, lay, xh, outs["gate"], M, s)
+            run(s, [single[i % n_layers][4 + (i // n_layers) % 2]], M)  # gate and up of all layers
 
-    if args.kernel_only in ("gate_m1", "gate_m64"):
-        M = 1 if args.kernel_only == "gate_m1" else 64
+    if args.kernel_only:
         with torch.cuda.stream(stream):
             for _ in range(5):
-                gate_loop(stream.cuda_stream, M, 2 * n_layers)
+                if args.kernel_only == "gate_up_m1":
+                    gate_up_loop(stream.cuda_stream, 1)
+                else:
+                    gate_loop(stream.cuda_stream, 64, 2 * n_layers)
         torch.cuda.synchronize()
-        log(f"{args.kernel_only}: 5 x {2 * n_layers} launches")
+        log(f"{args.kernel_only}: 5 passes")
         return
 
     # --- eager vs graph: same outputs -------------------------------------
@@ -229,11 +278,11 @@ def main():
         with torch.cuda.stream(stream):
             graph.replay()
         torch.cuda.synchronize()
-        for k in outs:
+        for k in ("qkv", "o", "gate_up", "down"):
             assert torch.equal(outs[k][:1], eager[k]), f"graph replay {rep} differs on {k}"
     log("graph replay == eager outputs")
 
-    # --- timed region: K replays of the decode-layer-set step -------------
+    # --- timed region: K replays of the decode step -------------------------
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
             graph.replay()
@@ -241,15 +290,21 @@ def main():
     ms_step = time_graph(graph, args.steps, stream)
     step_bytes = n_layers * sum(layer_bytes(N, K, 1) for _, N, K in LLAMA)
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"step: {ms_step * 1e3:.1f} us for {n_layers}x7 linears, {value:.1f} GB/s")
+    log(f"step (4 launches/layer): {ms_step * 1e3:.1f} us, {value:.1f} GB/s")
 
-    # --- per-layer shape: graph of back-to-back launches over 32 copies ----
     detail = {}
-    for i, (name, N, K) in enumerate(LLAMA):
-        def one(s, i=i, name=name):
-            for l in range(n_layers):
-                launch(L, layers[l][i], xf if name == "down" else xh, outs[name], 1, s)
-        gi = capture(one, stream)
+    gs1 = capture(step_single, stream)
+    for _ in range(2):
+        gs1.replay()
+    ms_single = time_graph(gs1, max(args.steps // 2, 3), stream)
+    detail["step_7_launches"] = {"ms": round(ms_single, 4),
+                                 "GB/s": round(step_bytes / (ms_single * 1e-3) / 1e9, 1)}
+    log(f"step (7 launches/layer): {ms_single * 1e3:.1f} us")
+    del gs1
+
+    # --- per-shape: graph of back-to-back launches over all layer copies ----
+    def per_shape(name, pick, N, K):
+        gi = capture(lambda s: [run(s, [pick(l)], 1) for l in range(n_layers)], stream)
         for _ in range(2):
             gi.replay()
         us = time_graph(gi, 10, stream) * 1e3 / n_layers
@@ -257,18 +312,27 @@ def main():
         detail[name] = {"N": N, "K": K, "us": round(us, 2), "GB/s": round(gbs, 1),
                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
                         "kernel": P.kernel_choice(1, N, K, GS)}
-        log(f"  {name:5s} {N:6d}x{K:6d} M=1: {us:7.2f} us {gbs:8.1f} GB/s")
+        log(f"  {name:8s} {N:6d}x{K:6d} M=1: {us:7.2f} us {gbs:8.1f} GB/s")
 
-    # --- dominant kernel (gate/up GEMV) for the roofline --------------------
-    copies = 2 * n_layers
-    gg = capture(lambda s: gate_loop(s, 1, copies), stream)
+    for i, (name, N, K) in enumerate(LLAMA):
+        per_shape(name, lambda l, i=i: single[l][i], N, K)
+    per_shape("qkv", lambda l: fused[l][0], 6144, 4096)
+
+    # --- dominant kernel (fused gate/up GEMV) for the roofline --------------
+    gg = capture(lambda s: gate_up_loop(s, 1), stream)
     for _ in range(2):
         gg.replay()
-    gate_us = time_graph(gg, 10, stream) * 1e3 / copies
-    gate_bytes = layer_bytes(14336, 4096, 1)
-    gate_gbs = gate_bytes / (gate_us * 1e-6) / 1e9
+    gu_us = time_graph(gg, 10, stream) * 1e3 / (2 * n_layers)
+    gu_bytes = layer_bytes(28672, 4096, 1)
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    detail["gate_up"] = {"N": 28672, "K": 4096, "us": round(gu_us, 2), "GB/s": round(gu_gbs, 1),
+                         "hbm_frac": round(gu_gbs / HBM_PEAK_GBS, 3),
+                         "kernel": P.kernel_choice(1, 28672, 4096, GS)}
+    log(f"  gate_up  28672x  4096 M=1: {gu_us:7.2f} us {gu_gbs:8.1f} GB/s")
+    del gg
 
     # --- M = 64 MFMA GEMM on gate_proj --------------------------------------
+    copies = 2 * n_layers
     gm = capture(lambda s: gate_loop(s, 64, copies), stream)
     for _ in range(2):
         gm.replay()
@@ -279,10 +343,11 @@ def main():
                           "mfma_frac": round(m64_tflops / MFMA_F16_PEAK_TFLOPS, 4),
                           "GB/s": round(m64_gbs, 1), "kernel": P.kernel_choice(64, 14336, 4096, GS)}
     log(f"  gate M=64: {m64_us:.2f} us {m64_tflops:.1f} TFLOP/s {m64_gbs:.1f} GB/s")
+    del gm
 
     if args.sweep:
         sweep = {}
-        for M in (1, 2, 4, 8, 16, 32, 64, 128):
+        for M in (1, 2, 4, 8, 16, 32, 64, M_MAX):
             gs_ = capture(lambda s, M=M: gate_loop(s, M, copies), stream)
             gs_.replay()
             us = time_graph(gs_, 5, stream) * 1e3 / copies
@@ -291,10 +356,11 @@ def main():
                         "TFLOP/s": round(2 * M * 14336 * 4096 / (us * 1e-6) / 1e12, 2),
                         "kernel": P.kernel_choice(M, 14336, 4096, GS)}
             log(f"  sweep gate M={M:3d}: {sweep[M]}")
+            del gs_
         detail["gate_sweep"] = sweep
 
     traffic = None
-    tfile = ROOT / "profiles" / "traffic_gemv_gate_m1.json"
+    tfile = ROOT / "profiles" / "traffic_gemv_gate_up_m1.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
 
@@ -316,13 +382,14 @@ def main():
         "dtype": "fp16",
         "data": "synthetic (seeded; weights N(0,0.02) RTN INT4 g128 asym, x N(0,1))",
         "config": {"workload": f"Llama-3.1-8B decode linear set at M=1: {n_layers} layers x "
-                               "(q,k,v,o 4096/1024, gate/up 14336, down 14336->4096), INT4 g128",
-                   "M": 1, "group_size": GS, "layers": n_layers,
+                               "(q,k,v 4096->4096/1024/1024 fused; o 4096->4096; gate,up "
+                               "4096->14336 fused; down 14336->4096), INT4 g128",
+                   "M": 1, "group_size": GS, "layers": n_layers, "launches_per_layer": 4,
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "w4a16_gemv (gate/up 4096->14336, M=1)",
-                     "avg_launch_us": round(gate_us, 3), "bytes_per_launch": gate_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "w4a16_gemv (fused gate/up 4096->28672, M=1)",
+                     "avg_launch_us": round(gu_us, 3), "bytes_per_launch": gu_bytes},
         "cpu_baseline": cpu,
         "detail": detail,
     }

@@ -140,3 +140,52 @@ class QuantizedLinear(nn.Module):
         return (f"in={self.in_features}, out={self.out_features}, dtype=INT4, "
                 f"scheme={self.config.scheme}, granularity={self.config.granularity}, "
                 f"use_kernel={getattr(self, 'use_kernel', False)}")
+
+
+class FusedQuantizedLinear(nn.Module):
+    """Several INT4 linears that read the same input (q/k/v, gate/up) run as one
+    kernel launch over their buffers concatenated along out_features.
+
+    Caller-side fusion: the reference launches one kernel per QuantizedLinear
+    (pare/layers/linear.py:140-159). Every output element is the same
+    dot product as in the separate layers; only the launch count changes, which
+    at decode sizes removes a fixed per-launch cost (ramp-up to full memory
+    bandwidth and drain) per merged layer. ``forward`` returns one tensor per
+    fused layer, in order (views of one [..., sum(out_features)] result).
+    """
+
+    def __init__(self, layers, use_kernel: bool = True) -> None:
+        super().__init__()
+        layers = list(layers)
+        if not layers:
+            raise ValueError("FusedQuantizedLinear needs at least one layer")
+        first = layers[0]
+        for lay in layers[1:]:
+            if lay.in_features != first.in_features:
+                raise ValueError("fused layers must share in_features")
+            if lay._group_size() != first._group_size() or lay.config.bits != first.config.bits:
+                raise ValueError("fused layers must share the quantisation group size")
+            same_gidx = (lay.g_idx is None and first.g_idx is None) or (
+                lay.g_idx is not None and first.g_idx is not None and torch.equal(lay.g_idx, first.g_idx))
+            if not same_gidx:
+                raise ValueError("fused layers must share g_idx (act_order permutation)")
+        bias = None
+        if any(lay.bias is not None for lay in layers):
+            dtype = next(lay.bias.dtype for lay in layers if lay.bias is not None)
+            bias = torch.cat([lay.bias.detach() if lay.bias is not None else
+                              torch.zeros(lay.out_features, dtype=dtype, device=lay.packed_weight.device)
+                              for lay in layers])
+        self.split_sizes = [lay.out_features for lay in layers]
+        self.fused = QuantizedLinear(
+            torch.cat([lay.packed_weight for lay in layers]),
+            torch.cat([lay.scale for lay in layers]),
+            torch.cat([lay.zero for lay in layers]),
+            first.config, bias, first.in_features, sum(self.split_sizes), use_kernel=use_kernel,
+            g_idx=first.g_idx)
+
+    @property
+    def in_features(self) -> int:
+        return self.fused.in_features
+
+    def forward(self, x: torch.Tensor):
+        return tuple(torch.split(self.fused(x), self.split_sizes, dim=-1))

@@ -527,6 +527,33 @@ def test_act_order_module():
     _check_out(y, ref, "act_order module")
 
 
+@pytest.mark.parametrize("M", [1, 4, 16, 64])
+def test_fused_linears_match_each_layer(M):
+    """q/k/v-style fusion: one launch over concatenated buffers gives every
+    layer's own output (within tolerance of each layer's oracle), bias included."""
+    K, gs = 512, 128
+    sizes = [256, 64, 96]
+    layers, refs_w, biases = [], [], []
+    for i, N in enumerate(sizes):
+        packed, s, z = _layer(N, K, gs, 70 + i)
+        b = (torch.arange(N, dtype=torch.float32) / N - 0.5) if i != 1 else None
+        layers.append(P.QuantizedLinear(_cuda(packed), _cuda(s), _cuda(z),
+                                        P.QuantConfig(group_size=gs),
+                                        b.to(DEV) if b is not None else None, K, N, use_kernel=True))
+        refs_w.append(O.dequantize_packed(packed, s, z))
+        biases.append(b)
+    fused = P.FusedQuantizedLinear(layers)
+    x = _x(M, K, 9)
+    with torch.no_grad():
+        outs = fused(x.to(DEV))
+    assert [o.shape[-1] for o in outs] == sizes
+    for i, (o, wref, b) in enumerate(zip(outs, refs_w, biases)):
+        ref = O.linear_fp32(x.float().numpy(), wref)
+        if b is not None:
+            ref = ref + b.numpy()
+        _check_out(o.contiguous(), ref, f"fused layer {i} M={M}")
+
+
 # ---------------------------------------------------------------------------
 # BASELINE full sizes
 # ---------------------------------------------------------------------------
