@@ -58,11 +58,20 @@ def layer_bytes(N, K, M, scale_b=4, zero_b=1):
 
 class Buf:
     """Device buffers of one INT4 launch in the kernels' format: kernel-layout
-    codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]."""
+    codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]; for M > 4 also
+    their group-major copies (built on first use, as a module does once)."""
 
     def __init__(self, name, w, s, z):
         self.name, self.w, self.s, self.z = name, w, s, z
         self.N, self.K = w.shape[0], w.shape[1] * 2
+        self._gm = None
+
+    def gm(self):
+        if self._gm is None:
+            import pare_amd as P
+
+            self._gm = P.sz_group_major(self.s.contiguous(), self.z.contiguous())
+        return self._gm
 
 
 def make_decoder_layer(seed, dev):
@@ -108,9 +117,12 @@ def launch(L, buf, x, y, M, stream):
     assert x.shape[0] >= M and x.shape[1] == buf.K and x.is_contiguous(), "x too small for M"
     assert y.shape[0] >= M and y.shape[1] == buf.N and y.is_contiguous(), "y too small for M"
     ws = WORKSPACE[0]
+    s_gm, z_gm = buf.gm() if M > 4 else (None, None)
     rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, buf.w.data_ptr(), buf.s.data_ptr(),
-                            buf.z.data_ptr(), _lib.PMI_U8, None, y.data_ptr(), _lib.PMI_F16,
-                            M, buf.N, buf.K, GS, ws.data_ptr(), ws.numel(), stream)
+                            buf.z.data_ptr(), _lib.PMI_U8, None,
+                            s_gm.data_ptr() if s_gm is not None else None,
+                            z_gm.data_ptr() if z_gm is not None else None, y.data_ptr(),
+                            _lib.PMI_F16, M, buf.N, buf.K, GS, ws.data_ptr(), ws.numel(), stream)
     if rc != 0:
         raise RuntimeError(_lib.last_error())
 

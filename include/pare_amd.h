@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 1
+#define PMI_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -87,11 +87,26 @@ PMI_API int pmi_repack_int4_for_kernel(const uint8_t* packed, uint8_t* out, cons
 PMI_API int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count,
                     int64_t count, void* stream);
 
+/* [N,G] scales (fp32) and zero points (PMI_F32 or PMI_U8) -> group-major
+ * copies scales_gm fp32 [G,N] and zeros_gm u8 [G,N], for pmi_matmul_w4a16.
+ * Zero points must be integers in [0,15]; the number that are not is added
+ * to *bad_count (device int32, nullable) and they are written as 0.
+ * No reference counterpart: a derived, per-layer layout like the kernel-layout
+ * weight of pare/layers/linear.py:148-151 (the reference kernel reads [N,G]
+ * per program, pare/kernels/matmul_int4.py:145-164). */
+PMI_API int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype,
+                               float* scales_gm, uint8_t* zeros_gm, int32_t* bad_count,
+                               int64_t N, int64_t G, void* stream);
+
 /* Y[M,N] = X[M,K] . dequant(W)^T with the dequantisation fused into the
  * matmul. x: fp16 [M,K] row-major, 16-byte aligned; w: kernel layout;
  * zeros: PMI_F32 or PMI_U8 [N,G]; perm (nullable, int32 [K]): act_order
  * gather, X is read as X[:, perm[j]] for weight column j (w must then be
  * repacked with the same perm); y: fp16 [M,N].
+ * scales_gm, zeros_gm (nullable, both or neither): the pmi_sz_group_major
+ * copies of scales and zeros; the MFMA GEMM reads them (one contiguous run per
+ * group) instead of gathering [N,G] rows when N % 4 == 0. The other kernels
+ * read scales and zeros.
  * workspace (nullable when workspace_bytes == 0): device scratch of
  * pmi_matmul_workspace_bytes() bytes, 256-byte aligned, zero-filled before
  * its first use; every call leaves it zero-filled again (it holds split-K
@@ -103,7 +118,8 @@ PMI_API int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_
  * Replaces: matmul_w4a16(x, packed_weight, scales, zeros, group_size)
  *           pare/kernels/matmul_int4.py:183-243 (kernel :66-176) */
 PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
-                     const void* zeros, int zero_dtype, const int32_t* perm, void* y,
+                     const void* zeros, int zero_dtype, const int32_t* perm,
+                     const float* scales_gm, const uint8_t* zeros_gm, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream);
 

@@ -11,11 +11,11 @@ All compute runs in libpare_amd.so (hand-written HIP); there is no CPU fallback.
 from .config import QuantConfig, QuantDtype
 from .kernels import kernel_available, kernel_choice, matmul_w4a16, triton_available
 from .linear import FusedQuantizedLinear, QuantizedLinear
-from .pack import dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, zeros_to_u8
+from .pack import dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major, zeros_to_u8
 from .quant import rtn_quantize
 
 __all__ = [
     "FusedQuantizedLinear", "QuantConfig", "QuantDtype", "QuantizedLinear", "dequantize_int4", "kernel_available",
     "kernel_choice", "matmul_w4a16", "perm_from_g_idx", "repack_int4_for_kernel",
-    "rtn_quantize", "triton_available", "zeros_to_u8",
+    "rtn_quantize", "sz_group_major", "triton_available", "zeros_to_u8",
 ]

@@ -38,8 +38,9 @@ SIGNATURES = {
     "pmi_device_supported": (_i, [_i]),
     "pmi_repack_int4_for_kernel": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "pmi_zeros_to_u8": (_i, [_vp, _vp, _vp, _i64, _vp]),
-    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i64,
-                             _vp, ctypes.c_size_t, _vp]),
+    "pmi_sz_group_major": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i64,
+                             _i64, _vp, ctypes.c_size_t, _vp]),
     "pmi_matmul_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i]),
     "pmi_dequant_w4a16": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _vp]),
     "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),

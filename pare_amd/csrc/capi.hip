@@ -125,8 +125,23 @@ size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
   return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
 }
 
+int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype, float* scales_gm,
+                       uint8_t* zeros_gm, int32_t* bad_count, int64_t N, int64_t G,
+                       void* stream) {
+  const char* fn = "pmi_sz_group_major";
+  if (int rc = check_zero_dtype(zero_dtype, fn)) return rc;
+  if (N < 0 || G <= 0) return fail(PMI_ERR_INVALID, "%s: need N >= 0 and G > 0", fn);
+  if (N * G >= (1ll << 31)) return fail(PMI_ERR_UNSUPPORTED, "%s: N*G too large", fn);
+  if (N == 0) return ok();
+  if (!scales || !zeros || !scales_gm || !zeros_gm) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  return from_hip(pmi::launch_sz_group_major(scales, zeros, zero_dtype == PMI_U8, scales_gm,
+                                             zeros_gm, bad_count, N, G, (hipStream_t)stream),
+                  fn);
+}
+
 int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
-                     const void* zeros, int zero_dtype, const int32_t* perm, void* y,
+                     const void* zeros, int zero_dtype, const int32_t* perm,
+                     const float* scales_gm, const uint8_t* zeros_gm, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "pmi_matmul_w4a16";
@@ -146,6 +161,10 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     return fail(PMI_ERR_INVALID, "%s: fp32 zeros must be 4-byte aligned", fn);
   if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
   if (perm && !aligned(perm, 4)) return fail(PMI_ERR_INVALID, "%s: perm must be 4-byte aligned", fn);
+  if (!scales_gm != !zeros_gm)
+    return fail(PMI_ERR_INVALID, "%s: scales_gm and zeros_gm are given together or not at all", fn);
+  if (scales_gm && (!aligned(scales_gm, 4) || !aligned(zeros_gm, 4)))
+    return fail(PMI_ERR_INVALID, "%s: scales_gm and zeros_gm must be 4-byte aligned", fn);
   if (workspace_bytes && (!workspace || !aligned(workspace, 256)))
     return fail(PMI_ERR_INVALID, "%s: workspace must be non-null and 256-byte aligned", fn);
 
@@ -172,8 +191,8 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     return from_hip(pmi::launch_skinny(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s),
                     fn);
   if (choice == 2)
-    return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size,
-                                     workspace, workspace_bytes, s), fn);
+    return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, scales_gm, zeros_gm, perm, y, M, N,
+                                     K, group_size, workspace, workspace_bytes, s), fn);
   // GEMV, four activation rows per launch.
   const uint16_t* xp = (const uint16_t*)x;
   uint16_t* yp = (uint16_t*)y;

@@ -51,11 +51,18 @@ hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, con
 
 // workspace: zero-filled before first use, left zeroed; may be smaller than
 // gemm_workspace_bytes() (then unsplit) but must hold the counter block and
-// ws_perm when perm is set.
+// ws_perm when perm is set. scales_gm / zeros_gm (nullable): group-major
+// copies fp32 [G, N] / u8 [G, N], used when both are given and N % 4 == 0.
 hipError_t launch_gemm(const void* x, const uint8_t* w, const float* scales, const void* zeros,
-                       int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
-                       int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
-                       hipStream_t stream);
+                       int zero_u8, const float* scales_gm, const uint8_t* zeros_gm,
+                       const int32_t* perm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                       void* workspace, size_t ws_bytes, hipStream_t stream);
+
+// [N, G] scales and zero points -> group-major fp32 [G, N] and u8 [G, N]
+// (zeros must hold integers in [0, 15]; others are counted into *bad).
+hipError_t launch_sz_group_major(const float* scales, const void* zeros, int zero_u8,
+                                 float* scales_gm, uint8_t* zeros_gm, int32_t* bad, int64_t N,
+                                 int64_t G, hipStream_t stream);
 
 hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,
                          int64_t K, int64_t gs, hipStream_t stream);

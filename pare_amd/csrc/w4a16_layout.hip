@@ -64,6 +64,33 @@ __global__ void zeros_to_u8_kernel(const float* __restrict__ zeros, uint8_t* __r
   if (bad && local_bad) atomicAdd(bad, local_bad);
 }
 
+// [N, G] -> [G, N] copies of the scales and zero points (zeros to u8, values
+// that are not integers in [0, 15] counted like zeros_to_u8_kernel). One
+// thread per output element: writes are coalesced, reads strided; it runs
+// once per layer.
+__global__ void sz_group_major_kernel(const float* __restrict__ scales,
+                                      const void* __restrict__ zeros, int zero_u8,
+                                      float* __restrict__ s_gm, uint8_t* __restrict__ z_gm,
+                                      int32_t* __restrict__ bad, int64_t N, int64_t G) {
+  int local_bad = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < N * G;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t g = i / N, n = i - g * N;
+    s_gm[i] = scales[n * G + g];
+    if (zero_u8) {
+      const uint8_t z = ((const uint8_t*)zeros)[n * G + g];
+      local_bad += z <= 15 ? 0 : 1;
+      z_gm[i] = z <= 15 ? z : (uint8_t)0;
+    } else {
+      const float z = ((const float*)zeros)[n * G + g];
+      const bool ok = z >= 0.f && z <= 15.f && z == rintf(z);  // false for NaN
+      local_bad += ok ? 0 : 1;
+      z_gm[i] = ok ? (uint8_t)(int)z : (uint8_t)0;
+    }
+  }
+  if (bad && local_bad) atomicAdd(bad, local_bad);
+}
+
 // w_hat = (float(q) - zero) * scale in fp32, then one rounding to out dtype
 // (pare/core/functional.py:90-91, pare/layers/linear.py:129).
 template <int OUT>
@@ -208,6 +235,14 @@ hipError_t launch_zeros_to_u8(const float* zeros, uint8_t* out, int32_t* bad, in
                               hipStream_t stream) {
   hipLaunchKernelGGL(zeros_to_u8_kernel, dim3(grid_for(count)), dim3(kBlock), 0, stream, zeros,
                      out, bad, count);
+  return hipGetLastError();
+}
+
+hipError_t launch_sz_group_major(const float* scales, const void* zeros, int zero_u8,
+                                 float* scales_gm, uint8_t* zeros_gm, int32_t* bad, int64_t N,
+                                 int64_t G, hipStream_t stream) {
+  hipLaunchKernelGGL(sz_group_major_kernel, dim3(grid_for(N * G)), dim3(kBlock), 0, stream, scales,
+                     zeros, zero_u8, scales_gm, zeros_gm, bad, N, G);
   return hipGetLastError();
 }
 

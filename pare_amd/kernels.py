@@ -118,6 +118,7 @@ def matmul_w4a16(
     group_size: int,
     *,
     perm: torch.Tensor | None = None,
+    sz_gm: tuple[torch.Tensor, torch.Tensor] | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Y[M,N] = X[M,K] @ dequant(W)^T with the dequantisation fused (fp16 in, fp16 out).
@@ -129,8 +130,10 @@ def matmul_w4a16(
       zeros:         same shape as scales; fp32 integer values or uint8.
       group_size:    quantisation group size; the K-tile of the kernel layout.
     Extensions: ``perm`` (int32 [K]) for act_order layers whose weights were
-    repacked with the same permutation; ``out`` to write into a preallocated
-    [M, N] fp16 tensor.
+    repacked with the same permutation; ``sz_gm``, the group-major copies of
+    scales and zeros from ``pack.sz_group_major`` (fp32 and uint8 [G, N]), which
+    the MFMA GEMM reads as contiguous runs; ``out`` to write into a
+    preallocated [M, N] fp16 tensor.
     Raises RuntimeError when x is not on a HIP device or the library is
     missing; AssertionError on layout violations, like the reference.
     """
@@ -161,6 +164,14 @@ def matmul_w4a16(
         assert perm.dtype == torch.int32 and perm.numel() == K and perm.device == dev, \
             "perm must be an int32 [K] tensor on x's device"
         perm = perm.contiguous()
+    s_gm = z_gm = None
+    if sz_gm is not None:
+        s_gm, z_gm = sz_gm
+        assert s_gm.dtype == torch.float32 and tuple(s_gm.shape) == (G, N) and s_gm.is_contiguous(), \
+            "sz_gm[0] must be a contiguous float32 [G, N] tensor"
+        assert z_gm.dtype == torch.uint8 and tuple(z_gm.shape) == (G, N) and z_gm.is_contiguous(), \
+            "sz_gm[1] must be a contiguous uint8 [G, N] tensor"
+        assert s_gm.device == dev and z_gm.device == dev, "sz_gm must be on x's device"
     if out is None:
         out = torch.empty(M, N, device=dev, dtype=torch.float16)
     else:
@@ -172,7 +183,9 @@ def matmul_w4a16(
         ws = _workspace(dev, stream, nbytes)
         _lib.check(L.pmi_matmul_w4a16(
             xa.data_ptr(), _lib.PMI_F16, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
-            perm.data_ptr() if perm is not None else None, out.data_ptr(), _lib.PMI_F16,
+            perm.data_ptr() if perm is not None else None,
+            s_gm.data_ptr() if s_gm is not None else None,
+            z_gm.data_ptr() if z_gm is not None else None, out.data_ptr(), _lib.PMI_F16,
             M, N, K, group_size, ws.data_ptr() if ws is not None else None,
             ws.numel() if ws is not None else 0, stream), "pmi_matmul_w4a16")
     return out

@@ -22,7 +22,8 @@ import torch.nn.functional as F
 
 from .config import QuantConfig, is_int4, kernel_group_size
 from .kernels import matmul_w4a16
-from .pack import dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, zeros_to_u8
+from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
+                   zeros_to_u8)
 
 
 class QuantizedLinear(nn.Module):
@@ -110,10 +111,11 @@ class QuantizedLinear(nn.Module):
         return F.linear(x, weight, self.bias)
 
     def _kernel_buffers(self):
-        """Kernel-layout weight, u8 zeros and act_order permutation, built once
-        per (device, weight contents) like linear.py:148-151."""
+        """Kernel-layout weight, u8 zeros, group-major scales/zeros and the
+        act_order permutation, built once per (device, weight contents) like
+        linear.py:148-151."""
         stamp = (self.packed_weight.device, self.packed_weight.data_ptr(),
-                 self.packed_weight._version, self.zero._version)
+                 self.packed_weight._version, self.zero._version, self.scale._version)
         cache = getattr(self, "_kernel_cache", None)
         if cache is None or cache[0] != stamp:
             gs = self._group_size()
@@ -121,16 +123,17 @@ class QuantizedLinear(nn.Module):
             if self.g_idx is not None:
                 perm = perm_from_g_idx(self.g_idx.to(self.packed_weight.device), gs)
             self._packed_weight_kernel = repack_int4_for_kernel(self.packed_weight, gs, perm=perm)
-            cache = (stamp, zeros_to_u8(self.zero), perm)
+            zero_u8 = zeros_to_u8(self.zero)
+            cache = (stamp, zero_u8, perm, sz_group_major(self.scale, zero_u8))
             self._kernel_cache = cache
-        return self._packed_weight_kernel, cache[1], cache[2]
+        return self._packed_weight_kernel, cache[1], cache[2], cache[3]
 
     def _forward_kernel(self, x: torch.Tensor) -> torch.Tensor:
         """pare/layers/linear.py:140-159 with the HIP kernels."""
-        w_k, zero_u8, perm = self._kernel_buffers()
+        w_k, zero_u8, perm, sz_gm = self._kernel_buffers()
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
-        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm)
+        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm, sz_gm=sz_gm)
         y = y.to(x.dtype)
         if self.bias is not None:
             y = y + self.bias

@@ -60,6 +60,32 @@ def zeros_to_u8(zeros: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def sz_group_major(scales: torch.Tensor, zeros: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Group-major copies of a layer's scales and zero points, fp32 [G, N] and
+    uint8 [G, N], for the MFMA GEMM (``matmul_w4a16(..., sz_gm=...)``): one
+    group's scales and zeros of consecutive rows are contiguous. Built once per
+    layer, like the kernel-layout weight. Raises ValueError unless every zero
+    point is an integer in [0, 15]."""
+    L = _lib.lib()
+    _require_cuda(scales, "sz_group_major")
+    s = _to_2d(scales).float().contiguous()
+    z = _to_2d(zeros)
+    z = z.contiguous() if z.dtype == torch.uint8 else z.float().contiguous()
+    assert s.shape == z.shape and s.device == z.device, "scales and zeros must be [N, G] on one device"
+    N, G = s.shape
+    s_gm = torch.empty(G, N, dtype=torch.float32, device=s.device)
+    z_gm = torch.empty(G, N, dtype=torch.uint8, device=s.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=s.device)
+    zdt = _lib.PMI_U8 if z.dtype == torch.uint8 else _lib.PMI_F32
+    with _DeviceGuard(s.device):
+        _lib.check(L.pmi_sz_group_major(s.data_ptr(), z.data_ptr(), zdt, s_gm.data_ptr(),
+                                        z_gm.data_ptr(), bad.data_ptr(), N, G,
+                                        _stream_handle(s.device)), "pmi_sz_group_major")
+    if int(bad.item()) != 0:
+        raise ValueError(f"{int(bad.item())} zero points are not integers in [0, 15]")
+    return s_gm, z_gm
+
+
 _OUT_DTYPES = {torch.float16: _lib.PMI_F16, torch.bfloat16: _lib.PMI_BF16,
                torch.float32: _lib.PMI_F32}
 

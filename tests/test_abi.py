@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == 1
+    assert L.pmi_abi_version() == 2
 
 
 def test_kernel_choice(L):
@@ -80,8 +80,9 @@ FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid
 
 
 def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.PMI_F32,
-        perm=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16):
-    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, y, ydt, M, N, K, gs, None, 0, None)
+        perm=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16, s_gm=None, z_gm=None):
+    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, s_gm, z_gm, y, ydt, M, N, K, gs, None, 0,
+                              None)
 
 
 @pytest.mark.parametrize("kw,code,msg", [
@@ -96,6 +97,9 @@ def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.P
     (dict(x=FAKE + 2), _lib.PMI_ERR_INVALID, "x must be 16-byte aligned"),
     (dict(w=FAKE + 4), _lib.PMI_ERR_INVALID, "weight must be 16-byte aligned"),
     (dict(z=FAKE + 1), _lib.PMI_ERR_INVALID, "fp32 zeros"),
+    (dict(s_gm=FAKE), _lib.PMI_ERR_INVALID, "together"),
+    (dict(z_gm=FAKE), _lib.PMI_ERR_INVALID, "together"),
+    (dict(s_gm=FAKE + 2, z_gm=FAKE), _lib.PMI_ERR_INVALID, "4-byte aligned"),
 ])
 def test_matmul_validation(L, kw, code, msg):
     rc = _mm(L, **kw)
@@ -107,6 +111,16 @@ def test_matmul_empty_is_noop(L):
     assert _mm(L, M=0, x=None, w=None, s=None, z=None, y=None) == _lib.PMI_OK
     assert _mm(L, N=0, x=None, w=None, s=None, z=None, y=None) == _lib.PMI_OK
     assert _lib.last_error() == ""
+
+
+def test_sz_group_major_validation(L):
+    rc = L.pmi_sz_group_major(FAKE, FAKE, _lib.PMI_F16, FAKE, FAKE, None, 4, 2, None)
+    assert rc == _lib.PMI_ERR_INVALID and "zero dtype" in _lib.last_error()
+    rc = L.pmi_sz_group_major(FAKE, FAKE, _lib.PMI_U8, FAKE, FAKE, None, 4, 0, None)
+    assert rc == _lib.PMI_ERR_INVALID and "G > 0" in _lib.last_error()
+    rc = L.pmi_sz_group_major(FAKE, None, _lib.PMI_U8, FAKE, FAKE, None, 4, 2, None)
+    assert rc == _lib.PMI_ERR_INVALID and "null" in _lib.last_error()
+    assert L.pmi_sz_group_major(None, None, _lib.PMI_U8, None, None, None, 0, 2, None) == _lib.PMI_OK
 
 
 def test_repack_validation(L):

@@ -64,20 +64,21 @@ def _check_out(y_gpu, y_ref, what):
     assert (err <= bound).all(), f"{what}: max_abs={err.max():.4e}"
 
 
-def _matmul_case(M, N, K, gs, seed, zero_u8=False, kernel="auto"):
+def _matmul_case(M, N, K, gs, seed, zero_u8=False, kernel="auto", gm=False):
     packed, s, z = _layer(N, K, gs, seed)
     x = _x(M, K, seed + 1000)
     w_k = P.repack_int4_for_kernel(_cuda(packed), gs)
     zz = _cuda(z)
     if zero_u8:
         zz = P.zeros_to_u8(zz)
+    sz_gm = P.sz_group_major(_cuda(s), zz) if gm else None
     with force_kernel(kernel):
         name = P.kernel_choice(M, N, K, gs)
-        print(f"[case] M={M} N={N} K={K} gs={gs} u8={zero_u8} kernel={name}", flush=True)
-        y = P.matmul_w4a16(x.to(DEV), w_k, _cuda(s), zz, gs)
+        print(f"[case] M={M} N={N} K={K} gs={gs} u8={zero_u8} gm={gm} kernel={name}", flush=True)
+        y = P.matmul_w4a16(x.to(DEV), w_k, _cuda(s), zz, gs, sz_gm=sz_gm)
     torch.cuda.synchronize()
     ref = O.linear_fp32(x.float().numpy(), O.dequantize_packed(packed, s, z))
-    _check_out(y, ref, f"M={M} N={N} K={K} gs={gs} u8={zero_u8} kernel={name}")
+    _check_out(y, ref, f"M={M} N={N} K={K} gs={gs} u8={zero_u8} gm={gm} kernel={name}")
 
 
 def test_device_is_supported():
@@ -292,6 +293,40 @@ def test_each_kernel(kernel, M, N, K, gs):
     _matmul_case(M, N, K, gs, M * 131 + N + K, kernel=kernel)
 
 
+@pytest.mark.parametrize("zero_u8", [False, True])
+def test_sz_group_major_bitexact(zero_u8):
+    N, K, gs = 300, 1024, 128
+    _, s, z = _layer(N, K, gs, 5)
+    zz = P.zeros_to_u8(_cuda(z)) if zero_u8 else _cuda(z)
+    s_gm, z_gm = P.sz_group_major(_cuda(s), zz)
+    torch.cuda.synchronize()
+    G = K // gs
+    assert s_gm.shape == (G, N) and z_gm.shape == (G, N) and z_gm.dtype == torch.uint8
+    s2, z2 = s.reshape(N, G), z.reshape(N, G)
+    assert (s_gm.cpu().numpy().view(np.uint32) == s2.T.view(np.uint32)).all()
+    assert (z_gm.cpu().numpy() == z2.T.astype(np.uint8)).all()
+
+
+def test_sz_group_major_rejects_bad_zeros():
+    s = torch.ones(8, 2, device=DEV)
+    z = torch.full((8, 2), 3.0, device=DEV)
+    z[5, 1] = 16.0
+    with pytest.raises(ValueError, match="1 zero points"):
+        P.sz_group_major(s, z)
+
+
+# The MFMA GEMM with the group-major scales and zeros: split and unsplit tiles,
+# ragged N and M, multi-unit groups; N % 4 != 0 takes the [N, G] path.
+GM_CASES = [(5, 1040, 1024, 128), (16, 4096, 4096, 128), (33, 520, 3584, 128),
+            (64, 14336, 4096, 128), (64, 4096, 14336, 128), (128, 1040, 2048, 128),
+            (17, 272, 2048, 256), (64, 300, 1024, 512), (40, 1042, 1024, 128)]
+
+
+@pytest.mark.parametrize("M,N,K,gs", GM_CASES)
+def test_gemm_group_major(M, N, K, gs):
+    _matmul_case(M, N, K, gs, M * 7 + N + K, zero_u8=True, kernel="gemm", gm=True)
+
+
 @pytest.mark.parametrize("kernel", ["gemv", "skinny"])
 @pytest.mark.parametrize("M", [1, 4])
 def test_each_kernel_u8_zeros(kernel, M):
@@ -373,6 +408,24 @@ def test_matmul_act_order(M, N, K, kernel):
     _check_out(y, ref, f"act_order M={M} N={N} K={K} kernel={name}")
 
 
+@pytest.mark.parametrize("M", [16, 64])
+def test_matmul_act_order_group_major(M):
+    N, K, gs = 3584, 3584, 128
+    rng = np.random.default_rng(M)
+    w = _w(N, K, M + 1)
+    packed, s, z, g = O.rtn_quantize_act_order(w, rng.permutation(K), gs)
+    x = _x(M, K, 6)
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    with force_kernel("gemm"):
+        print(f"[case] act_order gm M={M}", flush=True)
+        y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, perm=pm,
+                           sz_gm=P.sz_group_major(_cuda(s), zu8))
+    ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
+    _check_out(y, ref, f"act_order gm M={M}")
+
+
 def test_gemm_workspace_reused_across_shapes():
     """One workspace serves split-K GEMMs of different tile counts and act_order
     gathers in any order; each result matches the oracle and the split-K
@@ -406,7 +459,7 @@ def test_gemm_workspace_reused_across_shapes():
             with force_kernel("gemm"):
                 rc = L.pmi_matmul_w4a16(xd.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
                                         zd.data_ptr(), _lib.PMI_U8,
-                                        pm.data_ptr() if pm is not None else None,
+                                        pm.data_ptr() if pm is not None else None, None, None,
                                         y.data_ptr(), _lib.PMI_F16, M, N, K, gs, ws.data_ptr(),
                                         ws.numel(), stream)
             assert rc == 0, _lib.last_error()
