@@ -267,6 +267,13 @@ def main():
         for i in range(copies):
             run(s, [single[i % n_layers][4 + (i // n_layers) % 2]], M)  # gate and up of all layers
 
+    # the M > 4 legs read group-major scale/zero copies: build them outside any
+    # graph capture, as a module does once per layer
+    for layer in single:
+        layer[4].gm()
+        layer[5].gm()
+    torch.cuda.synchronize()
+
     if args.kernel_only:
         with torch.cuda.stream(stream):
             for _ in range(5):

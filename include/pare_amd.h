@@ -153,7 +153,8 @@ PMI_API int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float*
                      int64_t N, int64_t K, int64_t group_size, int sym, void* stream);
 
 /* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
- * 2 = MFMA GEMM, 3 = skinny MFMA kernel (M <= 16). Host-only; no reference
+ * 2 = MFMA GEMM (group_size % 128 == 0 and K % 256 == 0), 3 = skinny MFMA
+ * kernel (M <= 16). Host-only; no reference
  * counterpart (the reference has one Triton kernel). */
 PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size);
 

@@ -115,13 +115,14 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   if (forced) return forced;
   if (M <= 4) return 1;
   if (pmi::skinny_supported(M, N, K, group_size)) return 3;
-  return group_size % 128 == 0 ? 2 : 1;
+  return pmi::gemm_supported(K, group_size) ? 2 : 1;
 }
 
 size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
                                   int has_perm) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
-  if (pmi_matmul_kernel_choice(M, N, K, group_size) != 2 || group_size % 128 != 0) return 0;
+  if (pmi_matmul_kernel_choice(M, N, K, group_size) != 2 || !pmi::gemm_supported(K, group_size))
+    return 0;
   return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
 }
 
@@ -174,7 +175,7 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
   // act_order on the GEMM gathers X[:, perm] into the workspace; without one
   // the automatic choice falls back to the GEMV.
-  const bool perm_fits = !perm || group_size % 128 != 0 ||
+  const bool perm_fits = !perm || !pmi::gemm_supported(K, group_size) ||
                          workspace_bytes >= pmi::gemm_workspace_bytes(M, N, K, group_size, true) -
                                                 pmi::gemm_config(M, N, K, group_size, true).ws_split;
   if (choice == 2 && !perm_fits) {
@@ -185,8 +186,9 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   if (choice == 3 && !pmi::skinny_supported(M, N, K, group_size))
     return fail(PMI_ERR_UNSUPPORTED, "%s: forced skinny kernel needs M <= 16, group_size %% 128 "
                 "== 0 and the activations within 64 KiB of LDS", fn);
-  if (choice == 2 && group_size % 128 != 0)
-    return fail(PMI_ERR_UNSUPPORTED, "%s: forced MFMA GEMM needs group_size %% 128 == 0", fn);
+  if (choice == 2 && !pmi::gemm_supported(K, group_size))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: forced MFMA GEMM needs group_size %% 128 == 0 and "
+                "K %% 256 == 0", fn);
   if (choice == 3)
     return from_hip(pmi::launch_skinny(x, w, scales, zeros, zu8, perm, y, M, N, K, group_size, s),
                     fn);

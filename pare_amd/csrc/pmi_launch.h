@@ -42,6 +42,8 @@ SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
 hipError_t launch_skinny(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                          int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                          int64_t K, int64_t gs, hipStream_t stream);
+// The MFMA GEMM runs whole 128-column groups, consumed two at a time.
+inline bool gemm_supported(int64_t K, int64_t gs) { return gs % 128 == 0 && K % 256 == 0; }
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 

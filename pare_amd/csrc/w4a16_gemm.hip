@@ -1,15 +1,17 @@
 // Split-K MFMA INT4 W4A16 GEMM for M > 4, gfx950 (v_mfma_f32_16x16x32_f16).
 //
-// Work layout. A workgroup is 4 waves and owns 128 weight rows (a "tile") for up
-// to 64 activation rows (MT MFMA row tiles of 16), over a contiguous range of
-// "units". A unit is 128 columns of K: 64 bytes of every packed row (kernel
-// layout), i.e. columns k0+64c+b (low nibble of byte b) and k0+gs/2+64c+b (high
-// nibble), b < 64, of the group starting at k0. Units are consumed in pairs:
-// wave w takes weight rows 64*(w&1)..+63 (four 16-row MFMA tiles) of the pair's
-// unit w>>1, so each wave reads from LDS only the activations of its own units
-// and every activation fragment it reads feeds four weight tiles. The two
-// k-parities are added through LDS at the end. With K split over `splits`
-// workgroups per tile, the grid is tiles x splits.
+// Work layout. A workgroup is 4 compute waves and 4 producer waves (two waves
+// per SIMD) and owns 128 weight rows (a "tile") for up to 64 activation rows
+// (MT MFMA row tiles of 16), over a contiguous range of "units". A unit is 128
+// columns of K: 64 bytes of every packed row (kernel layout), i.e. columns
+// k0+64c+b (low nibble of byte b) and k0+gs/2+64c+b (high nibble), b < 64, of
+// the group starting at k0. Units are consumed in pairs: compute wave w takes
+// weight rows 64*(w&1)..+63 (four 16-row MFMA tiles) of the pair's unit w>>1,
+// so each wave reads from LDS only the activations of its own units and every
+// activation fragment it reads feeds four weight tiles. The two k-parities
+// are added through LDS at the end. The producer waves only issue the copies
+// and wait for them. With K split over `splits` workgroups per tile, the grid
+// is tiles x splits.
 //
 // Operands. Lane l holds 16 bytes of each of its four weight tiles per unit
 // (row l%16, bytes 16*(l/16)..+15). Each k-step takes 8 of those bytes and one
@@ -24,12 +26,13 @@
 // bytes, 16-byte chunks XOR-swizzled per row so the A reads of 16 rows hit 16
 // bank groups), its 128 x 64 weight bytes, and the scale and zero-point words
 // of its 128 rows - goes straight from memory into an LDS slot with
-// buffer_load ... lds (no VGPRs in flight). P pairs of slots form a ring; each
-// step waits for its own copies of the oldest pair with an explicit vmcnt,
-// crosses one plain s_barrier (which also frees the pair computed in the
-// previous step) and issues the pair P-1 steps ahead. Loads are
-// unconditional (ranges are clamped, never branched around) and the
-// steady-state loop is straight-line code.
+// buffer_load ... lds (no VGPRs in flight). P pairs of slots form a ring; at
+// each step the producers wait for their copies of the oldest pair with an
+// explicit vmcnt, everyone crosses one plain s_barrier (which also frees the
+// pair computed in the previous step), the producers issue the pair P-1
+// steps ahead and the compute waves compute. Loads are unconditional (ranges
+// are clamped, never branched around) and the steady-state loops are
+// straight-line code.
 //
 // Split-K. Every split stores its fp32 partial tile (lane-contiguous, coalesced)
 // in the caller's workspace and bumps the tile's counter; the last workgroup to
@@ -48,22 +51,35 @@
 namespace pmi {
 namespace {
 
-constexpr int kWaves = 4;               // waves per workgroup
-constexpr int kNT = 4;                  // 16-row weight tiles per wave
+constexpr int kWaves = 4;               // compute waves per workgroup
+constexpr int kProducers = 4;           // copy-issuing waves per workgroup
+constexpr int kNT = 4;                  // 16-row weight tiles per compute wave
 constexpr int kBN = 128;                // weight rows per workgroup
-constexpr int kThreads = kWaves * 64;
+constexpr int kThreads = (kWaves + kProducers) * 64;
 constexpr int kWBytes = kBN * 64;       // weight bytes of one unit
 constexpr int kSBytes = kBN * 4;        // scales of one unit
 constexpr int kZBytes = kBN * 4;        // zero-point words of one unit
 
+// LDS rings (units are consumed in pairs, one unit per k parity):
+//   weights of a pair - 128 rows x 128 bytes, each row's 8 chunks of 16 bytes
+//   XOR-swizzled by row % 8 - then the scale and zero words of its two units,
+//   kWPair bytes, PW slots;
+//   activations of a unit, kX bytes, 2*PX slots.
+// Weights come from HBM and get the deep ring; activations are re-read from
+// L2 by every workgroup and get a shallow one. A pair's two units are 128
+// contiguous bytes of every packed row: each weight copy fetches whole cache
+// lines (8 rows x 128 bytes), which the DRAM serves far better than the 64-byte
+// halves one unit would give.
+constexpr int kWLines = kBN * 128;                              // weight bytes of a pair
+constexpr int kWPair = kWLines + 2 * (kSBytes + kZBytes);       // weight slot of a pair
 template <int MT>
 struct Tiling {
-  static constexpr int R = 16 * MT;                          // activation rows
-  static constexpr int kX = R * 256;                         // activation tile of a unit
-  static constexpr int kSlot = kX + kWBytes + kSBytes + kZBytes;
-  static constexpr int kPair = 2 * kSlot;
-  static constexpr int P = MT == 1 ? 5 : (MT == 2 ? 4 : 3);  // unit pairs in the ring
-  static constexpr int kCopies = MT + 3;                     // copies per wave per unit
+  static constexpr int R = 16 * MT;                             // activation rows
+  static constexpr int kX = R * 256;                            // activation tile of a unit
+  static constexpr int PW = MT == 4 ? 5 : 6;                    // weight pairs in the ring
+  static constexpr int PX = MT == 4 ? 2 : 3;                    // activation pairs in the ring
+  static constexpr int kWCopies = 12;                           // per weight producer per pair
+  static constexpr int kXCopies = 4 * MT;                       // per activation producer per pair
 };
 
 struct GemmArgs {
@@ -76,7 +92,7 @@ struct GemmArgs {
   f16* y;
   float* part;    // split-K partial tiles (splits > 1)
   int* counters;  // one per (m-block, tile), zero between calls
-  int M, N, K, gs, splits, n_tiles;
+  int M, N, K, gs, splits, n_tiles, grid_m;
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -124,12 +140,6 @@ PMI_DEV void static_for(F&& f) {
 // memory accesses across it.
 PMI_DEV void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
-// The value of v, hidden from the optimiser (no instruction is emitted).
-PMI_DEV int opaque(int v) {
-  asm("" : "+v"(v));
-  return v;
-}
-
 // B operand: 8 nibbles (one run of two words) as fp16 (q - z).
 PMI_DEV f16x8 b_operand(uint32_t t0, uint32_t t1, f16x2 nz) {
   const uint32_t K = 0x64646464u;
@@ -147,119 +157,55 @@ PMI_DEV f16x8 b_operand(uint32_t t0, uint32_t t1, f16x2 nz) {
 template <int MT, bool ZU8, bool SZT>
 __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
   using T = Tiling<MT>;
-  constexpr int R = T::R, kX = T::kX, kSlot = T::kSlot, P = T::P;
-  constexpr int kPairCopies = 2 * T::kCopies;
-  static_assert(P >= 2 && P <= 5 && (P - 1) * kPairCopies < 64, "pipeline depth");
-  static_assert(P * T::kPair <= 160 * 1024, "LDS budget");
-  static_assert(2 * MT * kNT * 64 * 16 <= T::kPair, "k-parity reduction fits one pair");
-  // one LDS array per pair of ring slots: the compiler tracks each pair's
-  // copies apart, so reading one pair never waits for copies into another
-  __shared__ __attribute__((aligned(16))) uint8_t lp0[T::kPair], lp1[T::kPair], lp2[T::kPair],
-      lp3[T::kPair], lp4[T::kPair];
+  constexpr int R = T::R, kX = T::kX, PW = T::PW, PX = T::PX;
+  constexpr int kWC = T::kWCopies, kXC = T::kXCopies;
+  static_assert(PW >= 2 && (PW - 1) * kWC < 64 && PX >= 2 && (PX - 1) * kXC < 64,
+                "copies in flight per producer wave fit vmcnt (63)");
+  static_assert(PW * kWPair + 2 * PX * kX <= 160 * 1024, "LDS budget");
+  static_assert(2 * MT * kNT * 64 * 16 <= PW * kWPair, "k-parity reduction fits the weight ring");
+  __shared__ __attribute__((aligned(16))) uint8_t wring[PW * kWPair];
+  __shared__ __attribute__((aligned(16))) uint8_t xring[2 * PX * kX];
   __shared__ int last_flag;
-  auto pair_ptr = [&](auto PAIR) -> uint8_t* {
-    constexpr int q = decltype(PAIR)::value;
-    if constexpr (q == 0) return lp0;
-    else if constexpr (q == 1) return lp1;
-    else if constexpr (q == 2) return lp2;
-    else if constexpr (q == 3) return lp3;
-    else return lp4;
-  };
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the copies' LDS base is M0
-  const int rh = wv & 1, kp = wv >> 1;                       // row half, k parity
+  // waves 0..3 compute, 4 and 5 copy weights (+ scales, zero points), 6 and 7
+  // copy activations
+  const bool producer = wv >= kWaves;
+  const bool wprod = wv == 4 || wv == 5, xprod = wv >= 6;
+  const int pw = wv & 1;                                     // index within a producer pair
+  const int rh = wv & 1;                                     // compute: row half
+  const int kp = producer ? 2 : (wv >> 1);                   // compute: k parity
   const int kq = l >> 4, ln = l & 15;
   const int bid = blockIdx.x;
   const int sp = bid % a.splits;
+  // (tile, m-block) of this workgroup. Workgroups are dealt to the 8 XCDs
+  // round-robin by index, so the m-blocks of one tile are numbered 8 apart:
+  // they then share an XCD and its L2, and the second read of the tile's
+  // weights hits there. (Only a placement preference: correctness does not
+  // depend on it.)
   const int tl = bid / a.splits;
-  const int tile = tl % a.n_tiles, mb = tl / a.n_tiles;
+  int tile, mb;
+  {
+    const int gm = a.grid_m, full = (a.n_tiles / 8) * 8;
+    if (tl < full * gm) {
+      const int r = tl % (8 * gm);
+      tile = (tl / (8 * gm)) * 8 + (r & 7);
+      mb = r >> 3;
+    } else {
+      const int rem = a.n_tiles - full, r = tl - full * gm;
+      tile = full + r % rem;
+      mb = r / rem;
+    }
+  }
   const int M = a.M, N = a.N, K = a.K, gs = a.gs;
-  const int units = K >> 7;
-  const int u_begin = (int)((int64_t)sp * units / a.splits);
-  const int u_end = (int)((int64_t)(sp + 1) * units / a.splits);
+  const int units = K >> 7;  // even (K % 256 == 0): every pair is whole
+  const int u_begin = 2 * (int)((int64_t)sp * (units >> 1) / a.splits);
+  const int u_end = 2 * (int)((int64_t)(sp + 1) * (units >> 1) / a.splits);
   const int upg = gs >> 7;
   const int G = K / gs;
   const int row_bytes = K >> 1;
-
-  const __amdgpu_buffer_rsrc_t rw = rsrc(a.w, (int64_t)N * row_bytes);
-  const __amdgpu_buffer_rsrc_t rs = rsrc(a.s, (int64_t)N * G * 4);
-  // u8 zero points are fetched as the aligned word holding the byte; an
-  // aligned word never crosses a page, so it lies in the zeros' allocation
-  const __amdgpu_buffer_rsrc_t rz =
-      rsrc(a.z, ZU8 ? (((int64_t)N * G + 3) & ~(int64_t)3) : (int64_t)N * G * 4);
-  const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (int64_t)M * K * 2);
-
-  // Copies of this wave per unit: weight tiles 2*wv, 2*wv+1; activation rows
-  // 4*(wv*MT + r) .. +3 (16 chunks each; LDS chunk p of row m holds activation
-  // chunk p ^ (m % 16)); the scale (waves 0, 1) or zero-point (waves 2, 3)
-  // words of rows 64*(wv&1) + l.
-  int vw[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    int n = tile * kBN + (2 * wv + j) * 16 + ln;
-    n = n < N ? n : N - 1;
-    vw[j] = n * row_bytes + 16 * kq;
-  }
-  int vx[MT];
-#pragma unroll
-  for (int r = 0; r < MT; ++r) {
-    const int mloc = 4 * (wv * MT + r) + (l >> 4);
-    const int c = (l & 15) ^ (mloc & 15);
-    int mg = mb * R + mloc;
-    mg = mg < M ? mg : M - 1;
-    vx[r] = mg * K * 2 + (c >> 3) * gs + 16 * (c & 7);
-  }
-  const bool sz_scale = wv < 2;
-  __amdgpu_buffer_rsrc_t rsz;
-  int gmul, vsz;
-  if constexpr (SZT) {
-    // waves 0, 1: scales of rows 64*wv + l; waves 2, 3: the zero bytes of rows
-    // 64*(wv-2) + 4l .. +3 (lanes 16..63 repeat lanes 0..15; rows past N are
-    // clamped into the array, N % 4 == 0)
-    rsz = sz_scale ? rsrc(a.s_gm, (int64_t)G * N * 4) : rsrc(a.z_gm, (int64_t)G * N);
-    gmul = sz_scale ? 4 * N : N;  // bytes per group
-    int n = sz_scale ? tile * kBN + 64 * (wv & 1) + l : tile * kBN + 64 * (wv & 1) + 4 * (l & 15);
-    const int nmax = sz_scale ? N - 1 : N - 4;
-    n = n < nmax ? n : nmax;
-    vsz = sz_scale ? 4 * n : n;
-  } else {
-    rsz = sz_scale ? rs : rz;
-    gmul = (sz_scale || !ZU8) ? 4 : 1;  // bytes per (row, group) entry
-    int n = tile * kBN + 64 * (wv & 1) + l;
-    n = n < N ? n : N - 1;
-    vsz = n * G * gmul;
-  }
-
-  // everything unit u needs -> the slot at `base`
-  auto issue_unit = [&](uint8_t* base, int u) {
-    u = u < u_end ? u : u_end - 1;
-    const int g = u / upg;
-    const int xoff = __builtin_amdgcn_readfirstlane((g * gs + 64 * (u - g * upg)) * 2);
-    const int woff = __builtin_amdgcn_readfirstlane(u * 64);
-#pragma unroll
-    for (int r = 0; r < MT; ++r) copy_to_lds<16>(rx, base + (wv * MT + r) * 1024, vx[r], xoff);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) copy_to_lds<16>(rw, base + kX + (2 * wv + j) * 1024, vw[j], woff);
-    if constexpr (SZT)
-      copy_to_lds<4>(rsz, base + kX + kWBytes + wv * 256, vsz, __builtin_amdgcn_readfirstlane(g * gmul));
-    else
-      copy_to_lds<4>(rsz, base + kX + kWBytes + wv * 256, (vsz + g * gmul) & ~3, 0);
-  };
-  auto issue_pair = [&](auto PAIR, int q) {
-    uint8_t* base = pair_ptr(PAIR);
-    issue_unit(base, u_begin + 2 * q);
-    issue_unit(base + kSlot, u_begin + 2 * q + 1);
-  };
-
-  // per-lane constants of the compute: this wave's rows and their zero words
-  int zrow[kNT];
-#pragma unroll
-  for (int j = 0; j < kNT; ++j) {
-    int n = tile * kBN + 64 * rh + 16 * j + ln;
-    n = n < N ? n : N - 1;
-    zrow[j] = n * G;
-  }
+  const int n_pairs = (u_end - u_begin) >> 1;
 
   f32x4 acc[MT][kNT];
 #pragma unroll
@@ -267,96 +213,191 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < kNT; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const uint8_t* base, int u) {
-    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-    const int g = u / upg;
-    u32x4 w[kNT];
-    f16x2 nz[kNT];
-    float sc[kNT];
+  if (wprod) {
+    // ---- weight producer pw: rows 64*pw .. +63 as 8 copies of 8 rows x 128
+    // bytes (lane l: row 8i + l/8, chunk l%8 of the LDS row, which holds the
+    // pair's chunk (l%8) ^ (row%8)), and the scale (pw 0) or zero-point (pw 1)
+    // words of rows 0..63 and 64..127 of both units
+    const __amdgpu_buffer_rsrc_t rw = rsrc(a.w, (int64_t)N * row_bytes);
+    int vl[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rloc = 64 * pw + 8 * i + (l >> 3);
+      int n = tile * kBN + rloc;
+      n = n < N ? n : N - 1;
+      vl[i] = n * row_bytes + 16 * ((l & 7) ^ (rloc & 7));
+    }
+    const bool scale = pw == 0;
+    __amdgpu_buffer_rsrc_t rsz;
+    int gmul, vsz[2];
+    if constexpr (SZT) {
+      // scales: rows h*64 + l; zero bytes: rows h*64 + 4l .. +3 (lanes 16..63
+      // repeat lanes 0..15; rows past N are clamped into the array, N % 4 == 0)
+      rsz = scale ? rsrc(a.s_gm, (int64_t)G * N * 4) : rsrc(a.z_gm, (int64_t)G * N);
+      gmul = scale ? 4 * N : N;  // bytes per group
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int n = scale ? tile * kBN + 64 * h + l : tile * kBN + 64 * h + 4 * (l & 15);
+        const int nmax = scale ? N - 1 : N - 4;
+        n = n < nmax ? n : nmax;
+        vsz[h] = scale ? 4 * n : n;
+      }
+    } else {
+      // u8 zero points are fetched as the aligned word holding the byte; an
+      // aligned word never crosses a page, so it lies in the zeros' allocation
+      rsz = scale ? rsrc(a.s, (int64_t)N * G * 4)
+                  : rsrc(a.z, ZU8 ? (((int64_t)N * G + 3) & ~(int64_t)3) : (int64_t)N * G * 4);
+      gmul = (scale || !ZU8) ? 4 : 1;  // bytes per (row, group) entry
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int n = tile * kBN + 64 * h + l;
+        n = n < N ? n : N - 1;
+        vsz[h] = n * G * gmul;
+      }
+    }
+    // slot: [weight lines 128 x 128 B][unit 0: scales, zero words][unit 1: ...]
+    auto issue_pair = [&](int slot, int q) {
+      uint8_t* base = wring + slot * kWPair;
+      int u0 = u_begin + 2 * q;
+      u0 = u0 < u_end - 2 ? u0 : u_end - 2;
+      const int woff = __builtin_amdgcn_readfirstlane(u0 * 64);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) copy_to_lds<16>(rw, base + (64 * pw + 8 * i) * 128, vl[i], woff);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int g = (u0 + e) / upg;
+        uint8_t* sz = base + kWLines + e * (kSBytes + kZBytes) + pw * kSBytes;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (SZT)
+            copy_to_lds<4>(rsz, sz + h * 256, vsz[h], __builtin_amdgcn_readfirstlane(g * gmul));
+          else
+            copy_to_lds<4>(rsz, sz + h * 256, (vsz[h] + g * gmul) & ~3, 0);
+        }
+      }
+    };
+    // pairs 0 .. PW-2 in flight; step q waits for pair q and issues pair
+    // q+PW-1 (clamped past the range) into the slot pair q-1 used
+    for (int q = 0; q < PW - 1; ++q) issue_pair(q, q);
+    int slot = PW - 1;
+    for (int q = 0; q < n_pairs; ++q) {
+      wait_vmcnt<(PW - 2) * kWC>();
+      barrier_only();
+      issue_pair(slot, q + PW - 1);
+      slot = slot + 1 == PW ? 0 : slot + 1;
+    }
+    wait_vmcnt<0>();  // clamped copies past the range may still be landing
+  } else if (xprod) {
+    // ---- activation producer pw: tile rows 4*(pw*2*MT + r) .. +3, 16 chunks
+    // each; LDS chunk p of row m holds activation chunk p ^ (m % 16)
+    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (int64_t)M * K * 2);
+    int vx[2 * MT];
+#pragma unroll
+    for (int r = 0; r < 2 * MT; ++r) {
+      const int mloc = 4 * (pw * 2 * MT + r) + (l >> 4);
+      const int c = (l & 15) ^ (mloc & 15);
+      int mg = mb * R + mloc;
+      mg = mg < M ? mg : M - 1;
+      vx[r] = mg * K * 2 + (c >> 3) * gs + 16 * (c & 7);
+    }
+    auto issue_unit = [&](int slot, int u) {
+      uint8_t* base = xring + slot * kX;
+      u = u < u_end ? u : u_end - 1;
+      const int g = u / upg;
+      const int xoff = __builtin_amdgcn_readfirstlane((g * gs + 64 * (u - g * upg)) * 2);
+#pragma unroll
+      for (int r = 0; r < 2 * MT; ++r)
+        copy_to_lds<16>(rx, base + (pw * 2 * MT + r) * 1024, vx[r], xoff);
+    };
+    for (int q = 0; q < PX - 1; ++q) {
+      issue_unit(2 * q, u_begin + 2 * q);
+      issue_unit(2 * q + 1, u_begin + 2 * q + 1);
+    }
+    int slot = 2 * (PX - 1);
+    for (int q = 0; q < n_pairs; ++q) {
+      wait_vmcnt<(PX - 2) * kXC>();
+      barrier_only();
+      issue_unit(slot, u_begin + 2 * (q + PX - 1));
+      issue_unit(slot + 1, u_begin + 2 * (q + PX - 1) + 1);
+      slot = slot + 2 == 2 * PX ? 0 : slot + 2;
+    }
+    wait_vmcnt<0>();
+  } else {
+    // ---- compute wave (row half rh, k parity kp): no copies of its own, so
+    // its LDS reads never wait on the copy queue; the step barrier orders them
+    int zrow[kNT];
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
-      const int row = 64 * rh + 16 * j + ln;
-      // Every per-tile LDS offset goes through opaque(): each read is then one
-      // offset from the pair array. Folded into a chain of offsets, the later
-      // reads lose the LDS alias information and the compiler would wait for
-      // every copy in flight before them.
-      w[j] = *reinterpret_cast<const u32x4*>(base + opaque(kX + (4 * rh + j) * 1024 + 16 * l));
-      sc[j] = *reinterpret_cast<const float*>(base + opaque(kX + kWBytes + 4 * row));
-      uint32_t z;
-      if constexpr (SZT) {
-        z = base[opaque(kX + kWBytes + kSBytes + 256 * rh + 16 * j + ln)];
-      } else {
-        const uint32_t zw =
-            *reinterpret_cast<const uint32_t*>(base + opaque(kX + kWBytes + kSBytes + 4 * row));
-        z = ZU8 ? (zw >> (((zrow[j] + g) & 3) * 8)) & 0xFFu : (uint32_t)(int)__builtin_bit_cast(float, zw);
-      }
-      nz[j] = as_f16x2(neg_magic_zero_x2(z));
+      int n = tile * kBN + 64 * rh + 16 * j + ln;
+      n = n < N ? n : N - 1;
+      zrow[j] = n * G;
     }
-    f32x4 cg[MT][kNT];
+    int wslot = 0, xslot = kp;
+    for (int q = 0; q < n_pairs; ++q) {
+      barrier_only();  // every copy of pair q is in; every wave is done with pair q-1
+      const int u = u_begin + 2 * q + kp;
+      if (u < u_end) {
+        const uint8_t* wb = wring + wslot * kWPair;
+        const uint8_t* szb = wb + kWLines + kp * (kSBytes + kZBytes);
+        const uint8_t* xb = xring + xslot * kX;
+        const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+        const int g = u / upg;
+        u32x4 w[kNT];
+        f16x2 nz[kNT];
+        float sc[kNT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int run = t >> 1, half = t & 1;
-      const int c = run * 8 + 2 * kq + half;
-      f16x8 A[MT];
+        for (int j = 0; j < kNT; ++j) {
+          const int row = 64 * rh + 16 * j + ln;
+          // 16 bytes of this unit: chunk 4*kp + kq of the row's 128, swizzled
+          w[j] = *reinterpret_cast<const u32x4*>(wb + row * 128 + 16 * ((4 * kp + kq) ^ (row & 7)));
+          sc[j] = *reinterpret_cast<const float*>(szb + 4 * row);
+          uint32_t z;
+          if constexpr (SZT) {
+            z = szb[kSBytes + 256 * rh + 16 * j + ln];  // rows 64h + 4l.. at 256h + 4l
+          } else {
+            const uint32_t zw = *reinterpret_cast<const uint32_t*>(szb + kSBytes + 4 * row);
+            z = ZU8 ? (zw >> (((zrow[j] + g) & 3) * 8)) & 0xFFu
+                    : (uint32_t)(int)__builtin_bit_cast(float, zw);
+          }
+          nz[j] = as_f16x2(neg_magic_zero_x2(z));
+        }
+        f32x4 cg[MT][kNT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        A[mt] = *reinterpret_cast<const f16x8*>(base + (16 * mt + ln) * 256 + ((c ^ ln) << 4));
+        for (int t = 0; t < 4; ++t) {
+          const int run = t >> 1, half = t & 1;
+          const int c = run * 8 + 2 * kq + half;
+          f16x8 A[MT];
 #pragma unroll
-      for (int j = 0; j < kNT; ++j) {
-        const uint32_t w0 = w[j][2 * half], w1 = w[j][2 * half + 1];
-        const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
-        const uint32_t t1 = (run ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
-        const f16x8 B = b_operand(t0, t1, nz[j]);
+          for (int mt = 0; mt < MT; ++mt)
+            A[mt] = *reinterpret_cast<const f16x8*>(xb + (16 * mt + ln) * 256 + ((c ^ ln) << 4));
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B, t == 0 ? zero4 : cg[mt][j],
-                                                             0, 0, 0);
+          for (int j = 0; j < kNT; ++j) {
+            const uint32_t w0 = w[j][2 * half], w1 = w[j][2 * half + 1];
+            const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
+            const uint32_t t1 = (run ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
+            const f16x8 B = b_operand(t0, t1, nz[j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B, t == 0 ? zero4 : cg[mt][j],
+                                                                 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kNT; ++j)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(sc[j], cg[mt][j][i], acc[mt][j][i]);
       }
+      wslot = wslot + 1 == PW ? 0 : wslot + 1;
+      xslot = xslot + 2 >= 2 * PX ? xslot + 2 - 2 * PX : xslot + 2;
     }
-#pragma unroll
-    for (int j = 0; j < kNT; ++j)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(sc[j], cg[mt][j][i], acc[mt][j][i]);
-  };
-
-  // Pipeline: pairs 0 .. P-2 in flight before the loop; step q waits for pair
-  // q, computes one unit of it per wave and issues pair q+P-1 into the pair
-  // array that step q-1 finished with.
-  const int nu = u_end - u_begin;
-  const int full_pairs = nu >> 1, n_pairs = (nu + 1) >> 1;
-  static_for<0, P - 1>([&](auto I) { issue_pair(I, (int)I); });
-
-  int q0 = 0;
-  for (; q0 + P <= full_pairs; q0 += P) {
-    static_for<0, P>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      // pairs q0+i .. q0+i+P-2 are in flight: wait for the oldest
-      wait_vmcnt<(P - 2) * kPairCopies>();
-      barrier_only();  // every wave's copies of pair q0+i are in; pair array (i+P-1)%P is free
-      issue_pair(std::integral_constant<int, (i + P - 1) % P>{}, q0 + i + P - 1);
-      compute(pair_ptr(I) + kp * kSlot, u_begin + 2 * (q0 + i) + kp);
-    });
   }
-  // Remainder: at most P pairs, the last possibly a single unit; only the
-  // first can still need its successor issued.
-  static_for<0, P>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    if (q0 + i < n_pairs) {
-      wait_vmcnt<0>();
-      barrier_only();
-      if (q0 + i + P - 1 < n_pairs) issue_pair(std::integral_constant<int, (i + P - 1) % P>{}, q0 + i + P - 1);
-      const int u = u_begin + 2 * (q0 + i) + kp;
-      if (u < u_end) compute(pair_ptr(I) + kp * kSlot, u);
-    }
-  });
 
   // ---- k-parity reduction through LDS --------------------------------------
-  wait_vmcnt<0>();  // clamped copies past the range may still be landing
   __syncthreads();
   {
-    f32x4* red = reinterpret_cast<f32x4*>(lp0);
+    f32x4* red = reinterpret_cast<f32x4*>(wring);
     if (kp == 1) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -508,7 +549,13 @@ hipError_t launch_mt(const GemmConfig& c, const GemmArgs& a, int zero_u8, hipStr
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm) {
   (void)gs;
   GemmConfig c;
-  c.m_tiles = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  // 33..64 rows: two 32-row m-blocks per tile when that grid still fits one
+  // pass over the CUs (it needs fewer K splits, whose partial tiles are added
+  // at the end); otherwise one 64-row block, which reads the weights once.
+  static const int env_mt = env_int("PMI_GEMM_MT", 0);
+  const int64_t n_tiles = (N + kBN - 1) / kBN;
+  c.m_tiles = M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 64 && 2 * n_tiles <= device_cus() ? 2 : 4));
+  if (env_mt == 1 || env_mt == 2 || env_mt == 4) c.m_tiles = env_mt;
   const int64_t bm = 16 * c.m_tiles;
   c.grid_m = (int)((M + bm - 1) / bm);
   c.n_tiles = (int)((N + kBN - 1) / kBN);
@@ -575,6 +622,7 @@ hipError_t launch_gemm(const void* x, const uint8_t* w, const float* scales, con
   a.gs = (int)gs;
   a.splits = c.splits;
   a.n_tiles = c.n_tiles;
+  a.grid_m = c.grid_m;
   if (c.m_tiles == 1) return launch_mt<1>(c, a, zero_u8, stream);
   if (c.m_tiles == 2) return launch_mt<2>(c, a, zero_u8, stream);
   return launch_mt<4>(c, a, zero_u8, stream);

@@ -7,7 +7,7 @@ kernels for gfx950 behind libpare_amd.so:
   - M <= 16 with the activations within 64 KiB of LDS and group size % 128 == 0:
     the skinny MFMA kernel (w4a16_skinny.hip);
   - otherwise: MFMA GEMM (w4a16_gemm.hip) for group sizes that are multiples
-    of 128, or the GEMV four activation rows at a time.
+    of 128 and K % 256 == 0, or the GEMV four activation rows at a time.
 There is no CPU or PyTorch fallback: every call runs the HIP library or raises.
 """
 

@@ -59,6 +59,8 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 64) == 1     # group size not % 128
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1
+    assert L.pmi_matmul_kernel_choice(32, 4096, 384, 128) == 1     # odd group count: GEMV
+    assert L.pmi_matmul_workspace_bytes(32, 4096, 384, 128, 0) == 0
 
 
 def test_kernel_override(L):

@@ -53,14 +53,23 @@ def _kernels(asm: str) -> dict[str, str]:
 
 
 def _loops(body: str) -> list[str]:
-    """Text of each innermost loop: from its header label to the branch back to it."""
-    loops = []
-    for m in re.finditer(r"^(\.LBB\w+):\s*;\s*=>This Inner Loop Header", body, re.M):
-        label = m.group(1)
-        back = re.search(rf"s_cbranch\w*\s+{re.escape(label)}\s*$", body[m.end():], re.M)
-        assert back, f"no back-branch to {label}"
-        loops.append(body[m.end():m.end() + back.start()])
-    return loops
+    """Text of each innermost loop, gathered from the compiler's block
+    annotations ("=>This Inner Loop Header" and "in Loop: Header=BBx_y"),
+    whatever order the blocks were laid out in."""
+    loops: dict[str, list[str]] = {}
+    current = None
+    for line in body.splitlines():
+        m = re.match(r"^(?:\.L(BB\w+):|; %bb\.\d+:)(.*)$", line)
+        if m:
+            note = m.group(2)
+            if "Inner Loop Header" in note and m.group(1):
+                current = m.group(1)
+            else:
+                h = re.search(r"in Loop: Header=(BB\w+)", note)
+                current = h.group(1) if h else None
+        if current is not None:
+            loops.setdefault(current, []).append(line)
+    return ["\n".join(v) for v in loops.values()]
 
 
 def test_every_gemm_variant_compiled(gemm_asm):
@@ -69,13 +78,16 @@ def test_every_gemm_variant_compiled(gemm_asm):
     assert len(names) == 9, sorted(names)
 
 
-def test_gemm_steady_loop_never_drains_the_copy_queue(gemm_asm):
+def test_gemm_compute_loop_never_waits_for_copies(gemm_asm):
+    """The compute waves issue no copies, so their loop (the one with the MFMAs)
+    must hold no vmcnt wait at all; the producer loops wait for their own
+    copies only. Every loop crosses one barrier per step."""
     for name, body in _kernels(gemm_asm).items():
         loops = _loops(body)
-        assert loops, f"{name}: no steady-state loop found"
-        for text in loops:
-            waits = re.findall(r"s_waitcnt\s+vmcnt\((\d+)\)", text)
-            assert waits, f"{name}: steady-state loop has no vmcnt wait"
-            assert "0" not in waits, f"{name}: vmcnt(0) inside the steady-state loop"
-            assert "s_barrier" in text, f"{name}: steady-state loop lost its barrier"
-
+        mfma_loops = [t for t in loops if "v_mfma" in t]
+        assert len(mfma_loops) == 1, f"{name}: expected one compute loop, found {len(mfma_loops)}"
+        assert not re.search(r"s_waitcnt[^\n]*vmcnt", mfma_loops[0]), \
+            f"{name}: the compute loop waits on the copy queue"
+        assert "s_barrier" in mfma_loops[0], f"{name}: the compute loop lost its barrier"
+        assert any("buffer_load" in t and "s_barrier" in t for t in loops), \
+            f"{name}: no producer loop"

@@ -284,7 +284,8 @@ KERNEL_CASES = [
     ("skinny", 5, 272, 2048, 256), ("skinny", 13, 400, 1024, 128), ("skinny", 16, 272, 1024, 128),
     ("skinny", 1, 200, 18944, 128), ("skinny", 1, 1024, 14336, 128), ("skinny", 3, 64, 512, 512),
     ("gemm", 5, 1040, 1024, 128), ("gemm", 16, 4096, 4096, 128), ("gemm", 64, 520, 3584, 128),
-    ("gemm", 17, 272, 2048, 256),
+    ("gemm", 17, 272, 2048, 256), ("gemm", 48, 1040, 14336, 128), ("gemm", 96, 300, 4096, 128),
+    ("gemv", 32, 200, 384, 128),
 ]
 
 
