@@ -18,7 +18,8 @@ Printed JSON line: value = aggregate algorithmic HBM throughput (GB/s) of the
 step; "roofline" is that of the dominant kernel (the fused gate/up GEMV),
 "cpu_baseline" the reference's dequantize-on-the-fly path restated on the
 host CPU (oracle, timed on a bounded sample), "detail" per-shape µs / GB/s, the
-seven-launch step and the M=64 MFMA GEMM TFLOP/s.
+seven-launch step, the M=64 MFMA GEMM TFLOP/s and the Qwen2.5-7B act_order
+layers (g_idx from a seeded permutation, M = 1 and 16).
 
 Algorithmic bytes per call: N*K/2 (INT4 codes) + N*G*(4 + 1) (fp32 scale +
 u8 zero, the format the kernels read) + M*K*2 (x) + M*N*2 (y); FLOPs 2*M*N*K.
@@ -46,6 +47,8 @@ N_LAYERS = 32
 LLAMA = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
          ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
 FUSED = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
+# Qwen2.5-7B-shaped GPTQ act_order layers (config 4): name, N, K
+QWEN = [("q_o", 3584, 3584), ("k_v", 512, 3584), ("gate_up", 18944, 3584), ("down", 3584, 18944)]
 
 
 def log(*a):
@@ -61,8 +64,8 @@ class Buf:
     codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]; for M > 4 also
     their group-major copies (built on first use, as a module does once)."""
 
-    def __init__(self, name, w, s, z):
-        self.name, self.w, self.s, self.z = name, w, s, z
+    def __init__(self, name, w, s, z, perm=None):
+        self.name, self.w, self.s, self.z, self.perm = name, w, s, z, perm
         self.N, self.K = w.shape[0], w.shape[1] * 2
         self._gm = None
 
@@ -119,12 +122,32 @@ def launch(L, buf, x, y, M, stream):
     ws = WORKSPACE[0]
     s_gm, z_gm = buf.gm() if M > 4 else (None, None)
     rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, buf.w.data_ptr(), buf.s.data_ptr(),
-                            buf.z.data_ptr(), _lib.PMI_U8, None,
+                            buf.z.data_ptr(), _lib.PMI_U8,
+                            buf.perm.data_ptr() if buf.perm is not None else None,
                             s_gm.data_ptr() if s_gm is not None else None,
                             z_gm.data_ptr() if z_gm is not None else None, y.data_ptr(),
                             _lib.PMI_F16, M, buf.N, buf.K, GS, ws.data_ptr(), ws.numel(), stream)
     if rc != 0:
         raise RuntimeError(_lib.last_error())
+
+
+def make_act_order_layer(N, K, seed, dev):
+    """A Qwen-style act_order layer: g_idx groups a seeded permutation P of the
+    input channels by 128, so the kernel-layout weight holds columns in P order
+    (contiguous groups) and the matmul gathers X[:, P] (pare_amd's perm path)."""
+    import torch
+
+    import pare_amd as P
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = torch.randn(N, K, generator=g, device=dev) * 0.02
+    perm = torch.randperm(K, generator=g, device=dev).to(torch.int32)
+    packed, scale, zero = P.rtn_quantize(w[:, perm.long()].contiguous(), GS)
+    del w
+    buf = Buf("act_order", P.repack_int4_for_kernel(packed, GS), scale.reshape(N, K // GS),
+              P.zeros_to_u8(zero).reshape(N, K // GS), perm=perm)
+    buf.gm()
+    return buf
 
 
 def capture(fn, stream):
@@ -225,8 +248,10 @@ def main():
         return
 
     shapes = [(N, K) for _, N, K in LLAMA] + [(6144, 4096), (28672, 4096)]
-    ws_bytes = max(L.pmi_matmul_workspace_bytes(M, N, K, GS, 0)
-                   for M in (1, 2, 4, 8, 16, 32, 64, M_MAX) for N, K in shapes)
+    ws_bytes = max(max(L.pmi_matmul_workspace_bytes(M, N, K, GS, 0)
+                       for M in (1, 2, 4, 8, 16, 32, 64, M_MAX) for N, K in shapes),
+                   max(L.pmi_matmul_workspace_bytes(M, N, K, GS, 1)
+                       for M in (1, 16) for _, N, K in QWEN))
     WORKSPACE.append(torch.zeros(max(ws_bytes, 1 << 20), dtype=torch.uint8, device=dev))
 
     n_layers = args.layers
@@ -363,6 +388,31 @@ def main():
                           "GB/s": round(m64_gbs, 1), "kernel": P.kernel_choice(64, 14336, 4096, GS)}
     log(f"  gate M=64: {m64_us:.2f} us {m64_tflops:.1f} TFLOP/s {m64_gbs:.1f} GB/s")
     del gm
+
+    # --- Qwen2.5-7B act_order layers at M = 1 and 16 (config 4) ---------------
+    qwen = {}
+    for qi, (name, N, K) in enumerate(QWEN):
+        wbytes = N * K // 2
+        n_copies = int(min(48, max(8, -(-600_000_000 // wbytes))))  # > 512 MB: beyond the MALL
+        bufs = [make_act_order_layer(N, K, 7000 + 100 * qi + c, dev) for c in range(n_copies)]
+        xq = torch.randn(16, K, generator=g, device=dev).to(torch.float16)
+        yq = torch.empty(16, N, dtype=torch.float16, device=dev)
+        torch.cuda.synchronize()
+        row = {"N": N, "K": K, "copies": n_copies}
+        for M in (1, 16):
+            gq = capture(lambda s, M=M: [launch(L, b, xq, yq, M, s) for b in bufs], stream)
+            gq.replay()
+            us = time_graph(gq, 5, stream) * 1e3 / n_copies
+            byt = layer_bytes(N, K, M) + 4 * K
+            row[f"M{M}"] = {"us": round(us, 2), "GB/s": round(byt / (us * 1e-6) / 1e9, 1),
+                            "TFLOP/s": round(2 * M * N * K / (us * 1e-6) / 1e12, 2),
+                            "kernel": P.kernel_choice(M, N, K, GS)}
+            log(f"  qwen act_order {name:8s} {N:6d}x{K:6d} M={M:2d}: {row[f'M{M}']}")
+            del gq
+        qwen[name] = row
+        del bufs
+        torch.cuda.empty_cache()
+    detail["qwen_act_order"] = qwen
 
     if args.sweep:
         sweep = {}

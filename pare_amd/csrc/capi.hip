@@ -121,9 +121,12 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
 size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
                                   int has_perm) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
-  if (pmi_matmul_kernel_choice(M, N, K, group_size) != 2 || !pmi::gemm_supported(K, group_size))
-    return 0;
-  return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
+  const int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
+  if (choice == 2 && pmi::gemm_supported(K, group_size))
+    return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
+  // the GEMV reads act_order activations gathered once into the workspace
+  if (choice == 1 && has_perm) return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
+  return 0;
 }
 
 int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype, float* scales_gm,
@@ -195,9 +198,18 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   if (choice == 2)
     return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, scales_gm, zeros_gm, perm, y, M, N,
                                      K, group_size, workspace, workspace_bytes, s), fn);
-  // GEMV, four activation rows per launch.
+  // GEMV, four activation rows per launch. With act_order and room in the
+  // workspace, X[:, perm] is gathered once and the GEMV reads it directly;
+  // otherwise every wave gathers its own activation columns.
   const uint16_t* xp = (const uint16_t*)x;
   uint16_t* yp = (uint16_t*)y;
+  if (perm && workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
+    uint16_t* xg = (uint16_t*)((uint8_t*)workspace + pmi::kWsCounterBytes);
+    hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
+    if (e != hipSuccess) return from_hip(e, fn);
+    xp = xg;
+    perm = nullptr;
+  }
   for (int64_t m = 0; m < M; m += 4) {
     const int64_t mt = M - m < 4 ? M - m : 4;
     hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, perm, yp + m * N, mt, N, K,

@@ -42,6 +42,16 @@ SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
 hipError_t launch_skinny(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                          int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                          int64_t K, int64_t gs, hipStream_t stream);
+// The matmul workspace starts with a block of split-K counters that nothing
+// else writes (zero between calls); the act_order gather X[:, perm] follows it.
+constexpr size_t kWsCounterBytes = 64 * 1024;
+inline size_t ws_align(size_t v) { return (v + 255) & ~(size_t)255; }
+inline size_t ws_perm_bytes(int64_t M, int64_t K) { return ws_align((size_t)M * K * 2); }
+
+// X[:, perm] -> out (fp16 [M, K], K % 8 == 0), one pass.
+hipError_t launch_gather_cols(const void* x, const int32_t* perm, void* out, int64_t M, int64_t K,
+                              hipStream_t stream);
+
 // The MFMA GEMM runs whole 128-column groups, consumed two at a time.
 inline bool gemm_supported(int64_t K, int64_t gs) { return gs % 128 == 0 && K % 256 == 0; }
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);

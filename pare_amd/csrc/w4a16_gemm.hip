@@ -525,12 +525,10 @@ int device_cus() {
   return cus;
 }
 
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-
 // The workspace starts with a fixed block of split-K counters that nothing else
 // ever writes, so counters left at zero by one call are zero for the next one
 // whatever shapes the workspace served in between.
-constexpr size_t kCounterBytes = 64 * 1024;
+constexpr size_t kCounterBytes = kWsCounterBytes;
 constexpr int64_t kMaxCounters = kCounterBytes / 4;
 
 template <int MT>
@@ -545,6 +543,14 @@ hipError_t launch_mt(const GemmConfig& c, const GemmArgs& a, int zero_u8, hipStr
 }
 
 }  // namespace
+
+hipError_t launch_gather_cols(const void* x, const int32_t* perm, void* out, int64_t M, int64_t K,
+                              hipStream_t stream) {
+  const int64_t threads = M * (K / 8);
+  hipLaunchKernelGGL(gather_cols_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     stream, (const f16*)x, perm, (f16*)out, (int)M, (int)K);
+  return hipGetLastError();
+}
 
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm) {
   (void)gs;
@@ -569,8 +575,8 @@ GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_per
   if (s < 1 || tiles > kMaxCounters) s = 1;
   c.splits = (int)s;
   c.grid = (int)(tiles * c.splits);
-  c.ws_perm = has_perm ? align256((size_t)M * K * 2) : 0;
-  c.ws_split = c.splits > 1 ? align256((size_t)tiles * c.splits * bm * kBN * 4) : 0;
+  c.ws_perm = has_perm ? ws_perm_bytes(M, K) : 0;
+  c.ws_split = c.splits > 1 ? ws_align((size_t)tiles * c.splits * bm * kBN * 4) : 0;
   return c;
 }
 
@@ -597,10 +603,7 @@ hipError_t launch_gemm(const void* x, const uint8_t* w, const float* scales, con
   if (perm) {
     // act_order: gather X[:, perm] once into the workspace
     f16* xg = (f16*)(ws + kCounterBytes);
-    const int64_t threads = M * (K / 8);
-    hipLaunchKernelGGL(gather_cols_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       stream, xp, perm, xg, (int)M, (int)K);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_gather_cols(xp, perm, xg, M, K, stream);
     if (e != hipSuccess) return e;
     xp = xg;
   }

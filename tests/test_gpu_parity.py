@@ -409,6 +409,41 @@ def test_matmul_act_order(M, N, K, kernel):
     _check_out(y, ref, f"act_order M={M} N={N} K={K} kernel={name}")
 
 
+@pytest.mark.parametrize("M", [1, 3, 6])
+def test_gemv_act_order_gathered_equals_in_kernel_gather(M):
+    """With a workspace the GEMV reads X[:, perm] gathered once; without one each
+    wave gathers its own columns. Same products, same order: identical bits."""
+    N, K, gs = 3584, 18944, 128
+    rng = np.random.default_rng(M + 40)
+    w = _w(N, K, M + 41)
+    packed, s, z, g = O.rtn_quantize_act_order(w, rng.permutation(K), gs)
+    x = _x(M, K, 9).to(DEV)
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    sd = _cuda(s).reshape(N, K // gs).contiguous()
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    need = L.pmi_matmul_workspace_bytes(M, N, K, gs, 1)
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    with force_kernel("gemv"):
+        print(f"[case] act_order gemv gather M={M}", flush=True)
+        for wsp, nb in ((ws.data_ptr(), need), (None, 0)):
+            y = torch.empty(M, N, dtype=torch.float16, device=DEV)
+            rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
+                                    zu8.data_ptr(), _lib.PMI_U8, pm.data_ptr(), None, None,
+                                    y.data_ptr(), _lib.PMI_F16, M, N, K, gs, wsp, nb, stream)
+            assert rc == 0, _lib.last_error()
+            outs.append(y)
+    torch.cuda.synchronize()
+    assert int(ws[:65536].count_nonzero()) == 0, "the counter block must stay zero"
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    ref = O.linear_fp32(x.float().cpu().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
+    _check_out(outs[0], ref, f"act_order gemv gathered M={M}")
+
+
 @pytest.mark.parametrize("M", [16, 64])
 def test_matmul_act_order_group_major(M):
     N, K, gs = 3584, 3584, 128
