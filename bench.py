@@ -61,8 +61,9 @@ def layer_bytes(N, K, M, scale_b=4, zero_b=1):
 
 class Buf:
     """Device buffers of one INT4 launch in the kernels' format: kernel-layout
-    codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]; for M > 4 also
-    their group-major copies (built on first use, as a module does once)."""
+    codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]; for the MFMA
+    GEMM legs also their group-major copies (built once, outside graph capture,
+    as a module does per layer)."""
 
     def __init__(self, name, w, s, z, perm=None):
         self.name, self.w, self.s, self.z, self.perm = name, w, s, z, perm
@@ -120,7 +121,8 @@ def launch(L, buf, x, y, M, stream):
     assert x.shape[0] >= M and x.shape[1] == buf.K and x.is_contiguous(), "x too small for M"
     assert y.shape[0] >= M and y.shape[1] == buf.N and y.is_contiguous(), "y too small for M"
     ws = WORKSPACE[0]
-    s_gm, z_gm = buf.gm() if M > 4 else (None, None)
+    # group-major copies wherever they were built (the GEMV ignores them)
+    s_gm, z_gm = buf._gm if buf._gm is not None else (None, None)
     rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, buf.w.data_ptr(), buf.s.data_ptr(),
                             buf.z.data_ptr(), _lib.PMI_U8,
                             buf.perm.data_ptr() if buf.perm is not None else None,

@@ -113,9 +113,14 @@ int pmi_set_kernel_override(int kernel) {
 int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size) {
   const int forced = g_kernel_override.load();
   if (forced) return forced;
-  if (M <= 4) return 1;
-  if (pmi::skinny_supported(M, N, K, group_size)) return 3;
-  return pmi::gemm_supported(K, group_size) ? 2 : 1;
+  // Measured on MI355X (gate/up/down and q/k/v/o shapes): the GEMV wins up to
+  // M = 2, and up to M = 4 for N < 8192, where the GEMM's K splits cost more
+  // than its matrix cores save; the skinny kernel wins over the GEMM for
+  // N <= 8192 while the activations fit its LDS.
+  const bool gemm = pmi::gemm_supported(K, group_size);
+  if (M <= 2 || (M <= 4 && (N < 8192 || !gemm))) return 1;
+  if (M >= 5 && N <= 8192 && pmi::skinny_supported(M, N, K, group_size)) return 3;
+  return gemm ? 2 : 1;
 }
 
 size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,

@@ -48,7 +48,8 @@ def test_version(L):
 
 
 def test_kernel_choice(L):
-    # GEMV for M <= 4; skinny MFMA kernel up to M = 16 while the activations fit the LDS budget
+    # GEMV for M <= 2 (M <= 4 for N < 8192); skinny MFMA kernel up to M = 16 for
+    # N <= 8192 while the activations fit the LDS budget; MFMA GEMM otherwise
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
     assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128) == 1
     assert L.pmi_matmul_kernel_choice(8, 4096, 3072, 128) == 3
@@ -60,6 +61,12 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1
     assert L.pmi_matmul_kernel_choice(32, 4096, 384, 128) == 1     # odd group count: GEMV
+    assert L.pmi_matmul_kernel_choice(2, 14336, 4096, 128) == 1    # GEMV up to M = 2
+    assert L.pmi_matmul_kernel_choice(3, 14336, 4096, 128) == 2    # large N: GEMM from M = 3
+    assert L.pmi_matmul_kernel_choice(4, 28672, 4096, 128) == 2
+    assert L.pmi_matmul_kernel_choice(4, 28672, 4096, 64) == 1     # no GEMM for gs 64
+    assert L.pmi_matmul_kernel_choice(8, 14336, 2048, 128) == 2    # skinny only for N <= 8192
+    assert L.pmi_matmul_kernel_choice(5, 4096, 2048, 128) == 3
     assert L.pmi_matmul_workspace_bytes(32, 4096, 384, 128, 0) == 0
 
 

@@ -261,6 +261,12 @@ def test_matmul_m_sweep(M):
     _matmul_case(M, 1040, 1024, 128, 100 + M)
 
 
+@pytest.mark.parametrize("M", [3, 4, 8])
+def test_matmul_large_n_small_m(M):
+    """N >= 8192: the automatic choice moves to the MFMA GEMM from M = 3."""
+    _matmul_case(M, 9000, 1024, 128, 300 + M, zero_u8=True)
+
+
 @pytest.mark.parametrize("N,K", [(1024, 4096), (4096, 4096), (520, 3584), (96, 18944),
                                  (4096, 14336)])
 @pytest.mark.parametrize("M", [1, 4, 16])
