@@ -13,6 +13,9 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
+# PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
+ABI_VERSION = 2
+
 PMI_OK = 0
 PMI_ERR_INVALID = -1
 PMI_ERR_UNSUPPORTED = -2
