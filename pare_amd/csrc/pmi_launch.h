@@ -9,12 +9,14 @@ namespace pmi {
 
 struct GemvConfig {
   int rows_per_wave;    // U: rows per batch of one wave (x stays in registers)
+  int depth;            // D: batches in a wave's register ring (D - 1 in flight)
   int slices_per_wave;  // 1, or 2 when K needs more than 8 slices
   int slice_waves;      // waves that split one row's K range (1 slice = 2048 columns)
   int row_waves;        // waves that take different rows of the same slices
   int n_slices;         // ceil(K / 2048)
   int rows_per_wg;      // contiguous rows owned by one workgroup
   int grid;             // workgroups
+  int lds_bytes;        // per-row partials of the slice waves (0 with one slice wave)
 };
 
 struct GemmConfig {

@@ -8,28 +8,32 @@
 // them into fp16 pairs that line up with the nibble unpack, and keeps them in
 // registers for the life of the wave, together with their sum Sx.
 //
-// Arithmetic. A nibble zero-extended into an fp16 half is the subnormal
-// q * 2^-24, exact. v_dot2_f32_f16 on those halves and the activation pairs
-// gives sum x*q * 2^-24 with exact products and fp32 sums, and the group term
-// is s * (2^24 * sum x*q - z * Sx) = s * sum x*(q - z). Per 32-bit word of
-// nibbles: 7 bit ops + 4 v_dot2_f32_f16; per row two FMAs per activation row.
+// Arithmetic. A nibble masked into an fp16 half in place is a subnormal:
+// bits 0-3 give q * 2^-24, bits 4-7 give q * 2^-20, both exact.
+// v_dot2_f32_f16 on those halves and the activation pairs forms exact products
+// with fp32 sums; low and high nibbles go to separate accumulators, and the
+// group term is s * (2^24 * sum_lo + 2^20 * sum_hi - z * Sx) = s * sum x*(q - z).
+// Per 32-bit word of nibbles: 5 bit ops + 4 v_dot2_f32_f16.
 //
 // Pipeline. A workgroup is slice_waves x row_waves waves and owns a contiguous
-// range of rows. Each wave walks its rows in batches of U with a two-deep
-// software pipeline: buffer loads of batch i+1 (row offsets in SGPRs, so no
-// address VALU) are in flight while batch i is unpacked and reduced. Every
-// load is unconditional, so the compiler waits for exactly the older batch.
+// range of rows. Each wave walks its rows in batches of U through a D-deep
+// register ring: buffer loads of batch i+D-1 (row offsets in SGPRs, so no
+// address VALU) are issued before batch i is unpacked and reduced. Every load
+// is unconditional, so the compiler waits for exactly the older batch.
 //
 // Reduction. Partial sums of a batch are reduced across the 64 lanes with a
 // transpose butterfly (v_permlane32_swap / v_permlane16_swap for the two wide
-// steps, DPP row_mirror / row_half_mirror / quad_perm for the rest), then
-// across the slice waves through LDS in a fixed order: results are
-// deterministic and no workspace or atomics are used.
+// steps, DPP row_mirror / row_half_mirror / quad_perm for the rest). Waves of
+// one workgroup do not synchronise while streaming: per-row partials of the
+// slice waves wait in LDS and are added in a fixed order after one barrier at
+// the end. Results are deterministic and no workspace or atomics are used.
 //
 // Semantics follow the reference Triton kernel (pare/kernels/matmul_int4.py:
 // 105-176): w = (q - zero) * scale per group, fp32 accumulation, fp16 output.
 #include "pmi_common.h"
 #include "pmi_launch.h"
+
+#include <type_traits>
 
 namespace pmi {
 namespace {
@@ -169,12 +173,15 @@ PMI_DEV void wave_transpose_reduce(float (&v)[VP], int lane) {
 }
 
 // One batch of U weight rows for the SPW slices a lane covers. z holds the raw
-// zero point (u8 value or fp32 bits) and is converted only when used.
-template <int U, int SPW>
+// zero point (u8 value or fp32 bits) and is widened and converted only where
+// the batch is reduced: widening a u8 load where it is issued made the
+// compiler mask the loop-carried registers of the ring before the streaming
+// loop, which waits for every load in flight.
+template <int U, int SPW, bool ZU8>
 struct Batch {
   u32x4 w[SPW][U];
   float s[SPW][U];
-  uint32_t z[SPW][U];
+  typename std::conditional<ZU8, uint8_t, uint32_t>::type z[SPW][U];
 };
 
 struct Rsrc {
@@ -191,7 +198,7 @@ PMI_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
 // offset 0 (their activations are zero). Row offsets are wave-uniform and go
 // in the SGPR offset of the buffer load; lane offsets are fixed per wave.
 template <int U, int SPW, bool ZU8>
-PMI_DEV void load_batch(Batch<U, SPW>& bt, const Rsrc& rs, int first_row, int row_last,
+PMI_DEV void load_batch(Batch<U, SPW, ZU8>& bt, const Rsrc& rs, int first_row, int row_last,
                         int row_bytes, int G, const int (&boff)[SPW], const int (&grp)[SPW]) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -217,87 +224,80 @@ PMI_DEV float zero_value(uint32_t raw) {
   return __builtin_bit_cast(float, raw);
 }
 
-// Unpacks and reduces one batch, then writes its U x MT outputs.
+// Unpacks and reduces one batch. Each nibble pair of a weight word is masked
+// into an fp16x2 operand in place: low nibbles (bits 0-3 of a half) are the
+// subnormals q * 2^-24, high nibbles (bits 4-7) the subnormals q * 2^-20; both
+// stay inside the mantissa, so the values are exact and v_dot2_f32_f16 forms
+// exact products. The two scales go to separate accumulators, combined per
+// row as s * (2^24 * sum_lo + 2^20 * sum_hi - z * Sx). 5 bit ops + 4 dot2 per
+// word. After the wave reduction, lane `idx`-writers hold row u's value for
+// activation row m in v[0] (idx = u * MT + m).
 template <int MT, int U, int SPW, bool ZU8>
-PMI_DEV void finish_batch(const Batch<U, SPW>& bt, const uint32_t (&xp)[SPW][MT][16],
-                          const float (&sx)[SPW][MT], float* __restrict__ red,
-                          f16* __restrict__ y, int lane, int wave, int wr, int slice_waves,
-                          int row_waves, int batch_row0, int row_lim, int N) {
-  constexpr int V = U * MT;
-  constexpr int VP = Pow2Ceil<V>::value;
-  constexpr int LOGV = Log2<VP>::value;
-  float v[VP];
+PMI_DEV void reduce_batch(const Batch<U, SPW, ZU8>& bt, const uint32_t (&xp)[SPW][MT][16],
+                          const float (&sx)[SPW][MT], float (&out)[Pow2Ceil<U * MT>::value],
+                          int lane) {
+  constexpr int VP = Pow2Ceil<U * MT>::value;
+  float (&v)[VP] = out;
 #pragma unroll
   for (int i = 0; i < VP; ++i) v[i] = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int sp = 0; sp < SPW; ++sp) {
-      float p[MT];
+      float pl[MT], ph[MT];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) p[m] = 0.f;
+      for (int m = 0; m < MT; ++m) pl[m] = ph[m] = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t wd = bt.w[sp][u][i];
-        const uint32_t w4 = wd >> 4;
-        // (lo0,lo2) (lo1,lo3) (hi0,hi2) (hi1,hi3) as fp16 subnormals q * 2^-24
+        const uint32_t w8 = wd >> 8;
+        // (lo0,lo2) (lo1,lo3) as q * 2^-24; (hi0,hi2) (hi1,hi3) as q * 2^-20
         const f16x2 h0 = as_f16x2(wd & 0x000F000Fu);
-        const f16x2 h1 = as_f16x2((wd >> 8) & 0x000F000Fu);
-        const f16x2 h2 = as_f16x2(w4 & 0x000F000Fu);
-        const f16x2 h3 = as_f16x2((w4 >> 8) & 0x000F000Fu);
+        const f16x2 h1 = as_f16x2(w8 & 0x000F000Fu);
+        const f16x2 h2 = as_f16x2(wd & 0x00F000F0u);
+        const f16x2 h3 = as_f16x2(w8 & 0x00F000F0u);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          p[m] = dot2_acc(h0, xp[sp][m][4 * i + 0], p[m]);
-          p[m] = dot2_acc(h1, xp[sp][m][4 * i + 1], p[m]);
-          p[m] = dot2_acc(h2, xp[sp][m][4 * i + 2], p[m]);
-          p[m] = dot2_acc(h3, xp[sp][m][4 * i + 3], p[m]);
+          pl[m] = dot2_acc(h0, xp[sp][m][4 * i + 0], pl[m]);
+          pl[m] = dot2_acc(h1, xp[sp][m][4 * i + 1], pl[m]);
+          ph[m] = dot2_acc(h2, xp[sp][m][4 * i + 2], ph[m]);
+          ph[m] = dot2_acc(h3, xp[sp][m][4 * i + 3], ph[m]);
         }
       }
       const float sc = bt.s[sp][u];
-      const float s24 = sc * 16777216.0f;               // s * 2^24, exact
+      const float s24 = sc * 16777216.0f;  // s * 2^24, exact
+      const float s20 = sc * 1048576.0f;   // s * 2^20, exact
       const float sz = -sc * zero_value<ZU8>(bt.z[sp][u]);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        v[u * MT + m] = fmaf(p[m], s24, v[u * MT + m]);
-        v[u * MT + m] = fmaf(sz, sx[sp][m], v[u * MT + m]);
+        float& acc = v[u * MT + m];
+        acc = fmaf(pl[m], s24, acc);
+        acc = fmaf(ph[m], s20, acc);
+        acc = fmaf(sz, sx[sp][m], acc);
       }
     }
   }
   wave_transpose_reduce<VP>(v, lane);
-
-  const int idx = LOGV == 0 ? 0 : (lane >> (6 - LOGV));
-  const bool writer = (lane & ((64 >> LOGV) - 1)) == 0 && idx < V;
-  if (slice_waves == 1) {
-    if (writer) {
-      const int u = idx / MT, m = idx - (idx / MT) * MT;
-      const int n = batch_row0 + wr * U + u;
-      if (n < row_lim) y[(int64_t)m * N + n] = f32_to_f16_rne(v[0]);
-    }
-    return;
-  }
-  if (writer) red[wave * V + idx] = v[0];
-  __syncthreads();
-  for (int e = threadIdx.x; e < row_waves * V; e += blockDim.x) {
-    const int wr2 = e / V, id2 = e - (e / V) * V;
-    float s = 0.f;
-    for (int q = 0; q < slice_waves; ++q) s += red[(wr2 * slice_waves + q) * V + id2];
-    const int u = id2 / MT, m = id2 - (id2 / MT) * MT;
-    const int n = batch_row0 + wr2 * U + u;
-    if (n < row_lim) y[(int64_t)m * N + n] = f32_to_f16_rne(s);
-  }
 }
 
-template <int MT, int U, int SPW, bool PERM, bool ZU8>
+// Workgroup: slice_waves x row_waves waves owning rows_per_wg contiguous rows.
+// Wave (ws, wr) covers slices ws, ws + slice_waves, ... (SPW of them) of rows
+// row0 + wr*U + b*stride + u, batch b = 0, 1, ... Batches stream through a
+// D-deep register ring: batch b + D - 1 is issued before batch b is reduced,
+// so D - 1 batches stay in flight. D = 1 (no ring) is for launches in which
+// every wave holds one batch. Waves never synchronise until the end:
+// with one slice wave the results go straight to y, otherwise each wave
+// parks its per-row partial in LDS and one barrier precedes the fixed-order
+// sum over slice waves (deterministic; no atomics, no workspace).
+template <int MT, int U, int D, int SPW, bool PERM, bool ZU8>
 __global__ void __launch_bounds__(kMaxWaves * 64)
 w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   const float* __restrict__ scales, const void* __restrict__ zeros,
                   const int32_t* __restrict__ perm, f16* __restrict__ y, int N, int K, int gs,
                   int n_slices, int slice_waves, int row_waves, int rows_per_wg) {
+  extern __shared__ float part[];  // [rows_per_wg][slice_waves][MT] when slice_waves > 1
   constexpr int VP = Pow2Ceil<U * MT>::value;
-  // Double-buffered by batch parity: one barrier per batch suffices, because
-  // a wave cannot rewrite a buffer before every wave has passed the barrier
-  // of the batch in between.
-  __shared__ float red[2][kMaxWaves * VP];
+  constexpr int LOGV = Log2<VP>::value;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -317,8 +317,8 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   rs.s = make_rsrc(scales, (uint32_t)N * (uint32_t)G * 4u);
   rs.z = make_rsrc(zeros, (uint32_t)N * (uint32_t)G * (ZU8 ? 1u : 4u));
 
-  // Issue order matters: activation loads, then the first weight batch, and
-  // only then wait for the activations, so the HBM stream starts at once.
+  // Issue order matters: activation loads, then the first weight batches,
+  // and only then wait for the activations, so the HBM stream starts at once.
   // sched_barrier keeps the scheduler from sinking loads below the waits.
   int boff[SPW], grp[SPW];
   bool act[SPW];
@@ -339,93 +339,146 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
       load_x_raw<PERM>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
   }
 
-  Batch<U, SPW> a, b;
   const int my_row0 = row0 + wr * U;
   const int row_last = row_lim - 1;
-  load_batch<U, SPW, ZU8>(a, rs, my_row0, row_last, row_bytes, G, boff, grp);
-  __builtin_amdgcn_sched_barrier(0);
-
   uint32_t xp[SPW][MT][16];
   float sx[SPW][MT];
+  // Pairs the activations with the nibble order and sums each lane's 32.
+  auto setup_x = [&]() {
 #pragma unroll
-  for (int sp = 0; sp < SPW; ++sp)
+    for (int sp = 0; sp < SPW; ++sp)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      pair_x(xa[sp][m], xb[sp][m], xp[sp][m]);
-      if (!act[sp]) {
+      for (int m = 0; m < MT; ++m) {
+        pair_x(xa[sp][m], xb[sp][m], xp[sp][m]);
+        if (!act[sp]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xp[sp][m][i] = 0u;
+          for (int i = 0; i < 16; ++i) xp[sp][m][i] = 0u;
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = dot2_acc(as_f16x2(0x3C003C00u), xp[sp][m][i], acc);
+        sx[sp][m] = acc;
       }
-      float acc = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc = dot2_acc(as_f16x2(0x3C003C00u), xp[sp][m][i], acc);
-      sx[sp][m] = acc;  // sum of the lane's 32 activations
+  };
+  const int idx = LOGV == 0 ? 0 : (lane >> (6 - LOGV));
+  const bool writer = (lane & ((64 >> LOGV) - 1)) == 0 && idx < U * MT;
+  const int wu = idx / MT, wm = idx - (idx / MT) * MT;
+  // Reduces batch b and stores (or parks) its results.
+  auto finish = [&](const Batch<U, SPW, ZU8>& bt, int b) {
+    float v[VP];
+    reduce_batch<MT, U, SPW, ZU8>(bt, xp, sx, v, lane);
+    if (writer) {
+      const int lr = wr * U + b * stride + wu;  // row within the workgroup
+      if (row0 + lr < row_lim) {
+        if (slice_waves == 1)
+          y[(int64_t)wm * N + row0 + lr] = f32_to_f16_rne(v[0]);
+        else
+          part[(lr * slice_waves + ws) * MT + wm] = v[0];
+      }
     }
+  };
 
-  // Steady state: batch i+1 loads while batch i computes. The tail is
-  // peeled so that every path issues a fixed number of loads (static
-  // vmcnt waits) and no load past the last batch is made.
-  int i = 0;
-  for (; i + 2 < n_batches; i += 2) {
-    load_batch<U, SPW, ZU8>(b, rs, my_row0 + (i + 1) * stride, row_last, row_bytes, G, boff, grp);
+  if constexpr (D == 1) {
+    // No ring (the host picks it when every wave has one batch): batches go
+    // one after the other, the first load ahead of the activation setup.
+    Batch<U, SPW, ZU8> bt;
+    load_batch<U, SPW, ZU8>(bt, rs, my_row0, row_last, row_bytes, G, boff, grp);
     __builtin_amdgcn_sched_barrier(0);
-    finish_batch<MT, U, SPW, ZU8>(a, xp, sx, red[0], y, lane, wave, wr, slice_waves, row_waves,
-                                  row0 + i * stride, row_lim, N);
-    load_batch<U, SPW, ZU8>(a, rs, my_row0 + (i + 2) * stride, row_last, row_bytes, G, boff, grp);
-    __builtin_amdgcn_sched_barrier(0);
-    finish_batch<MT, U, SPW, ZU8>(b, xp, sx, red[1], y, lane, wave, wr, slice_waves, row_waves,
-                                  row0 + (i + 1) * stride, row_lim, N);
-  }
-  if (i + 1 < n_batches) {
-    load_batch<U, SPW, ZU8>(b, rs, my_row0 + (i + 1) * stride, row_last, row_bytes, G, boff, grp);
-    __builtin_amdgcn_sched_barrier(0);
-    finish_batch<MT, U, SPW, ZU8>(a, xp, sx, red[0], y, lane, wave, wr, slice_waves, row_waves,
-                                  row0 + i * stride, row_lim, N);
-    finish_batch<MT, U, SPW, ZU8>(b, xp, sx, red[1], y, lane, wave, wr, slice_waves, row_waves,
-                                  row0 + (i + 1) * stride, row_lim, N);
+    setup_x();
+    finish(bt, 0);
+    for (int b = 1; b < n_batches; ++b) {
+      load_batch<U, SPW, ZU8>(bt, rs, my_row0 + b * stride, row_last, row_bytes, G, boff, grp);
+      finish(bt, b);
+    }
   } else {
-    finish_batch<MT, U, SPW, ZU8>(a, xp, sx, red[0], y, lane, wave, wr, slice_waves, row_waves,
-                                  row0 + i * stride, row_lim, N);
+    Batch<U, SPW, ZU8> ring[D];
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      load_batch<U, SPW, ZU8>(ring[d], rs, my_row0 + d * stride, row_last, row_bytes, G, boff,
+                              grp);
+    __builtin_amdgcn_sched_barrier(0);
+    setup_x();
+    // Steady state, unrolled by D so every ring slot is a fixed register set.
+    // Each step issues its load unconditionally (past the last batch it
+    // re-reads the last row), so the wait before a reduction is always for
+    // exactly the D - 1 younger batches.
+    for (int i = 0; i < n_batches; i += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        if (i + d >= n_batches) break;
+        load_batch<U, SPW, ZU8>(ring[(d + D - 1) % D], rs, my_row0 + (i + d + D - 1) * stride,
+                                row_last, row_bytes, G, boff, grp);
+        __builtin_amdgcn_sched_barrier(0);
+        finish(ring[d], i + d);
+      }
+    }
+  }
+  if (slice_waves == 1) return;
+  __syncthreads();
+  const int nr = row_lim - row0;
+  for (int e = threadIdx.x; e < nr * MT; e += blockDim.x) {
+    const int lr = e / MT, m = e - (e / MT) * MT;
+    float s = 0.f;
+    for (int q = 0; q < slice_waves; ++q) s += part[(lr * slice_waves + q) * MT + m];
+    y[(int64_t)m * N + row0 + lr] = f32_to_f16_rne(s);
   }
 }
 
-template <int MT, int U, int SPW, bool ZU8>
+template <int MT, int U, int D, int SPW>
 hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
-                      const void* zeros, const int32_t* perm, void* y, int N, int K, int gs,
-                      hipStream_t stream) {
+                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
+                      int gs, hipStream_t stream) {
   const dim3 block(64 * c.slice_waves * c.row_waves);
-  if (perm)
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, SPW, true, ZU8>), dim3(c.grid), block, 0, stream,
-                       (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,
-                       c.slice_waves, c.row_waves, c.rows_per_wg);
-  else
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, SPW, false, ZU8>), dim3(c.grid), block, 0,
-                       stream, (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs,
-                       c.n_slices, c.slice_waves, c.row_waves, c.rows_per_wg);
+  const size_t lds = c.lds_bytes;
+#define PMI_GEMV_LAUNCH(P, Z)                                                                  \
+  hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, P, Z>), dim3(c.grid), block, lds, stream, \
+                     (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,      \
+                     c.slice_waves, c.row_waves, c.rows_per_wg)
+  if (perm) {
+    if (zero_u8) PMI_GEMV_LAUNCH(true, true);
+    else PMI_GEMV_LAUNCH(true, false);
+  } else {
+    if (zero_u8) PMI_GEMV_LAUNCH(false, true);
+    else PMI_GEMV_LAUNCH(false, false);
+  }
+#undef PMI_GEMV_LAUNCH
   return hipGetLastError();
 }
 
-template <int MT, int U, int SPW>
-hipError_t launch_z(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
-                    const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                    int gs, hipStream_t stream) {
-  if (zero_u8) return launch_cfg<MT, U, SPW, true>(c, x, w, scales, zeros, perm, y, N, K, gs, stream);
-  return launch_cfg<MT, U, SPW, false>(c, x, w, scales, zeros, perm, y, N, K, gs, stream);
-}
-
+// The (U, D) pairs instantiated: one activation row keeps one, two or four
+// rows per batch (a three-deep ring with one or two); more activation rows
+// keep a two-deep ring with one, two or (one slice per lane) four rows, and
+// only one row when a lane holds more than four activation-row slices, which
+// bounds the registers per lane. Every U but the last also comes without a
+// ring (D = 1) for launches of one batch per wave.
 template <int MT, int SPW>
-hipError_t launch_u(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
-                    const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                    int gs, hipStream_t stream) {
-  // Register budget: with more than four activation-row slices per lane a
-  // batch of one row is the most that fits without spilling.
-  if constexpr (MT * SPW > 4) {
-    return launch_z<MT, 1, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+hipError_t launch_ud(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
+                     const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
+                     int gs, hipStream_t stream) {
+#define PMI_GEMV_UD(U_, D_) \
+  if (c.rows_per_wave == U_ && c.depth == D_) \
+    return launch_cfg<MT, U_, D_, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream)
+  if constexpr (MT == 1) {
+    PMI_GEMV_UD(4, 2);
+    PMI_GEMV_UD(2, 3);
+    PMI_GEMV_UD(1, 3);
+    PMI_GEMV_UD(4, 1);
+    PMI_GEMV_UD(2, 1);
+    PMI_GEMV_UD(1, 1);
+  } else if constexpr (MT * SPW > 4) {
+    PMI_GEMV_UD(1, 2);
   } else {
-    if (c.rows_per_wave <= 2)
-      return launch_z<MT, 2, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-    return launch_z<MT, 4, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+    if constexpr (SPW == 1) {
+      PMI_GEMV_UD(4, 2);
+      PMI_GEMV_UD(4, 1);
+    }
+    PMI_GEMV_UD(2, 2);
+    PMI_GEMV_UD(1, 2);
+    PMI_GEMV_UD(2, 1);
+    PMI_GEMV_UD(1, 1);
   }
+#undef PMI_GEMV_UD
+  return hipErrorInvalidValue;  // gemv_config only yields the pairs above
 }
 
 template <int MT>
@@ -433,8 +486,8 @@ hipError_t launch_mt(const GemvConfig& c, const void* x, const uint8_t* w, const
                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
                      int gs, hipStream_t stream) {
   if (c.slices_per_wave == 2)
-    return launch_u<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-  return launch_u<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+    return launch_ud<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+  return launch_ud<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
 }
 
 int env_int(const char* name, int dflt) {
@@ -455,29 +508,73 @@ int device_cus() {
   return cus;
 }
 
+constexpr int kMaxPartBytes = 32 * 1024;  // LDS for the per-row partials
+
 }  // namespace
 
 GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
   GemvConfig c;
+  const int mt = (int)(M < 4 ? M : 4);
   const int64_t row_chunks = K / 32;
   c.n_slices = (int)((row_chunks + kSliceChunks - 1) / kSliceChunks);
   // At most 8 waves per workgroup; more than 8 slices -> two slices per wave.
   c.slices_per_wave = c.n_slices > kMaxWaves ? 2 : 1;
   c.slice_waves = (c.n_slices + c.slices_per_wave - 1) / c.slices_per_wave;
   c.row_waves = kMaxWaves / c.slice_waves;
-  // Tuning overrides (benchmark sweeps only).
+  // Rows per batch (U) and workgroups per CU, from a sweep of every built
+  // variant on MI355X at M = 1 (graph-timed, 21-64 weight copies beyond the
+  // MALL). Long rows (three or more slice waves, e.g. K = 14336): four rows,
+  // one workgroup per CU (8.6 us against 9.0 us for pairs). Otherwise by rows
+  // per CU: >= 96 (N = 28672) pairs at three per CU (14.0 us), >= 48
+  // (N = 14336) pairs at one per CU (8.5 us), >= 20 (N = 6144) single rows
+  // at two per CU (5.4 us). Fewer rows (q/o, k/v): one batch per wave, of the
+  // most rows that still give every CU a workgroup (N = 4096: four rows,
+  // 4.4 us; N = 1024: one row, 3.2 us).
+  // Tuning overrides (benchmark sweeps only), restricted to what is built.
   static const int env_u = env_int("PMI_GEMV_U", 0);
   static const int env_wr = env_int("PMI_GEMV_ROW_WAVES", 0);
   static const int env_wpc = env_int("PMI_GEMV_WG_PER_CU", 0);
+  static const int env_spw = env_int("PMI_GEMV_SPW", 0);
+  if (env_spw == 2 && c.n_slices > 1 && c.slices_per_wave == 1) {
+    c.slices_per_wave = 2;
+    c.slice_waves = (c.n_slices + 1) / 2;
+    c.row_waves = kMaxWaves / c.slice_waves;
+  }
   if (env_wr > 0 && env_wr * c.slice_waves <= kMaxWaves) c.row_waves = env_wr;
-  c.rows_per_wave = M * c.slices_per_wave > 4 ? 1 : 4;
-  if (M * c.slices_per_wave <= 4 && (env_u == 2 || env_u == 4)) c.rows_per_wave = env_u;
-  const int64_t target = (int64_t)device_cus() * (env_wpc > 0 ? env_wpc : 2);
+  const int lanes_x = mt * c.slices_per_wave;  // activation-row slices per lane
+  const int max_u = lanes_x > 4 ? 1 : (c.slices_per_wave == 1 || lanes_x <= 2 ? 4 : 2);
+  int wpc = 2;
+  const int64_t cus = device_cus();
+  const int64_t rows_per_cu = N / cus;
+  bool one_batch = false;
+  if (mt == 1 && c.slice_waves >= 3) { c.rows_per_wave = 4; wpc = 1; }
+  else if (mt == 1 && rows_per_cu >= 96) { c.rows_per_wave = 2; wpc = 3; }
+  else if (mt == 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 1; }
+  else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 1; wpc = 2; }
+  else if (mt > 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 2; }
+  else one_batch = true;
+  if (one_batch || c.rows_per_wave > max_u) {
+    c.rows_per_wave = max_u;
+    while (c.rows_per_wave > 1 &&
+           N < (int64_t)c.row_waves * c.rows_per_wave * cus * 7 / 8)
+      c.rows_per_wave /= 2;
+  }
+  if ((env_u == 1 || env_u == 2 || env_u == 4) && env_u <= max_u) c.rows_per_wave = env_u;
+  if (env_wpc > 0) wpc = env_wpc;
+  c.depth = (mt == 1 && c.rows_per_wave != 4) ? 3 : 2;
+  const int64_t target = cus * wpc;
   const int64_t stride = (int64_t)c.row_waves * c.rows_per_wave;
   int64_t rows = (N + target - 1) / target;
   if (rows < stride) rows = stride;  // every wave of a workgroup gets rows
+  if (c.slice_waves > 1) {
+    const int64_t per_row = (int64_t)c.slice_waves * mt * 4;
+    const int64_t cap = kMaxPartBytes / per_row / stride * stride;
+    if (rows > cap) rows = cap;
+  }
   c.rows_per_wg = (int)rows;
   c.grid = (int)((N + rows - 1) / rows);
+  if (rows <= stride && lanes_x <= 4) c.depth = 1;  // one batch per wave: no ring
+  c.lds_bytes = c.slice_waves > 1 ? (int)(rows * c.slice_waves * mt * 4) : 0;
   return c;
 }
 

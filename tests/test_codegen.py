@@ -91,3 +91,66 @@ def test_gemm_compute_loop_never_waits_for_copies(gemm_asm):
         assert "s_barrier" in mfma_loops[0], f"{name}: the compute loop lost its barrier"
         assert any("buffer_load" in t and "s_barrier" in t for t in loops), \
             f"{name}: no producer loop"
+
+
+# --- split-K GEMV -----------------------------------------------------------
+
+GEMV = B.CSRC / "w4a16_gemv.hip"
+
+
+@pytest.fixture(scope="module")
+def gemv_asm(tmp_path_factory) -> str:
+    cc = _hipcc()
+    if cc is None or shutil.which(cc) is None and not Path(cc).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "gemv.s"
+    flags = [f for f in B.HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+    cmd = [cc, *flags, f"-I{B.REPO_DIR / 'include'}", "--cuda-device-only", "-S", str(GEMV),
+           "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return out.read_text()
+
+
+def _gemv_kernels(asm: str) -> dict[tuple, str]:
+    """Body of every w4a16_gemv_kernel<MT, U, D, SPW, PERM, ZU8> instantiation,
+    keyed by (MT, U, D, SPW, PERM, ZU8, mangled name)."""
+    out = {}
+    pat = r"^(_ZN\S*w4a16_gemv_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELb(\d)E\S*):"
+    for m in re.finditer(pat, asm, re.M):
+        end = asm.find("s_endpgm", m.end())
+        key = tuple(int(m.group(i)) for i in range(2, 8)) + (m.group(1),)
+        out[key] = asm[m.end():end]
+    return out
+
+
+def test_gemv_ring_never_drains_before_the_stream(gemv_asm):
+    """A ring variant (D >= 2) enters its streaming loop with D - 1 batches in
+    flight. Any full wait (vmcnt(0)) before the loop header drains them, which
+    cost 1-1.5 us per gate/up launch when the compiler once masked the
+    loop-carried zero-point registers there. Left out: the in-kernel
+    act_order gather (PERM), which must wait for its permutation loads before
+    it can gather, and lanes holding more than four activation-row slices
+    (M >= 3 with K > 16384), which spill registers."""
+    kernels = _gemv_kernels(gemv_asm)
+    rings = {k: v for k, v in kernels.items() if k[2] >= 2 and k[4] == 0 and k[0] * k[3] <= 4}
+    assert len(rings) >= 16, sorted(kernels)
+    for key, body in rings.items():
+        name = key[-1]
+        head = body.split("Inner Loop Header", 1)[0]
+        assert "Inner Loop Header" in body, f"{name}: no streaming loop"
+        assert not re.search(r"s_waitcnt[^\n]*vmcnt\(0\)", head), \
+            f"{name}: waits for every load before the streaming loop"
+
+
+def test_gemv_no_spill_on_the_common_variants(gemv_asm):
+    """One and two activation rows with one slice per lane and u8 zero points
+    (every Llama and Qwen decode shape up to K = 16384) must not touch scratch
+    memory."""
+    checked = 0
+    for key, body in _gemv_kernels(gemv_asm).items():
+        mt, u, d, spw, perm, zu8, name = key
+        if mt <= 2 and spw == 1 and zu8 == 1:
+            checked += 1
+            assert "scratch_store" not in body, f"{name}: spills to scratch"
+    assert checked >= 8
