@@ -154,11 +154,12 @@ PMI_API int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float*
 
 /* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
  * 2 = MFMA GEMM (group_size % 128 == 0 and K % 256 == 0), 3 = skinny MFMA
- * kernel (M <= 16). Host-only; no reference
- * counterpart (the reference has one Triton kernel). */
+ * kernel (M <= 16), 4 = register-streamed MFMA GEMM (group_size == 128,
+ * K % 512 == 0). Host-only; no reference counterpart (the reference has one
+ * Triton kernel). */
 PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size);
 
-/* Forces pmi_matmul_w4a16 onto one kernel (1, 2 or 3 as above; 0 restores the
+/* Forces pmi_matmul_w4a16 onto one kernel (1 to 4 as above; 0 restores the
  * automatic choice) for every thread of the process; returns the previous
  * setting, or PMI_ERR_INVALID for an unknown value. A test and benchmarking
  * hook with no reference counterpart. A forced kernel that cannot run a shape

@@ -18,7 +18,8 @@ CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libpare_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
-SOURCES = ["capi.hip", "w4a16_gemv.hip", "w4a16_gemm.hip", "w4a16_skinny.hip", "w4a16_layout.hip"]
+SOURCES = ["capi.hip", "w4a16_gemv.hip", "w4a16_gemm.hip", "w4a16_gemm64.hip", "w4a16_skinny.hip",
+           "w4a16_layout.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

@@ -104,7 +104,7 @@ int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count, i
 }
 
 int pmi_set_kernel_override(int kernel) {
-  if (kernel < 0 || kernel > 3)
+  if (kernel < 0 || kernel > 4)
     return fail(PMI_ERR_INVALID, "pmi_set_kernel_override: unknown kernel %d", kernel);
   ok();
   return g_kernel_override.exchange(kernel);
@@ -120,6 +120,17 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   const bool gemm = pmi::gemm_supported(K, group_size);
   if (M <= 2 || (M <= 4 && (N < 8192 || !gemm))) return 1;
   if (M >= 5 && N <= 8192 && pmi::skinny_supported(M, N, K, group_size)) return 3;
+  // The register-streamed GEMM beats the MFMA GEMM by 3-8 % from M = 128 on
+  // (Llama and Qwen shapes up to M = 512), and at 33-64 rows when its 128-row
+  // blocks alone fill the CUs (fused gate/up at M = 64: 26.7 us against
+  // 28.4 us); with a K split at M <= 64 it loses (gate_proj at M = 64: 23.2
+  // us against 19.2 us).
+  if (pmi::gemm64_supported(M, K, group_size)) {
+    if (M > 64) return 4;
+    if (M > 32 && pmi::gemm64_config(M, N, K).splits == 1 &&
+        pmi::gemm64_config(M, N, K).grid >= 7 * pmi::device_cu_count() / 8)
+      return 4;
+  }
   return gemm ? 2 : 1;
 }
 
@@ -129,8 +140,14 @@ size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
   const int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
   if (choice == 2 && pmi::gemm_supported(K, group_size))
     return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
+  if (choice == 4 && pmi::gemm64_supported(M, K, group_size)) {
+    const size_t split = pmi::gemm64_config(M, N, K).ws_split;
+    const size_t perm = has_perm ? pmi::ws_perm_bytes(M, K) : 0;
+    return split + perm ? pmi::kWsCounterBytes + perm + split : 0;
+  }
   // the GEMV reads act_order activations gathered once into the workspace
-  if (choice == 1 && has_perm) return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
+  if ((choice == 1 || choice == 4) && has_perm)
+    return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
   return 0;
 }
 
@@ -190,6 +207,28 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     if (forced) return fail(PMI_ERR_UNSUPPORTED, "%s: forced MFMA GEMM with perm needs a workspace "
                             "of pmi_matmul_workspace_bytes() bytes", fn);
     choice = 1;
+  }
+  if (choice == 4 && !pmi::gemm64_supported(M, K, group_size))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: forced register-streamed GEMM needs group_size == 128 "
+                "and M*K*2 < 2^31", fn);
+  if (choice == 4) {
+    // act_order: X[:, perm] is gathered into the workspace first (as for the
+    // MFMA GEMM); the split-K partial tiles follow it
+    const void* xs = x;
+    size_t part_offset = pmi::kWsCounterBytes;
+    if (perm) {
+      if (workspace_bytes < pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K))
+        return fail(PMI_ERR_UNSUPPORTED, "%s: register-streamed GEMM with perm needs a workspace "
+                    "of pmi_matmul_workspace_bytes() bytes", fn);
+      void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
+      hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
+      if (e != hipSuccess) return from_hip(e, fn);
+      xs = xg;
+      part_offset += pmi::ws_perm_bytes(M, K);
+    }
+    return from_hip(pmi::launch_gemm64(xs, w, scales, zeros, zu8, scales_gm, zeros_gm, y, M, N, K,
+                                       workspace_bytes >= pmi::kWsCounterBytes ? workspace : nullptr,
+                                       workspace_bytes, part_offset, s), fn);
   }
   if (choice == 3 && !pmi::skinny_supported(M, N, K, group_size))
     return fail(PMI_ERR_UNSUPPORTED, "%s: forced skinny kernel needs M <= 16, group_size %% 128 "

@@ -37,6 +37,9 @@ struct SkinnyConfig {
   size_t lds;          // dynamic LDS bytes
 };
 
+// Compute units of the current device (cached; 256 when the query fails).
+int device_cu_count();
+
 GemvConfig gemv_config(int64_t M, int64_t N, int64_t K);
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
@@ -53,6 +56,26 @@ inline size_t ws_perm_bytes(int64_t M, int64_t K) { return ws_align((size_t)M * 
 // X[:, perm] -> out (fp16 [M, K], K % 8 == 0), one pass.
 hipError_t launch_gather_cols(const void* x, const int32_t* perm, void* out, int64_t M, int64_t K,
                               hipStream_t stream);
+
+// The register-streamed GEMM (blocks of 64 activation rows) runs whole
+// 128-column groups; its activation offsets are int32.
+inline bool gemm64_supported(int64_t M, int64_t K, int64_t gs) {
+  return gs == 128 && K % 128 == 0 && M * K * 2 < (1ll << 31);
+}
+struct Gemm64Config {
+  int n_blocks;     // 128-row weight blocks
+  int grid_m;       // 64-row activation blocks
+  int splits;       // workgroups sharing one block's K range
+  int grid;         // workgroups
+  size_t ws_split;  // workspace bytes for the partial tiles (splits > 1)
+};
+Gemm64Config gemm64_config(int64_t M, int64_t N, int64_t K);
+// workspace (nullable): zero-filled counter block first, partial tiles at
+// part_offset; too small for them -> unsplit.
+hipError_t launch_gemm64(const void* x, const uint8_t* w, const float* scales, const void* zeros,
+                         int zero_u8, const float* scales_gm, const uint8_t* zeros_gm, void* y,
+                         int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes,
+                         size_t part_offset, hipStream_t stream);
 
 // The MFMA GEMM runs whole 128-column groups, consumed two at a time.
 inline bool gemm_supported(int64_t K, int64_t gs) { return gs % 128 == 0 && K % 256 == 0; }

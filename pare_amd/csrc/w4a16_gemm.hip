@@ -95,60 +95,12 @@ struct GemmArgs {
   int M, N, K, gs, splits, n_tiles, grid_m;
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
-PMI_DEV __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
-template <int N>
-PMI_DEV void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
-}
-
-// BYTES (4 or 16) per lane from a buffer straight into LDS (buffer_load_dword /
-// _dwordx4 ... lds): lane i writes lds + BYTES*i; `lds` must be wave-uniform
-// (it is M0). The builtin only exists for the device; the host pass, which
-// only needs the kernels' launch stubs, sees an empty body.
-template <int BYTES>
-PMI_DEV void copy_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  static_assert(BYTES == 4 || BYTES == 16, "dword or dwordx4 copies");
-  if constexpr (BYTES == 16)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds, 16, voff, soff, 0, 0);
-  else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds, 4, voff, soff, 0, 0);
-#else
-  (void)r, (void)lds, (void)voff, (void)soff;
-#endif
-}
-
 template <int I, int N, class F>
 PMI_DEV void static_for(F&& f) {
   if constexpr (I < N) {
     f(std::integral_constant<int, I>{});
     static_for<I + 1, N>(f);
   }
-}
-
-// Workgroup barrier without the fence of __syncthreads(): that fence counts
-// in-flight buffer->LDS copies as pending LDS stores and would drain the whole
-// ring at every step. Callers order memory themselves (vmcnt waits before,
-// operands consumed before); the clobber keeps the compiler from moving
-// memory accesses across it.
-PMI_DEV void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
-// B operand: 8 nibbles (one run of two words) as fp16 (q - z).
-PMI_DEV f16x8 b_operand(uint32_t t0, uint32_t t1, f16x2 nz) {
-  const uint32_t K = 0x64646464u;
-  const f16x2 h0 = as_f16x2(__builtin_amdgcn_perm(K, t0, 0x04010400u)) + nz;
-  const f16x2 h1 = as_f16x2(__builtin_amdgcn_perm(K, t0, 0x04030402u)) + nz;
-  const f16x2 h2 = as_f16x2(__builtin_amdgcn_perm(K, t1, 0x04010400u)) + nz;
-  const f16x2 h3 = as_f16x2(__builtin_amdgcn_perm(K, t1, 0x04030402u)) + nz;
-  const u32x4 r = {as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3)};
-  return __builtin_bit_cast(f16x8, r);
 }
 
 // SZT: scales and zero points come from the group-major copies (one unit's

@@ -191,7 +191,7 @@ def matmul_w4a16(
     return out
 
 
-_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3}
+_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4}
 
 
 class force_kernel:
@@ -212,6 +212,6 @@ class force_kernel:
 
 
 def kernel_choice(M: int, N: int, K: int, group_size: int) -> str:
-    """'gemv', 'gemm' or 'skinny': the kernel matmul_w4a16 runs for this shape."""
+    """'gemv', 'gemm', 'skinny' or 'gemm64': the kernel matmul_w4a16 runs for this shape."""
     c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size)
-    return {1: "gemv", 2: "gemm", 3: "skinny"}[c]
+    return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64"}[c]

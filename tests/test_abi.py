@@ -60,6 +60,14 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 64) == 1     # group size not % 128
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1
+    # register-streamed GEMM: from M = 128, and at M = 33..64 when its 128-row
+    # blocks fill the CUs without a K split (fused gate/up, N = 28672)
+    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128) == 2
+    assert L.pmi_matmul_kernel_choice(64, 28672, 4096, 128) == 4
+    assert L.pmi_matmul_kernel_choice(32, 28672, 4096, 128) == 2
+    assert L.pmi_matmul_kernel_choice(128, 14336, 4096, 128) == 4
+    assert L.pmi_matmul_kernel_choice(512, 4096, 14336, 128) == 4
+    assert L.pmi_matmul_kernel_choice(128, 4096, 4096, 256) == 2   # group size 256: MFMA GEMM
     assert L.pmi_matmul_kernel_choice(32, 4096, 384, 128) == 1     # odd group count: GEMV
     assert L.pmi_matmul_kernel_choice(2, 14336, 4096, 128) == 1    # GEMV up to M = 2
     assert L.pmi_matmul_kernel_choice(3, 14336, 4096, 128) == 2    # large N: GEMM from M = 3

@@ -300,6 +300,33 @@ def test_each_kernel(kernel, M, N, K, gs):
     _matmul_case(M, N, K, gs, M * 131 + N + K, kernel=kernel)
 
 
+# The register-streamed GEMM (group size 128): one and two 32-row tiles,
+# ragged M inside a 64-row block and across blocks, ragged N, short and long
+# K including an odd number of groups (the two K waves then differ by one
+# stage), K split over up to 16 workgroups (small N) or none (large N), fp32
+# and u8 zero points, with and without the group-major scale/zero copies.
+GEMM64_CASES = [(1, 64, 512, False, False), (5, 272, 2048, True, False),
+                (17, 100, 4096, False, False), (32, 1040, 1024, True, True),
+                (33, 520, 3584, True, True), (48, 1040, 14336, False, False),
+                (64, 4096, 4096, True, True), (64, 300, 18944, True, False),
+                (65, 272, 2048, True, True), (100, 130, 1024, False, False),
+                (128, 1040, 4096, True, True), (64, 14336, 4096, True, True),
+                (40, 200, 384, True, False), (64, 128, 1152, False, True),
+                (20, 36000, 640, True, True)]
+
+
+@pytest.mark.parametrize("M,N,K,zero_u8,gm", GEMM64_CASES)
+def test_gemm64(M, N, K, zero_u8, gm):
+    _matmul_case(M, N, K, 128, M * 13 + N + K, zero_u8=zero_u8, kernel="gemm64", gm=gm)
+
+
+def test_gemm64_rejects_other_group_sizes():
+    packed, s, z = _layer(64, 1024, 256, 3)
+    w_k = P.repack_int4_for_kernel(_cuda(packed), 256)
+    with force_kernel("gemm64"), pytest.raises(RuntimeError, match="group_size == 128"):
+        P.matmul_w4a16(_x(16, 1024, 4).to(DEV), w_k, _cuda(s), _cuda(z), 256)
+
+
 @pytest.mark.parametrize("zero_u8", [False, True])
 def test_sz_group_major_bitexact(zero_u8):
     N, K, gs = 300, 1024, 128
@@ -354,7 +381,7 @@ def test_zero_input_gives_zero_output():
         assert y.abs().max().item() == 0.0
 
 
-@pytest.mark.parametrize("kernel", ["auto", "gemv", "gemm", "skinny"])
+@pytest.mark.parametrize("kernel", ["auto", "gemv", "gemm", "skinny", "gemm64"])
 def test_deterministic(kernel):
     packed, s, z = _layer(4096, 4096, 128, 9)
     w = P.repack_int4_for_kernel(_cuda(packed), 128)
@@ -395,7 +422,7 @@ def test_matmul_reference_errors():
         P.matmul_w4a16(_x(2, 512, 1).to(DEV)[:, ::2], w, _cuda(s), _cuda(z), 128)
 
 
-@pytest.mark.parametrize("kernel", ["auto", "gemv", "gemm"])
+@pytest.mark.parametrize("kernel", ["auto", "gemv", "gemm", "gemm64"])
 @pytest.mark.parametrize("M", [1, 16])
 @pytest.mark.parametrize("N,K", [(512, 3584), (3584, 3584), (200, 18944)])
 def test_matmul_act_order(M, N, K, kernel):
