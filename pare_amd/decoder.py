@@ -1,0 +1,248 @@
+"""A random-init Llama-3.1-8B-shaped decoder with every linear on the INT4 HIP
+path: the caller side of QuantizedLinear, used to measure end-to-end decode.
+
+The reference measures decode with HuggingFace ``generate`` on a quantised
+checkpoint (pare/eval/throughput.py:84-126: greedy, tok/s = batch * n_generate
+/ elapsed, elapsed including the prefill). No checkpoint can be fetched here,
+so the model is built from seeded random weights of the Llama-3.1-8B shape
+(hidden 4096, 32 heads, 8 KV heads, FFN 14336, vocab 128256), quantised with
+RTN INT4 g128 on the device. Every linear except lm_head is a QuantizedLinear
+(lm_head stays fp16, as the reference's default excludes it, pare/config.py:52);
+q/k/v and gate/up each run as one fused launch (FusedQuantizedLinear).
+Attention, RMSNorm, RoPE (plain, theta 500000; Llama 3.1's long-context
+frequency scaling changes nothing at these lengths' cost) and the KV cache are
+fp16 PyTorch-ROCm.
+
+Decode steps run as one captured HIP graph per batch size: the step reads the
+token and position from device tensors, writes its K/V at that position of a
+fixed-length cache and attends over the whole cache with a position mask, so
+every replay has the same shapes. The greedy argmax runs outside the graph.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .config import QuantConfig
+from .linear import FusedQuantizedLinear, QuantizedLinear
+from .quant import rtn_quantize
+
+
+@dataclass
+class DecoderConfig:
+    hidden: int = 4096
+    heads: int = 32
+    kv_heads: int = 8
+    ffn: int = 14336
+    vocab: int = 128256
+    layers: int = 32
+    rope_theta: float = 500000.0
+    rms_eps: float = 1e-5
+    group_size: int = 128
+    init_std: float = 0.02
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+
+def _int4_linear(n_out: int, n_in: int, gen: torch.Generator, cfg: DecoderConfig,
+                 dev: torch.device) -> QuantizedLinear:
+    w = torch.randn(n_out, n_in, generator=gen, device=dev) * cfg.init_std
+    packed, scale, zero = rtn_quantize(w, cfg.group_size)
+    del w
+    qcfg = QuantConfig(bits=4, scheme="rtn", group_size=cfg.group_size)
+    return QuantizedLinear(packed, scale, zero, qcfg, None, n_in, n_out, use_kernel=True)
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float, dev: torch.device):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim, dtype=torch.float16, device=dev))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (xf * self.weight.float()).to(x.dtype)
+
+
+def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """RoPE on the two halves of the head dimension (Llama's rotate_half)."""
+    d = x.shape[-1] // 2
+    x1, x2 = x[..., :d].float(), x[..., d:].float()
+    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg: DecoderConfig, gen: torch.Generator, dev: torch.device):
+        super().__init__()
+        h, kvd = cfg.hidden, cfg.kv_heads * cfg.head_dim
+        self.cfg = cfg
+        self.attn_norm = RMSNorm(h, cfg.rms_eps, dev)
+        self.mlp_norm = RMSNorm(h, cfg.rms_eps, dev)
+        self.qkv = FusedQuantizedLinear([_int4_linear(h, h, gen, cfg, dev),
+                                         _int4_linear(kvd, h, gen, cfg, dev),
+                                         _int4_linear(kvd, h, gen, cfg, dev)])
+        self.o = _int4_linear(h, h, gen, cfg, dev)
+        self.gate_up = FusedQuantizedLinear([_int4_linear(cfg.ffn, h, gen, cfg, dev),
+                                             _int4_linear(cfg.ffn, h, gen, cfg, dev)])
+        self.down = _int4_linear(h, cfg.ffn, gen, cfg, dev)
+
+    def forward(self, x, cos, sin, cache_k, cache_v, pos, mask, causal: bool):
+        """x [B, T, hidden]; cos/sin [T, head_dim/2]; cache_k/v [B, kv_heads,
+        L, head_dim]; pos int64 [T] cache positions of the T tokens; mask
+        (bool [L], True = attend) for decode, or None with ``causal`` for a
+        prefill that fills positions 0..T-1."""
+        cfg = self.cfg
+        B, T, _ = x.shape
+        q, k, v = self.qkv(self.attn_norm(x))
+        q = q.reshape(B, T, cfg.heads, cfg.head_dim).transpose(1, 2)
+        k = k.reshape(B, T, cfg.kv_heads, cfg.head_dim).transpose(1, 2)
+        v = v.reshape(B, T, cfg.kv_heads, cfg.head_dim).transpose(1, 2)
+        q, k = _rotate(q, cos, sin), _rotate(k, cos, sin)
+        cache_k.index_copy_(2, pos, k)
+        cache_v.index_copy_(2, pos, v)
+        if causal:
+            a = F.scaled_dot_product_attention(q, k.contiguous(), v.contiguous(), is_causal=True,
+                                               enable_gqa=True)
+        else:
+            a = F.scaled_dot_product_attention(q, cache_k, cache_v, attn_mask=mask, enable_gqa=True)
+        a = a.transpose(1, 2).reshape(B, T, cfg.hidden)
+        x = x + self.o(a)
+        g, u = self.gate_up(self.mlp_norm(x))
+        return x + self.down(F.silu(g) * u)
+
+
+class QuantizedDecoder(nn.Module):
+    """Embedding -> ``layers`` x DecoderLayer -> RMSNorm -> fp16 lm_head."""
+
+    def __init__(self, cfg: DecoderConfig, device, seed: int = 0):
+        super().__init__()
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        self.cfg = cfg
+        self.embed = nn.Parameter(
+            (torch.randn(cfg.vocab, cfg.hidden, generator=gen, device=dev) * cfg.init_std).half())
+        self.layers = nn.ModuleList([DecoderLayer(cfg, gen, dev) for _ in range(cfg.layers)])
+        self.norm = RMSNorm(cfg.hidden, cfg.rms_eps, dev)
+        self.lm_head = nn.Parameter(
+            (torch.randn(cfg.vocab, cfg.hidden, generator=gen, device=dev) * cfg.init_std).half())
+        self._graphs: dict = {}
+
+    def rope_tables(self, max_len: int):
+        cfg, dev = self.cfg, self.embed.device
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, device=dev).float()
+                                         / cfg.head_dim))
+        ang = torch.arange(max_len, device=dev).float()[:, None] * inv[None, :]
+        return ang.cos(), ang.sin()
+
+    def new_cache(self, batch: int, max_len: int):
+        cfg = self.cfg
+        shape = (batch, cfg.kv_heads, max_len, cfg.head_dim)
+        return [(torch.zeros(shape, dtype=torch.float16, device=self.embed.device),
+                 torch.zeros(shape, dtype=torch.float16, device=self.embed.device))
+                for _ in range(cfg.layers)]
+
+    def forward_tokens(self, tokens, cos, sin, cache, pos, mask, causal: bool):
+        """Logits [B, T, vocab] of ``tokens`` [B, T] at cache positions ``pos``."""
+        x = F.embedding(tokens, self.embed)
+        c, s = cos.index_select(0, pos), sin.index_select(0, pos)
+        for layer, (ck, cv) in zip(self.layers, cache):
+            x = layer(x, c, s, ck, cv, pos, mask, causal)
+        return F.linear(self.norm(x), self.lm_head)
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, n_generate: int, use_graph: bool = True):
+        """Greedy decode: returns (tokens [B, n_generate], timings). The prompt
+        [B, P] is prefilled in one pass; each decode step is one graph replay
+        (or the same ops eagerly) plus an argmax."""
+        B, P = prompt.shape
+        L = P + n_generate
+        cos, sin = self.rope_tables(L)
+        cache = self.new_cache(B, L)
+        dev = self.embed.device
+        out = torch.empty(B, n_generate, dtype=torch.long, device=dev)
+        tok = torch.empty(B, 1, dtype=torch.long, device=dev)
+        pos = torch.zeros(1, dtype=torch.long, device=dev)
+        ar = torch.arange(L, device=dev)
+        mask = torch.zeros(L, dtype=torch.bool, device=dev)
+
+        def step():
+            mask.copy_(ar <= pos)
+            return self.forward_tokens(tok, cos, sin, cache, pos, mask, False)[:, -1]
+
+        graph = None
+        if use_graph:
+            # capture on a side stream after one eager run of the same step
+            # (lazy per-layer buffers must exist before capture)
+            s = torch.cuda.Stream(dev)
+            s.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(s):
+                tok.zero_()
+                pos.fill_(P)
+                step()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=s):
+                    logits_static = step()
+            torch.cuda.current_stream(dev).wait_stream(s)
+            for ck, cv in cache:
+                ck.zero_()
+                cv.zero_()
+        torch.cuda.synchronize(dev)
+
+        t0 = time.perf_counter()
+        logits = self.forward_tokens(prompt, cos, sin, cache, torch.arange(P, device=dev), None,
+                                     True)[:, -1]
+        out[:, 0] = logits.argmax(-1)
+        torch.cuda.synchronize(dev)
+        t1 = time.perf_counter()
+        for i in range(1, n_generate):
+            tok.copy_(out[:, i - 1:i])
+            pos.fill_(P + i - 1)
+            if graph is not None:
+                graph.replay()
+                logits = logits_static
+            else:
+                logits = step()
+            out[:, i] = logits.argmax(-1)
+        torch.cuda.synchronize(dev)
+        t2 = time.perf_counter()
+        return out, {"prefill_s": t1 - t0, "decode_s": t2 - t1, "elapsed_s": t2 - t0}
+
+    def linear_bytes_per_token(self) -> int:
+        """INT4 codes + fp32 scale + u8 zero of every QuantizedLinear, plus the
+        fp16 lm_head: the bytes one decode step must stream."""
+        total = 0
+        for m in self.modules():
+            if isinstance(m, QuantizedLinear):
+                g = m.scale.numel()
+                total += m.packed_weight.numel() + g * 5
+        return total + self.lm_head.numel() * 2
+
+
+def decoder_throughput(model: QuantizedDecoder, batch: int, prompt_len: int = 512,
+                       n_generate: int = 128, seed: int = 1, warmup: int = 1) -> dict:
+    """The reference's tok/s (pare/eval/throughput.py:106-116): batch *
+    n_generate / elapsed with the prefill inside elapsed; also decode-only
+    tok/s (n_generate - 1 steps after the prefill's first token)."""
+    dev = model.embed.device
+    g = torch.Generator(device=dev).manual_seed(seed)
+    prompt = torch.randint(0, model.cfg.vocab, (1, prompt_len), generator=g, device=dev)
+    prompt = prompt.repeat(batch, 1)
+    for _ in range(warmup):
+        model.generate(prompt, n_generate)
+    toks, t = model.generate(prompt, n_generate)
+    return {"batch": batch, "prompt_len": prompt_len, "n_generate": n_generate,
+            "tokens_per_sec": round(batch * n_generate / t["elapsed_s"], 2),
+            "ms_per_token": round(t["elapsed_s"] * 1e3 / n_generate, 3),
+            "decode_tokens_per_sec": round(batch * (n_generate - 1) / t["decode_s"], 2),
+            "decode_ms_per_step": round(t["decode_s"] * 1e3 / (n_generate - 1), 3),
+            "prefill_ms": round(t["prefill_s"] * 1e3, 2),
+            "first_tokens": toks[0, :8].tolist()}
