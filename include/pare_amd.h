@@ -166,6 +166,39 @@ PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t gr
  * makes pmi_matmul_w4a16 return PMI_ERR_UNSUPPORTED. */
 PMI_API int pmi_set_kernel_override(int kernel);
 
+/* ---- Caller-side fp16 ops of the end-to-end decoder ----------------------
+ * The model around the INT4 linears, one launch each. No reference
+ * counterpart: the reference runs these parts of the model as HuggingFace
+ * PyTorch ops (pare/eval/throughput.py:84-126 times HF generate). fp32
+ * arithmetic inside; buffers 16-byte aligned. */
+
+/* h = x (+ residual); residual_out = h (residual and residual_out both or
+ * neither); y = h * rsqrt(mean(h^2) + eps) * weight. x, y [rows, dim] fp16,
+ * weight [dim] fp16; dim % 8 == 0, dim <= 8192. */
+PMI_API int pmi_add_rmsnorm_f16(const void* x, const void* residual, const void* weight, void* y,
+                                void* residual_out, int64_t rows, int64_t dim, float eps,
+                                void* stream);
+
+/* RoPE (rotate_half on the two halves of the head dim) and the KV-cache
+ * write. qkv [B*T, (H + 2*KV)*D] fp16 (fused q/k/v rows), cos/sin fp32
+ * [L, D/2], pos int64 [T] (device) cache positions of the T tokens; writes
+ * q_out [B, H, T, D] rotated and the rotated k and the v into cache_k,
+ * cache_v [B, KV, L, D]. */
+PMI_API int pmi_rope_kv_f16(const void* qkv, const float* cos, const float* sin, const int64_t* pos,
+                            void* q_out, void* cache_k, void* cache_v, int64_t B, int64_t T,
+                            int64_t H, int64_t KV, int64_t D, int64_t L, void* stream);
+
+/* One-token grouped-query attention over cache positions 0..*pos (device
+ * int64): out[b, h] = softmax(q[b, h] . k^T * scale) v with KV head h/(H/KV).
+ * q, out [B, H, 128] fp16; caches [B, KV, L, 128] fp16; H/KV <= 4. */
+PMI_API int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cache_v,
+                                     const int64_t* pos, void* out, int64_t B, int64_t H,
+                                     int64_t KV, int64_t D, int64_t L, float scale, void* stream);
+
+/* out[r, c] = silu(gate_up[r, c]) * gate_up[r, F + c]; gate_up [rows, 2F],
+ * out [rows, F] fp16; F % 8 == 0. */
+PMI_API int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64_t F, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

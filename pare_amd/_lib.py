@@ -49,6 +49,12 @@ SIGNATURES = {
     "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),
     "pmi_matmul_kernel_choice": (_i, [_i64, _i64, _i64, _i64]),
     "pmi_set_kernel_override": (_i, [_i]),
+    "pmi_add_rmsnorm_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
+    "pmi_rope_kv_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                             _vp]),
+    "pmi_decode_attention_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                      ctypes.c_float, _vp]),
+    "pmi_silu_mul_f16": (_i, [_vp, _vp, _i64, _i64, _vp]),
 }
 
 _lock = threading.Lock()

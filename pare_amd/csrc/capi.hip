@@ -302,4 +302,70 @@ int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float* scale, 
                   fn);
 }
 
+// ---- caller-side decoder ops ---------------------------------------------
+
+int pmi_add_rmsnorm_f16(const void* x, const void* residual, const void* weight, void* y,
+                        void* residual_out, int64_t rows, int64_t dim, float eps, void* stream) {
+  const char* fn = "pmi_add_rmsnorm_f16";
+  if (rows < 0 || dim <= 0 || dim % 8 != 0 || dim > 8192)
+    return fail(PMI_ERR_INVALID, "%s: need rows >= 0 and 0 < dim <= 8192, dim %% 8 == 0", fn);
+  if (rows == 0) return ok();
+  if (!x || !weight || !y || (!residual != !residual_out))
+    return fail(PMI_ERR_INVALID, "%s: null buffer (residual and residual_out go together)", fn);
+  for (const void* p : {x, residual, weight, (const void*)y, (const void*)residual_out})
+    if (p && !aligned(p, 16)) return fail(PMI_ERR_INVALID, "%s: buffers must be 16-byte aligned", fn);
+  return from_hip(pmi::launch_add_rmsnorm(x, residual, weight, y, residual_out, rows, dim, eps,
+                                          (hipStream_t)stream), fn);
+}
+
+int pmi_rope_kv_f16(const void* qkv, const float* cos_t, const float* sin_t, const int64_t* pos,
+                    void* q_out, void* cache_k, void* cache_v, int64_t B, int64_t T, int64_t H,
+                    int64_t KV, int64_t D, int64_t L, void* stream) {
+  const char* fn = "pmi_rope_kv_f16";
+  if (B < 0 || T <= 0 || H <= 0 || KV <= 0 || H % KV != 0 || D <= 0 || D % 2 != 0 || L <= 0)
+    return fail(PMI_ERR_INVALID, "%s: bad shape (B=%lld T=%lld H=%lld KV=%lld D=%lld L=%lld)", fn,
+                (long long)B, (long long)T, (long long)H, (long long)KV, (long long)D, (long long)L);
+  if (B == 0) return ok();
+  if (!qkv || !cos_t || !sin_t || !pos || !q_out || !cache_k || !cache_v)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (B * T * (H + 2 * KV) * D >= (1ll << 31) || B * KV * L * D >= (1ll << 31))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: shape too large", fn);
+  return from_hip(pmi::launch_rope_kv(qkv, cos_t, sin_t, pos, q_out, cache_k, cache_v, B, T, H,
+                                      KV, D, L, (hipStream_t)stream), fn);
+}
+
+int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cache_v,
+                             const int64_t* pos, void* out, int64_t B, int64_t H, int64_t KV,
+                             int64_t D, int64_t L, float scale, void* stream) {
+  const char* fn = "pmi_decode_attention_f16";
+  if (B < 0 || H <= 0 || KV <= 0 || H % KV != 0 || L <= 0)
+    return fail(PMI_ERR_INVALID, "%s: bad shape", fn);
+  if (D != 128 || H / KV > 4)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: needs head_dim 128 and at most 4 query heads per KV head",
+                fn);
+  const int64_t group = H / KV, span = (L + 3) / 4;
+  if ((group * 4 * span + group * 4 * (2 + D)) * 4 > 64 * 1024)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: cache length %lld too long for the LDS score buffer", fn,
+                (long long)L);
+  if (B == 0) return ok();
+  if (!q || !cache_k || !cache_v || !pos || !out) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(q, 16) || !aligned(cache_k, 16) || !aligned(cache_v, 16) || !aligned(out, 4))
+    return fail(PMI_ERR_INVALID, "%s: q and the caches must be 16-byte aligned", fn);
+  if (B * KV * L * D >= (1ll << 31)) return fail(PMI_ERR_UNSUPPORTED, "%s: cache too large", fn);
+  return from_hip(pmi::launch_decode_attention(q, cache_k, cache_v, pos, out, B, H, KV, L, scale,
+                                               (hipStream_t)stream), fn);
+}
+
+int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64_t F, void* stream) {
+  const char* fn = "pmi_silu_mul_f16";
+  if (rows < 0 || F <= 0 || F % 8 != 0)
+    return fail(PMI_ERR_INVALID, "%s: need F > 0, F %% 8 == 0", fn);
+  if (rows == 0) return ok();
+  if (!gate_up || !out) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(gate_up, 16) || !aligned(out, 16))
+    return fail(PMI_ERR_INVALID, "%s: buffers must be 16-byte aligned", fn);
+  if (rows * F * 2 >= (1ll << 31)) return fail(PMI_ERR_UNSUPPORTED, "%s: too large", fn);
+  return from_hip(pmi::launch_silu_mul(gate_up, out, rows, F, (hipStream_t)stream), fn);
+}
+
 }  // extern "C"

@@ -1,0 +1,279 @@
+// Caller-side fp16 ops of the end-to-end decoder (the model around the INT4
+// linears): residual add + RMSNorm, RoPE + KV-cache write, grouped-query
+// decode attention, SiLU-gate multiply. One launch each, so a decoder layer is
+// about ten launches (four of them INT4 linears) instead of ~50 PyTorch
+// elementwise kernels. fp32 arithmetic inside, fp16 in and out.
+//
+// None of these has a counterpart in the reference's W4A16 path: the
+// reference runs the model around QuantizedLinear with HuggingFace PyTorch
+// ops (pare/eval/throughput.py:84-126 times HF generate).
+#include "pmi_common.h"
+#include "pmi_launch.h"
+
+namespace pmi {
+namespace {
+
+PMI_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+PMI_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// h = x (+ r); r_out = h (when r is given); y = h * rsqrt(mean(h^2) + eps) * w.
+// One workgroup of 256 threads per row; dim % 8 == 0, dim <= 8192.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const f16* __restrict__ x,
+                                                          const f16* __restrict__ r,
+                                                          const f16* __restrict__ w,
+                                                          f16* __restrict__ y,
+                                                          f16* __restrict__ r_out, int dim,
+                                                          float eps) {
+  __shared__ float part[4];
+  const int row = blockIdx.x, t = threadIdx.x;
+  const f16* xr = x + (size_t)row * dim;
+  const f16* rr = r ? r + (size_t)row * dim : nullptr;
+  constexpr int kPer = 32;  // up to 8192 / 256 values per thread
+  float h[kPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer / 8; ++i) {
+    const int c = (i * 256 + t) * 8;
+    if (c < dim) {
+      const f16x8 xv = *reinterpret_cast<const f16x8*>(xr + c);
+      f16x8 hv = xv;
+      if (rr) {
+        const f16x8 rv = *reinterpret_cast<const f16x8*>(rr + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hv[e] = (f16)((float)xv[e] + (float)rv[e]);
+        *reinterpret_cast<f16x8*>(r_out + (size_t)row * dim + c) = hv;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        h[i * 8 + e] = (float)hv[e];
+        ss += h[i * 8 + e] * h[i * 8 + e];
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) part[t >> 6] = ss;
+  __syncthreads();
+  const float inv = rsqrtf((part[0] + part[1] + part[2] + part[3]) / (float)dim + eps);
+#pragma unroll
+  for (int i = 0; i < kPer / 8; ++i) {
+    const int c = (i * 256 + t) * 8;
+    if (c < dim) {
+      const f16x8 wv = *reinterpret_cast<const f16x8*>(w + c);
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (f16)(h[i * 8 + e] * inv * (float)wv[e]);
+      *reinterpret_cast<f16x8*>(y + (size_t)row * dim + c) = o;
+    }
+  }
+}
+
+// qkv: [B*T, (H + 2*KV) * D] (fused q/k/v output); token bt = b*T + t sits at
+// cache position pos[t]. Writes q_out [B, H, T, D] rotated, and the rotated k
+// and the v of every token into cache_k / cache_v [B, KV, L, D]. Rotation on
+// the two halves of D (rotate_half), cos/sin fp32 [L, D/2] indexed by position.
+// One thread per (token, head, pair i < D/2) over all H + KV heads.
+__global__ void rope_kv_kernel(const f16* __restrict__ qkv, const float* __restrict__ cos_t,
+                               const float* __restrict__ sin_t, const int64_t* __restrict__ pos,
+                               f16* __restrict__ q_out, f16* __restrict__ cache_k,
+                               f16* __restrict__ cache_v, int B, int T, int H, int KV, int D,
+                               int L) {
+  const int half = D / 2;
+  const int64_t n = (int64_t)B * T * (H + KV) * half;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int d = (int)(i % half);
+  const int hh = (int)((i / half) % (H + KV));
+  const int bt = (int)(i / ((int64_t)half * (H + KV)));
+  const int b = bt / T, t = bt - (bt / T) * T;
+  int64_t p = pos[t];
+  p = p < 0 ? 0 : (p >= L ? L - 1 : p);
+  const int row = (H + 2 * KV) * D;
+  const f16* src = qkv + (size_t)bt * row + (size_t)hh * D;
+  const float x1 = (float)src[d], x2 = (float)src[d + half];
+  const float c = cos_t[p * half + d], s = sin_t[p * half + d];
+  const f16 o1 = (f16)(x1 * c - x2 * s), o2 = (f16)(x2 * c + x1 * s);
+  if (hh < H) {
+    f16* dst = q_out + (((size_t)b * H + hh) * T + t) * D;
+    dst[d] = o1;
+    dst[d + half] = o2;
+  } else {
+    const int kh = hh - H;
+    f16* dk = cache_k + (((size_t)b * KV + kh) * L + p) * D;
+    dk[d] = o1;
+    dk[d + half] = o2;
+    const f16* sv = qkv + (size_t)bt * row + (size_t)(H + KV + kh) * D;
+    f16* dv = cache_v + (((size_t)b * KV + kh) * L + p) * D;
+    dv[d] = sv[d];
+    dv[d + half] = sv[d + half];
+  }
+}
+
+// Decode attention, one query token per sequence: out[b, h, :] = softmax(q k^T
+// * scale over cache positions 0..*pos) v, query head h reading KV head
+// h / (H / KV). One workgroup per (b, KV head); wave (g, c) takes query head
+// g of the group and quarter c of the positions (kQuarters waves per head).
+// Scores: lane-parallel over positions, each lane a full 128-dim dot product
+// (q held in registers as fp16 pairs, v_dot2_f32_f16), stored in LDS. Then
+// exp and sum in fp32, and P V with lane l owning output dims 2l, 2l+1. The
+// quarters are combined through LDS with the usual max/sum rescaling.
+constexpr int kHeadDim = 128;
+constexpr int kQuarters = 4;
+
+__global__ __launch_bounds__(1024) void decode_attention_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ cache_k, const f16* __restrict__ cache_v,
+    const int64_t* __restrict__ pos, f16* __restrict__ out, int H, int KV, int L, float scale) {
+  constexpr int D = kHeadDim;
+  extern __shared__ float smem[];  // scores [group * kQuarters][span], then partials
+  const int b = blockIdx.x / KV, kh = blockIdx.x - (blockIdx.x / KV) * KV;
+  const int group = H / KV;
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int g = wv / kQuarters, c = wv - (wv / kQuarters) * kQuarters;
+  const int64_t p = *pos;
+  const int len = (int)(p < 0 ? 1 : (p >= L ? L : p + 1));
+  const int span = (L + kQuarters - 1) / kQuarters;
+  const int j0 = c * ((len + kQuarters - 1) / kQuarters);
+  const int j1 = min(len, j0 + (len + kQuarters - 1) / kQuarters);
+  const int h = kh * group + g;
+  const f16* kb = cache_k + ((size_t)b * KV + kh) * L * D;
+  const f16* vb = cache_v + ((size_t)b * KV + kh) * L * D;
+  float* s = smem + wv * span;
+  float* partial = smem + group * kQuarters * span;  // [wave][2 + D]
+
+  // q, pre-scaled, as 64 fp16 pairs in every lane
+  uint32_t qp[D / 2];
+  {
+    const u32x4* q4 = reinterpret_cast<const u32x4*>(q + ((size_t)b * H + h) * D);
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+      const u32x4 v = q4[i];
+      qp[4 * i] = v.x; qp[4 * i + 1] = v.y; qp[4 * i + 2] = v.z; qp[4 * i + 3] = v.w;
+    }
+  }
+  float mx = -INFINITY;
+  for (int j = j0 + l; j < j1; j += 64) {
+    const u32x4* k4 = reinterpret_cast<const u32x4*>(kb + (size_t)j * D);
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+      const u32x4 kv = k4[i];
+      d = dot2_acc(as_f16x2(kv.x), qp[4 * i], d);
+      d = dot2_acc(as_f16x2(kv.y), qp[4 * i + 1], d);
+      d = dot2_acc(as_f16x2(kv.z), qp[4 * i + 2], d);
+      d = dot2_acc(as_f16x2(kv.w), qp[4 * i + 3], d);
+    }
+    d *= scale;
+    s[j - j0] = d;
+    mx = fmaxf(mx, d);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int j = j0 + l; j < j1; j += 64) {
+    const float e = mx == -INFINITY ? 0.f : __expf(s[j - j0] - mx);
+    s[j - j0] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  float a0 = 0.f, a1 = 0.f;
+  for (int j = j0; j < j1; ++j) {
+    const float pj = s[j - j0];
+    const f16x2 v2 = *reinterpret_cast<const f16x2*>(vb + (size_t)j * D + 2 * l);
+    a0 = fmaf(pj, (float)v2[0], a0);
+    a1 = fmaf(pj, (float)v2[1], a1);
+  }
+  float* mine = partial + wv * (2 + D);
+  if (l == 0) {
+    mine[0] = mx;
+    mine[1] = sum;
+  }
+  mine[2 + 2 * l] = a0;
+  mine[3 + 2 * l] = a1;
+  __syncthreads();
+  if (c != 0) return;
+  float m = -INFINITY;
+#pragma unroll
+  for (int qq = 0; qq < kQuarters; ++qq) m = fmaxf(m, partial[(wv + qq) * (2 + D)]);
+  float tot = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int qq = 0; qq < kQuarters; ++qq) {
+    const float* pq = partial + (wv + qq) * (2 + D);
+    const float f = pq[0] == -INFINITY ? 0.f : __expf(pq[0] - m);
+    tot = fmaf(pq[1], f, tot);
+    o0 = fmaf(pq[2 + 2 * l], f, o0);
+    o1 = fmaf(pq[3 + 2 * l], f, o1);
+  }
+  const float inv = 1.f / tot;
+  f16x2 o;
+  o[0] = (f16)(o0 * inv);
+  o[1] = (f16)(o1 * inv);
+  *reinterpret_cast<f16x2*>(out + ((size_t)b * H + h) * D + 2 * l) = o;
+}
+
+// out[r, c] = silu(gu[r, c]) * gu[r, F + c] for c < F.
+__global__ void silu_mul_kernel(const f16* __restrict__ gu, f16* __restrict__ out, int rows,
+                                int F) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= (int64_t)rows * F) return;
+  const int r = (int)(i / F), c = (int)(i - (i / F) * F);
+  const f16x8 g = *reinterpret_cast<const f16x8*>(gu + (size_t)r * 2 * F + c);
+  const f16x8 u = *reinterpret_cast<const f16x8*>(gu + (size_t)r * 2 * F + F + c);
+  f16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float gf = (float)g[e];
+    const float sg = (float)(f16)(gf / (1.f + __expf(-gf)));
+    o[e] = (f16)(sg * (float)u[e]);
+  }
+  *reinterpret_cast<f16x8*>(out + (size_t)r * F + c) = o;
+}
+
+}  // namespace
+
+hipError_t launch_add_rmsnorm(const void* x, const void* r, const void* w, void* y, void* r_out,
+                              int64_t rows, int64_t dim, float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, stream, (const f16*)x,
+                     (const f16*)r, (const f16*)w, (f16*)y, (f16*)r_out, (int)dim, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv(const void* qkv, const float* cos_t, const float* sin_t,
+                          const int64_t* pos, void* q_out, void* cache_k, void* cache_v,
+                          int64_t B, int64_t T, int64_t H, int64_t KV, int64_t D, int64_t L,
+                          hipStream_t stream) {
+  const int64_t n = B * T * (H + KV) * (D / 2);
+  hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     (const f16*)qkv, cos_t, sin_t, pos, (f16*)q_out, (f16*)cache_k,
+                     (f16*)cache_v, (int)B, (int)T, (int)H, (int)KV, (int)D, (int)L);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
+                                   const int64_t* pos, void* out, int64_t B, int64_t H,
+                                   int64_t KV, int64_t L, float scale, hipStream_t stream) {
+  const int group = (int)(H / KV);
+  const int span = (int)((L + kQuarters - 1) / kQuarters);
+  const size_t lds = ((size_t)group * kQuarters * span + (size_t)group * kQuarters * (2 + kHeadDim)) * 4;
+  hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)(B * KV)),
+                     dim3(64 * group * kQuarters), lds, stream, (const f16*)q,
+                     (const f16*)cache_k, (const f16*)cache_v, pos, (f16*)out, (int)H, (int)KV,
+                     (int)L, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const void* gu, void* out, int64_t rows, int64_t F,
+                           hipStream_t stream) {
+  const int64_t n = rows * F / 8;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     (const f16*)gu, (f16*)out, (int)rows, (int)F);
+  return hipGetLastError();
+}
+
+}  // namespace pmi

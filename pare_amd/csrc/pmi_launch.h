@@ -101,6 +101,18 @@ hipError_t launch_sz_group_major(const float* scales, const void* zeros, int zer
                                  float* scales_gm, uint8_t* zeros_gm, int32_t* bad, int64_t N,
                                  int64_t G, hipStream_t stream);
 
+// Caller-side decoder ops (decode_ops.hip).
+hipError_t launch_add_rmsnorm(const void* x, const void* r, const void* w, void* y, void* r_out,
+                              int64_t rows, int64_t dim, float eps, hipStream_t stream);
+hipError_t launch_rope_kv(const void* qkv, const float* cos_t, const float* sin_t,
+                          const int64_t* pos, void* q_out, void* cache_k, void* cache_v,
+                          int64_t B, int64_t T, int64_t H, int64_t KV, int64_t D, int64_t L,
+                          hipStream_t stream);
+hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
+                                   const int64_t* pos, void* out, int64_t B, int64_t H,
+                                   int64_t KV, int64_t L, float scale, hipStream_t stream);
+hipError_t launch_silu_mul(const void* gu, void* out, int64_t rows, int64_t F, hipStream_t stream);
+
 hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,
                          int64_t K, int64_t gs, hipStream_t stream);
 

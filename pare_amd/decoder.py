@@ -9,14 +9,19 @@ so the model is built from seeded random weights of the Llama-3.1-8B shape
 RTN INT4 g128 on the device. Every linear except lm_head is a QuantizedLinear
 (lm_head stays fp16, as the reference's default excludes it, pare/config.py:52);
 q/k/v and gate/up each run as one fused launch (FusedQuantizedLinear).
-Attention, RMSNorm, RoPE (plain, theta 500000; Llama 3.1's long-context
-frequency scaling changes nothing at these lengths' cost) and the KV cache are
-fp16 PyTorch-ROCm.
+Activations, the KV cache and lm_head are fp16; RoPE is the plain form with
+theta 500000 (Llama 3.1's long-context frequency scaling changes no cost at
+these lengths); prefill attention is PyTorch's fp16 SDPA.
 
 Decode steps run as one captured HIP graph per batch size: the step reads the
 token and position from device tensors, writes its K/V at that position of a
-fixed-length cache and attends over the whole cache with a position mask, so
-every replay has the same shapes. The greedy argmax runs outside the graph.
+fixed-length cache and attends over the cache up to that position, so every
+replay has the same shapes. The greedy argmax runs outside the graph.
+
+With ``fused_ops`` (the default) the ops around the linears are the library's
+caller-side kernels: residual add + RMSNorm, RoPE + KV-cache write, grouped-
+query decode attention and SiLU-gate multiply, one launch each. With
+``fused_ops=False`` they are plain PyTorch ops (the check in the tests).
 """
 
 from __future__ import annotations
@@ -29,7 +34,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from .config import QuantConfig
+from .kernels import _stream_handle
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .quant import rtn_quantize
 
@@ -80,6 +87,59 @@ def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tens
     return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
 
 
+def rope_tables(head_dim: int, theta: float, max_len: int, device):
+    """cos, sin fp32 [max_len, head_dim/2] of the RoPE angles pos * theta^(-2i/d)."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
+    ang = torch.arange(max_len, device=device).float()[:, None] * inv[None, :]
+    return ang.cos(), ang.sin()
+
+
+def _check(rc: int, fn: str) -> None:
+    _lib.check(rc, fn)
+
+
+def add_rmsnorm(x: torch.Tensor, r: torch.Tensor | None, w: torch.Tensor, eps: float):
+    """(norm(x + r) * w, x + r) in one launch; r None: (norm(x) * w, x)."""
+    dim = x.shape[-1]
+    y = torch.empty_like(x)
+    h = torch.empty_like(x) if r is not None else x
+    _check(_lib.lib().pmi_add_rmsnorm_f16(
+        x.data_ptr(), r.data_ptr() if r is not None else None, w.data_ptr(), y.data_ptr(),
+        h.data_ptr() if r is not None else None, x.numel() // dim, dim, eps,
+        _stream_handle(x.device)), "pmi_add_rmsnorm_f16")
+    return y, h
+
+
+def rope_kv(qkv, cos, sin, pos, cache_k, cache_v, B, T, H, KV, D):
+    """Rotated q [B, H, T, D]; rotated k and v written into the caches at pos."""
+    q = torch.empty(B, H, T, D, dtype=torch.float16, device=qkv.device)
+    _check(_lib.lib().pmi_rope_kv_f16(
+        qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), q.data_ptr(),
+        cache_k.data_ptr(), cache_v.data_ptr(), B, T, H, KV, D, cache_k.shape[2],
+        _stream_handle(qkv.device)), "pmi_rope_kv_f16")
+    return q
+
+
+def decode_attention(q, cache_k, cache_v, pos, scale: float):
+    """q [B, H, 1, D] against cache positions 0..pos -> [B, H, D]."""
+    B, H, _, D = q.shape
+    out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
+    _check(_lib.lib().pmi_decode_attention_f16(
+        q.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), pos.data_ptr(), out.data_ptr(), B, H,
+        cache_k.shape[1], D, cache_k.shape[2], scale, _stream_handle(q.device)),
+        "pmi_decode_attention_f16")
+    return out
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up of a fused [.., 2F] gate/up output."""
+    F2 = gu.shape[-1]
+    out = torch.empty(*gu.shape[:-1], F2 // 2, dtype=torch.float16, device=gu.device)
+    _check(_lib.lib().pmi_silu_mul_f16(gu.data_ptr(), out.data_ptr(), gu.numel() // F2, F2 // 2,
+                                       _stream_handle(gu.device)), "pmi_silu_mul_f16")
+    return out
+
+
 class DecoderLayer(nn.Module):
     def __init__(self, cfg: DecoderConfig, gen: torch.Generator, dev: torch.device):
         super().__init__()
@@ -119,15 +179,38 @@ class DecoderLayer(nn.Module):
         g, u = self.gate_up(self.mlp_norm(x))
         return x + self.down(F.silu(g) * u)
 
+    def forward_fused(self, h, d, cos_t, sin_t, cache_k, cache_v, pos, causal: bool):
+        """The same layer on the library's fused ops. The residual stream is
+        carried as (h, d) with d the previous layer's pending output (None for
+        the first layer): each residual add happens inside the next RMSNorm.
+        cos_t/sin_t are the full [L, head_dim/2] tables (indexed by pos on the
+        device). Returns the new (h, d)."""
+        cfg = self.cfg
+        B, T, _ = h.shape
+        n1, h = add_rmsnorm(h, d, self.attn_norm.weight, cfg.rms_eps)
+        qkv = self.qkv.fused(n1)
+        q = rope_kv(qkv, cos_t, sin_t, pos, cache_k, cache_v, B, T, cfg.heads, cfg.kv_heads,
+                    cfg.head_dim)
+        if causal:
+            a = F.scaled_dot_product_attention(q, cache_k[:, :, :T], cache_v[:, :, :T],
+                                               is_causal=True, enable_gqa=True)
+            a = a.transpose(1, 2).reshape(B, T, cfg.hidden)
+        else:
+            a = decode_attention(q, cache_k, cache_v, pos, 1.0 / math.sqrt(cfg.head_dim))
+            a = a.reshape(B, 1, cfg.hidden)
+        n2, h = add_rmsnorm(h, self.o(a), self.mlp_norm.weight, cfg.rms_eps)
+        return h, self.down(silu_mul(self.gate_up.fused(n2)))
+
 
 class QuantizedDecoder(nn.Module):
     """Embedding -> ``layers`` x DecoderLayer -> RMSNorm -> fp16 lm_head."""
 
-    def __init__(self, cfg: DecoderConfig, device, seed: int = 0):
+    def __init__(self, cfg: DecoderConfig, device, seed: int = 0, fused_ops: bool = True):
         super().__init__()
         dev = torch.device(device)
         gen = torch.Generator(device=dev).manual_seed(seed)
         self.cfg = cfg
+        self.fused_ops = fused_ops
         self.embed = nn.Parameter(
             (torch.randn(cfg.vocab, cfg.hidden, generator=gen, device=dev) * cfg.init_std).half())
         self.layers = nn.ModuleList([DecoderLayer(cfg, gen, dev) for _ in range(cfg.layers)])
@@ -137,11 +220,7 @@ class QuantizedDecoder(nn.Module):
         self._graphs: dict = {}
 
     def rope_tables(self, max_len: int):
-        cfg, dev = self.cfg, self.embed.device
-        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, device=dev).float()
-                                         / cfg.head_dim))
-        ang = torch.arange(max_len, device=dev).float()[:, None] * inv[None, :]
-        return ang.cos(), ang.sin()
+        return rope_tables(self.cfg.head_dim, self.cfg.rope_theta, max_len, self.embed.device)
 
     def new_cache(self, batch: int, max_len: int):
         cfg = self.cfg
@@ -151,8 +230,15 @@ class QuantizedDecoder(nn.Module):
                 for _ in range(cfg.layers)]
 
     def forward_tokens(self, tokens, cos, sin, cache, pos, mask, causal: bool):
-        """Logits [B, T, vocab] of ``tokens`` [B, T] at cache positions ``pos``."""
+        """Logits [B, T, vocab] of ``tokens`` [B, T] at cache positions ``pos``
+        (a prefill, ``causal``, writes positions 0..T-1)."""
         x = F.embedding(tokens, self.embed)
+        if self.fused_ops:
+            d = None
+            for layer, (ck, cv) in zip(self.layers, cache):
+                x, d = layer.forward_fused(x, d, cos, sin, ck, cv, pos, causal)
+            n, _ = add_rmsnorm(x, d, self.norm.weight, self.cfg.rms_eps)
+            return F.linear(n, self.lm_head)
         c, s = cos.index_select(0, pos), sin.index_select(0, pos)
         for layer, (ck, cv) in zip(self.layers, cache):
             x = layer(x, c, s, ck, cv, pos, mask, causal)
@@ -175,7 +261,8 @@ class QuantizedDecoder(nn.Module):
         mask = torch.zeros(L, dtype=torch.bool, device=dev)
 
         def step():
-            mask.copy_(ar <= pos)
+            if not self.fused_ops:
+                mask.copy_(ar <= pos)
             return self.forward_tokens(tok, cos, sin, cache, pos, mask, False)[:, -1]
 
         graph = None

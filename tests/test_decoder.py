@@ -8,12 +8,13 @@ import pytest
 import torch
 
 import pare_amd as P
-from pare_amd.decoder import DecoderConfig, QuantizedDecoder, decoder_throughput
+from pare_amd.decoder import (DecoderConfig, QuantizedDecoder, add_rmsnorm, decode_attention,
+                              decoder_throughput, rope_kv, rope_tables, silu_mul)
 
 pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda:0")
-SMALL = DecoderConfig(hidden=512, heads=8, kv_heads=2, ffn=1024, vocab=2000, layers=2)
+SMALL = DecoderConfig(hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=2000, layers=2)
 
 
 def _set_kernel(model, on: bool):
@@ -78,3 +79,93 @@ def test_throughput_report(model):
     r = decoder_throughput(model, batch=2, prompt_len=32, n_generate=8, warmup=0)
     print(f"[decoder] {r}", flush=True)
     assert r["tokens_per_sec"] > 0 and r["decode_tokens_per_sec"] >= r["tokens_per_sec"] * 0.5
+
+
+def test_fused_ops_match_torch_ops(model):
+    """The library's caller-side ops (fused_ops=True) against the same model
+    on plain PyTorch ops: prefill logits and greedy tokens."""
+    g = torch.Generator(device=DEV).manual_seed(21)
+    toks = torch.randint(0, SMALL.vocab, (2, 30), generator=g, device=DEV)
+    cos, sin = model.rope_tables(30)
+    pos = torch.arange(30, device=DEV)
+    with torch.no_grad():
+        a = model.forward_tokens(toks, cos, sin, model.new_cache(2, 30), pos, None, True).float()
+        model.fused_ops = False
+        try:
+            b = model.forward_tokens(toks, cos, sin, model.new_cache(2, 30), pos, None, True).float()
+            ref_toks, _ = model.generate(toks[:, :12], 10, use_graph=False)
+        finally:
+            model.fused_ops = True
+        got_toks, _ = model.generate(toks[:, :12], 10, use_graph=True)
+    err = (a - b).abs().max().item()
+    print(f"[decoder] fused vs torch ops: max_abs={err:.3e}; tokens {got_toks[0].tolist()} "
+          f"vs {ref_toks[0].tolist()}", flush=True)
+    assert err <= 1e-2 + 1e-2 * b.abs().max().item()
+    assert (got_toks == ref_toks).float().mean().item() >= 0.9
+
+
+# --- the caller-side ops against fp32 PyTorch ---------------------------------
+
+@pytest.mark.parametrize("rows,dim,resid", [(1, 4096, False), (3, 4096, True), (7, 1024, True)])
+def test_add_rmsnorm(rows, dim, resid):
+    g = torch.Generator(device=DEV).manual_seed(rows * dim)
+    x = torch.randn(rows, dim, generator=g, device=DEV).half()
+    r = torch.randn(rows, dim, generator=g, device=DEV).half() if resid else None
+    w = (1 + 0.1 * torch.randn(dim, generator=g, device=DEV)).half()
+    y, h = add_rmsnorm(x, r, w, 1e-5)
+    hh = (x + r) if resid else x
+    hf = hh.float()
+    ref = hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5) * w.float()
+    assert torch.equal(h, hh)
+    assert (y.float() - ref).abs().max().item() <= 2e-3 * ref.abs().max().item() + 1e-3
+
+
+@pytest.mark.parametrize("B,T", [(1, 1), (2, 5)])
+def test_rope_kv(B, T):
+    H, KV, D, L = 8, 2, 128, 16
+    g = torch.Generator(device=DEV).manual_seed(B * 10 + T)
+    qkv = torch.randn(B * T, (H + 2 * KV) * D, generator=g, device=DEV).half()
+    cos_t, sin_t = rope_tables(D, 500000.0, L, DEV)
+    pos = torch.arange(3, 3 + T, device=DEV)
+    ck = torch.zeros(B, KV, L, D, dtype=torch.float16, device=DEV)
+    cv = torch.zeros_like(ck)
+    q = rope_kv(qkv, cos_t, sin_t, pos, ck, cv, B, T, H, KV, D)
+    x = qkv.view(B, T, H + 2 * KV, D).float()
+    c, s = cos_t[pos][None, :, None, :], sin_t[pos][None, :, None, :]
+    rot = torch.cat([x[..., :64] * c - x[..., 64:] * s, x[..., 64:] * c + x[..., :64] * s], -1)
+    assert (q.float() - rot[:, :, :H].transpose(1, 2)).abs().max().item() <= 2e-3
+    assert (ck[:, :, 3:3 + T].float() - rot[:, :, H:H + KV].transpose(1, 2)).abs().max().item() <= 2e-3
+    assert torch.equal(cv[:, :, 3:3 + T], qkv.view(B, T, H + 2 * KV, D)[:, :, H + KV:].transpose(1, 2))
+    assert ck[:, :, :3].abs().max().item() == 0 and ck[:, :, 3 + T:].abs().max().item() == 0
+
+
+@pytest.mark.parametrize("B,H,KV,L,p", [(1, 32, 8, 640, 511), (4, 32, 8, 640, 639), (2, 8, 2, 100, 0),
+                                        (3, 4, 4, 300, 77)])
+def test_decode_attention(B, H, KV, L, p):
+    D = 128
+    g = torch.Generator(device=DEV).manual_seed(B * L + p)
+    q = torch.randn(B, H, 1, D, generator=g, device=DEV).half()
+    ck = torch.randn(B, KV, L, D, generator=g, device=DEV).half()
+    cv = torch.randn(B, KV, L, D, generator=g, device=DEV).half()
+    pos = torch.full((1,), p, dtype=torch.long, device=DEV)
+    out = decode_attention(q, ck, cv, pos, 1 / D ** 0.5)
+    # fp32 reference over positions 0..p, each query head on its KV head
+    grp = H // KV
+    kf = ck[:, :, :p + 1].float().repeat_interleave(grp, dim=1)
+    vf = cv[:, :, :p + 1].float().repeat_interleave(grp, dim=1)
+    sc = (q.float() * (1 / D ** 0.5)) @ kf.transpose(-1, -2).contiguous()
+    ref = (torch.softmax(sc, -1) @ vf)[:, :, 0]
+    err = (out.float() - ref).abs().max().item()
+    print(f"[attn] B={B} H={H} KV={KV} L={L} p={p}: max_abs={err:.3e}", flush=True)
+    assert err <= 5e-3
+
+
+@pytest.mark.parametrize("rows,F", [(1, 14336), (4, 1024)])
+def test_silu_mul(rows, F):
+    g = torch.Generator(device=DEV).manual_seed(rows + F)
+    gu = torch.randn(rows, 2 * F, generator=g, device=DEV).half()
+    got = silu_mul(gu)
+    gf = gu.float()
+    ref = torch.nn.functional.silu(gf[:, :F]) * gf[:, F:]
+    err = (got.float() - ref).abs() / (ref.abs() + 1e-3)
+    assert err.max().item() <= 2e-3, err.max().item()
