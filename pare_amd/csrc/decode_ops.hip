@@ -123,8 +123,9 @@ __global__ void rope_kv_kernel(const f16* __restrict__ qkv, const float* __restr
 // g of the group and quarter c of the positions (kQuarters waves per head).
 // Scores: lane-parallel over positions, each lane a full 128-dim dot product
 // (q held in registers as fp16 pairs, v_dot2_f32_f16), stored in LDS. Then
-// exp and sum in fp32, and P V with lane l owning output dims 2l, 2l+1. The
-// quarters are combined through LDS with the usual max/sum rescaling.
+// exp and sum in fp32, and P V with lanes split over positions and 8-dim
+// chunks of V. The quarters are combined through LDS with the usual max/sum
+// rescaling.
 constexpr int kHeadDim = 128;
 constexpr int kQuarters = 4;
 
@@ -182,20 +183,46 @@ __global__ __launch_bounds__(1024) void decode_attention_kernel(
     sum += e;
   }
   sum = wave_sum(sum);
-  float a0 = 0.f, a1 = 0.f;
-  for (int j = j0; j < j1; ++j) {
-    const float pj = s[j - j0];
-    const f16x2 v2 = *reinterpret_cast<const f16x2*>(vb + (size_t)j * D + 2 * l);
-    a0 = fmaf(pj, (float)v2[0], a0);
-    a1 = fmaf(pj, (float)v2[1], a1);
+  // P V: lane (ps = l / 16, dc = l % 16) accumulates output dims 8dc..8dc+7
+  // over positions j = ps (mod 4), 16 positions per round and two rounds of
+  // 16-byte loads in flight; the four position groups are then added with
+  // cross-lane shuffles.
+  const int ps = l >> 4, dc = l & 15;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int jb = j0; jb < j1; jb += 32) {
+    u32x4 vv[8];
+    float pp[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = jb + 4 * k + ps;
+      const bool ok = j < j1;
+      const int jj = ok ? j : j0;
+      vv[k] = *reinterpret_cast<const u32x4*>(vb + (size_t)jj * D + 8 * dc);
+      pp[k] = ok ? s[jj - j0] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const f16x8 h8 = __builtin_bit_cast(f16x8, vv[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(pp[k], (float)h8[e], acc[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    acc[e] += __shfl_xor(acc[e], 16);
+    acc[e] += __shfl_xor(acc[e], 32);
   }
   float* mine = partial + wv * (2 + D);
   if (l == 0) {
     mine[0] = mx;
     mine[1] = sum;
   }
-  mine[2 + 2 * l] = a0;
-  mine[3 + 2 * l] = a1;
+  if (l < 16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mine[2 + 8 * dc + e] = acc[e];
+  }
   __syncthreads();
   if (c != 0) return;
   float m = -INFINITY;
