@@ -18,8 +18,10 @@ Printed JSON line: value = aggregate algorithmic HBM throughput (GB/s) of the
 step; "roofline" is that of the dominant kernel (the fused gate/up GEMV),
 "cpu_baseline" the reference's dequantize-on-the-fly path restated on the
 host CPU (oracle, timed on a bounded sample), "detail" per-shape µs / GB/s, the
-seven-launch step, the M=64 MFMA GEMM TFLOP/s and the Qwen2.5-7B act_order
-layers (g_idx from a seeded permutation, M = 1 and 16).
+seven-launch step, the M=64 MFMA GEMM TFLOP/s, the Qwen2.5-7B act_order
+layers (g_idx from a seeded permutation, M = 1 and 16)
+and the end-to-end decoder (configs[4]: 512-token prompt, 128 greedy tokens at
+batch 1 and 4, the reference's tok/s definition).
 
 Algorithmic bytes per call: N*K/2 (INT4 codes) + N*G*(4 + 1) (fp32 scale +
 u8 zero, the format the kernels read) + M*K*2 (x) + M*N*2 (y); FLOPs 2*M*N*K.
@@ -221,6 +223,7 @@ def main():
     ap.add_argument("--kernel-only", choices=["gate_up_m1", "gate_m64", "copy"], default=None,
                     help="run only one kernel loop (for rocprofv3 counter passes)")
     ap.add_argument("--sweep", action="store_true", help="also run the gate_proj M sweep")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoder leg")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -415,6 +418,29 @@ def main():
         del bufs
         torch.cuda.empty_cache()
     detail["qwen_act_order"] = qwen
+
+    # --- end-to-end decoder (config 5): tok/s at BS 1 and 4 -----------------
+    if not args.no_e2e:
+        from pare_amd.decoder import DecoderConfig, QuantizedDecoder, decoder_throughput
+
+        t0 = time.time()
+        model = QuantizedDecoder(DecoderConfig(), dev, seed=0)
+        torch.cuda.synchronize()
+        e2e = {"model": "random-init Llama-3.1-8B shape (32 layers, hidden 4096, 32/8 heads, "
+                        "FFN 14336, vocab 128256), every linear but lm_head INT4 g128 on the HIP "
+                        "path, fp16 lm_head/embeddings/KV cache",
+               "definition": "tokens_per_sec = batch * n_generate / elapsed, elapsed including "
+                             "the 512-token prefill (pare/eval/throughput.py:106-116)",
+               "bytes_per_token": model.linear_bytes_per_token()}
+        log(f"e2e model built in {time.time() - t0:.1f}s")
+        for bs in (1, 4):
+            r = decoder_throughput(model, batch=bs, prompt_len=512, n_generate=128)
+            e2e[f"bs{bs}"] = r
+            log(f"  e2e BS={bs}: {r['tokens_per_sec']} tok/s, {r['decode_ms_per_step']} ms/step "
+                f"decode, prefill {r['prefill_ms']} ms")
+        detail["e2e_decoder"] = e2e
+        del model
+        torch.cuda.empty_cache()
 
     if args.sweep:
         sweep = {}

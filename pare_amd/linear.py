@@ -110,23 +110,40 @@ class QuantizedLinear(nn.Module):
         weight = self.dequantize(dtype=x.dtype)
         return F.linear(x, weight, self.bias)
 
+    def _stamp(self):
+        return (self.packed_weight.device, self.packed_weight.data_ptr(),
+                self.packed_weight._version, self.zero._version, self.scale._version)
+
+    def _build_kernel_cache(self, w_kernel: torch.Tensor | None):
+        gs = self._group_size()
+        perm = None
+        if self.g_idx is not None:
+            perm = perm_from_g_idx(self.g_idx.to(self.packed_weight.device), gs)
+        if w_kernel is None:
+            w_kernel = repack_int4_for_kernel(self.packed_weight, gs, perm=perm)
+        self._packed_weight_kernel = w_kernel
+        zero_u8 = zeros_to_u8(self.zero)
+        self._kernel_cache = (self._stamp(), zero_u8, perm, sz_group_major(self.scale, zero_u8))
+
     def _kernel_buffers(self):
         """Kernel-layout weight, u8 zeros, group-major scales/zeros and the
         act_order permutation, built once per (device, weight contents) like
         linear.py:148-151."""
-        stamp = (self.packed_weight.device, self.packed_weight.data_ptr(),
-                 self.packed_weight._version, self.zero._version, self.scale._version)
         cache = getattr(self, "_kernel_cache", None)
-        if cache is None or cache[0] != stamp:
-            gs = self._group_size()
-            perm = None
-            if self.g_idx is not None:
-                perm = perm_from_g_idx(self.g_idx.to(self.packed_weight.device), gs)
-            self._packed_weight_kernel = repack_int4_for_kernel(self.packed_weight, gs, perm=perm)
-            zero_u8 = zeros_to_u8(self.zero)
-            cache = (stamp, zero_u8, perm, sz_group_major(self.scale, zero_u8))
-            self._kernel_cache = cache
+        if cache is None or cache[0] != self._stamp():
+            self._build_kernel_cache(None)
+            cache = self._kernel_cache
         return self._packed_weight_kernel, cache[1], cache[2], cache[3]
+
+    def adopt_kernel_layout(self, w_kernel: torch.Tensor) -> None:
+        """Uses a stored kernel-layout weight of this layer (the output of
+        ``repack_int4_for_kernel``, with the act_order permutation when the
+        layer has g_idx) instead of repacking on the first forward."""
+        if (w_kernel.dtype != torch.uint8 or w_kernel.shape != self.packed_weight.shape
+                or w_kernel.device != self.packed_weight.device):
+            raise ValueError("kernel-layout weight must be uint8 with the packed weight's shape "
+                             "and device")
+        self._build_kernel_cache(w_kernel.contiguous())
 
     def _forward_kernel(self, x: torch.Tensor) -> torch.Tensor:
         """pare/layers/linear.py:140-159 with the HIP kernels."""
