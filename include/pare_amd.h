@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 2
+#define PMI_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -86,6 +86,33 @@ PMI_API int pmi_repack_int4_for_kernel(const uint8_t* packed, uint8_t* out, cons
  * Replaces: the per-call zeros.float() of _to_2d   pare/kernels/matmul_int4.py:219-228 */
 PMI_API int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count,
                     int64_t count, void* stream);
+
+/* AWQ-GEMM checkpoint tensors -> the buffers above, one device pass each.
+ * qweight int32 [K, N/8] and qzeros int32 [G, N/8] hold eight 4-bit codes per
+ * word along N: column 8c + order[i] in bits 4i..4i+3 of word c, order =
+ * [0,2,4,6,1,3,5,7]; scales fp16 [G, N]. Writes packed (storage layout,
+ * u8 [N, K/2], 16-byte aligned), scale and zero (fp32 [N, G]; the zeros are
+ * the integer codes). Lossless: the AWQ convention is w = (q - z) * s, the
+ * same affine form. Requires N % 8 == 0, K % group_size == 0,
+ * group_size % 32 == 0 (group_size = K for one group per row).
+ * No reference counterpart in this direction: it inverts
+ * _pack_awq / _to_awq_linear   pare/model/export_awq.py:37-49,75-94, so an
+ * AWQ-GEMM checkpoint (the format vLLM and AutoAWQ load) runs on this path. */
+PMI_API int pmi_awq_gemm_to_storage(const int32_t* qweight, const int32_t* qzeros,
+                                    const void* scales, uint8_t* packed, float* scale, float* zero,
+                                    int64_t N, int64_t K, int64_t group_size, void* stream);
+
+/* The reverse: storage layout + scale fp32 [N,G] + zero (PMI_F32 or PMI_U8
+ * [N,G]) -> qweight, qzeros (int32, AWQ order) and scales fp16 [G, N] (round to
+ * nearest even). fp32 zeros are rounded half-to-even first, as the reference
+ * does; a zero outside [0,15] after rounding is added to *bad_count (device
+ * int32, nullable) and packed as 0 (the reference's shift would spill it
+ * into the neighbouring nibble). Same shape rules as above.
+ * Replaces: _to_awq_linear (qweight, qzeros, scales)   pare/model/export_awq.py:75-94 */
+PMI_API int pmi_storage_to_awq_gemm(const uint8_t* packed, const float* scale, const void* zero,
+                                    int zero_dtype, int32_t* qweight, int32_t* qzeros,
+                                    void* scales, int32_t* bad_count, int64_t N, int64_t K,
+                                    int64_t group_size, void* stream);
 
 /* [N,G] scales (fp32) and zero points (PMI_F32 or PMI_U8) -> group-major
  * copies scales_gm fp32 [G,N] and zeros_gm u8 [G,N], for pmi_matmul_w4a16.

@@ -15,7 +15,8 @@ is also the CPU baseline timed by ``bench.py``.
 Each function cites the reference file:line it follows (paths relative to the
 reference repository root). Pinning of every function — by the reference's
 own known-answer tests, closed forms, invariants and brute force — lives in
-``tests/test_oracle.py``; no function here is "parity unpinned".
+``tests/test_oracle.py`` (the AWQ-GEMM functions: ``tests/test_awq.py``); no
+function here is "parity unpinned".
 """
 
 from __future__ import annotations
@@ -68,6 +69,55 @@ def permute_columns_packed(packed: np.ndarray, perm: np.ndarray) -> np.ndarray:
     """Storage-layout weights with columns reordered as q[:, perm] (act_order
     extension; the reference has no g_idx, see pare/schemes/gptq.py:196-201)."""
     return pack_int4(unpack_int4(packed)[:, np.asarray(perm)])
+
+
+# ---------------------------------------------------------------------------
+# AWQ-GEMM int32 layout (pare/model/export_awq.py)
+# ---------------------------------------------------------------------------
+
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)   # export_awq.py:37-39
+
+
+def pack_awq(x: np.ndarray) -> np.ndarray:
+    """[..., N] codes in [0,15] -> [..., N//8] int32: element 8c + AWQ_ORDER[i]
+    goes to bits 4i..4i+3 of word c (export_awq.py:42-49)."""
+    x = np.asarray(x).astype(np.int64)
+    x = x.reshape(*x.shape[:-1], x.shape[-1] // 8, 8)
+    out = np.zeros(x.shape[:-1], dtype=np.int64)
+    for i, o in enumerate(AWQ_ORDER):
+        out |= x[..., o] << (4 * i)
+    return out.astype(np.uint32).view(np.int32)
+
+
+def unpack_awq(w: np.ndarray) -> np.ndarray:
+    """Inverse of pack_awq for codes in [0,15]: [..., C] int32 -> [..., 8C]."""
+    u = np.asarray(w).view(np.uint32).astype(np.int64)
+    out = np.empty((*u.shape, 8), dtype=np.int32)
+    for i, o in enumerate(AWQ_ORDER):
+        out[..., o] = (u >> (4 * i)) & 0xF
+    return out.reshape(*u.shape[:-1], -1)
+
+
+def to_awq_gemm(packed: np.ndarray, scale: np.ndarray, zero: np.ndarray):
+    """Storage-layout packed [N, K/2] + scale, zero [N, G] -> (qweight int32
+    [K, N/8], qzeros int32 [G, N/8], scales fp16 [G, N]) (export_awq.py:75-94:
+    zeros rounded half-to-even, scales cast to fp16)."""
+    N = packed.shape[0]
+    q = unpack_int4(packed).reshape(N, -1)
+    z = np.rint(np.asarray(zero, dtype=np.float32).reshape(N, -1)).astype(np.int64)
+    s = np.asarray(scale, dtype=np.float32).reshape(N, -1)
+    with np.errstate(over="ignore"):   # |s| >= 65520 becomes +-inf, as torch's .half()
+        s16 = s.T.astype(np.float16)
+    return pack_awq(q.T), pack_awq(z.T), s16
+
+
+def from_awq_gemm(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray):
+    """AWQ-GEMM tensors -> (packed storage layout [N, K/2], scale fp32 [N, G],
+    zero fp32 [N, G]); inverts to_awq_gemm up to the fp16 scales."""
+    q = unpack_awq(qweight).T              # [N, K]
+    z = unpack_awq(qzeros).T.astype(np.float32)
+    s = np.asarray(scales, dtype=np.float16).T.astype(np.float32)
+    return pack_int4(q), np.ascontiguousarray(s), np.ascontiguousarray(z)
 
 
 # ---------------------------------------------------------------------------

@@ -103,6 +103,51 @@ int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count, i
                   fn);
 }
 
+namespace {
+int check_awq(int64_t N, int64_t K, int64_t gs, const char* fn) {
+  if (int rc = check_shape(N, K, gs, fn)) return rc;
+  if (N % 8 != 0)
+    return fail(PMI_ERR_INVALID, "%s: N=%lld must be divisible by 8 (eight columns per int32)",
+                fn, (long long)N);
+  return PMI_OK;
+}
+}  // namespace
+
+int pmi_awq_gemm_to_storage(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                            uint8_t* packed, float* scale, float* zero, int64_t N, int64_t K,
+                            int64_t group_size, void* stream) {
+  const char* fn = "pmi_awq_gemm_to_storage";
+  if (int rc = check_awq(N, K, group_size, fn)) return rc;
+  if (N == 0) return ok();
+  if (!qweight || !qzeros || !scales || !packed || !scale || !zero)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(qweight, 4) || !aligned(qzeros, 4) || !aligned(scales, 2) || !aligned(scale, 4) ||
+      !aligned(zero, 4) || !aligned(packed, 16))
+    return fail(PMI_ERR_INVALID, "%s: misaligned buffer (packed needs 16 bytes)", fn);
+  return from_hip(pmi::launch_awq_to_storage(qweight, qzeros, scales, packed, scale, zero, N, K,
+                                             group_size, (hipStream_t)stream),
+                  fn);
+}
+
+int pmi_storage_to_awq_gemm(const uint8_t* packed, const float* scale, const void* zero,
+                            int zero_dtype, int32_t* qweight, int32_t* qzeros, void* scales,
+                            int32_t* bad_count, int64_t N, int64_t K, int64_t group_size,
+                            void* stream) {
+  const char* fn = "pmi_storage_to_awq_gemm";
+  if (int rc = check_awq(N, K, group_size, fn)) return rc;
+  if (int rc = check_zero_dtype(zero_dtype, fn)) return rc;
+  if (N == 0) return ok();
+  if (!qweight || !qzeros || !scales || !packed || !scale || !zero)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(qweight, 4) || !aligned(qzeros, 4) || !aligned(scales, 2) || !aligned(scale, 4) ||
+      !aligned(zero, zero_dtype == PMI_F32 ? 4 : 1) || !aligned(packed, 16))
+    return fail(PMI_ERR_INVALID, "%s: misaligned buffer (packed needs 16 bytes)", fn);
+  return from_hip(pmi::launch_storage_to_awq(packed, scale, zero, zero_dtype == PMI_U8, qweight,
+                                             qzeros, scales, bad_count, N, K, group_size,
+                                             (hipStream_t)stream),
+                  fn);
+}
+
 int pmi_set_kernel_override(int kernel) {
   if (kernel < 0 || kernel > 4)
     return fail(PMI_ERR_INVALID, "pmi_set_kernel_override: unknown kernel %d", kernel);

@@ -119,6 +119,15 @@ hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* per
 hipError_t launch_zeros_to_u8(const float* zeros, uint8_t* out, int32_t* bad, int64_t count,
                               hipStream_t stream);
 
+// AWQ-GEMM int32 layout <-> storage layout + fp32 [N,G] scales and zeros.
+hipError_t launch_awq_to_storage(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                                 uint8_t* packed, float* scale, float* zero, int64_t N, int64_t K,
+                                 int64_t gs, hipStream_t stream);
+hipError_t launch_storage_to_awq(const uint8_t* packed, const float* scale, const void* zero,
+                                 int zero_u8, int32_t* qweight, int32_t* qzeros, void* scales,
+                                 int32_t* bad, int64_t N, int64_t K, int64_t gs,
+                                 hipStream_t stream);
+
 hipError_t launch_dequant(const uint8_t* w, int layout, const float* scales, const void* zeros,
                           int zero_u8, const int32_t* idx, void* out, int out_dtype, int64_t N,
                           int64_t K, int64_t gs, hipStream_t stream);

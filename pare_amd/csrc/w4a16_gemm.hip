@@ -56,7 +56,6 @@ constexpr int kProducers = 4;           // copy-issuing waves per workgroup
 constexpr int kNT = 4;                  // 16-row weight tiles per compute wave
 constexpr int kBN = 128;                // weight rows per workgroup
 constexpr int kThreads = (kWaves + kProducers) * 64;
-constexpr int kWBytes = kBN * 64;       // weight bytes of one unit
 constexpr int kSBytes = kBN * 4;        // scales of one unit
 constexpr int kZBytes = kBN * 4;        // zero-point words of one unit
 

@@ -140,6 +140,121 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, int layout,
   }
 }
 
+// AWQ-GEMM int32 words (pare/model/export_awq.py:37-49): word c of a row packs
+// output columns 8c..8c+7, column 8c + order[i] in bits 4i..4i+3 with
+// order = [0,2,4,6,1,3,5,7]. awq_slot(o) is the inverse: the nibble index of
+// column 8c + o.
+PMI_DEV int awq_slot(int o) { return (o >> 1) | ((o & 1) << 2); }
+
+// qweight int32 [K, N/8] -> storage layout u8 [N, K/2]. One thread per
+// (32-column block kb of K, word column c): 32 coalesced word loads down K,
+// then eight 16-byte row writes (rows 8c..8c+7, bytes 16kb..16kb+15).
+__global__ void awq_to_storage_kernel(const int32_t* __restrict__ qweight,
+                                      uint8_t* __restrict__ packed, int64_t N, int64_t K) {
+  const int64_t NC = N >> 3;
+  const int64_t total = (K >> 5) * NC;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t kb = idx / NC, c = idx - kb * NC;
+    const int32_t* src = qweight + (kb << 5) * NC + c;
+    uint32_t out[8][4];
+#pragma unroll
+    for (int o = 0; o < 8; ++o)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) out[o][s] = 0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t w = (uint32_t)src[(int64_t)(8 * s + t) * NC];
+#pragma unroll
+        for (int o = 0; o < 8; ++o) out[o][s] |= ((w >> (4 * awq_slot(o))) & 0xFu) << (4 * t);
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      u32x4 v = {out[o][0], out[o][1], out[o][2], out[o][3]};
+      *reinterpret_cast<u32x4*>(packed + (8 * c + o) * (K >> 1) + (kb << 4)) = v;
+    }
+  }
+}
+
+// qzeros int32 [G, N/8], scales fp16 [G, N] -> zero, scale fp32 [N, G].
+__global__ void awq_sz_to_rows_kernel(const int32_t* __restrict__ qzeros,
+                                      const f16* __restrict__ scales, float* __restrict__ scale,
+                                      float* __restrict__ zero, int64_t N, int64_t G) {
+  const int64_t NC = N >> 3;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < G * NC;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t g = idx / NC, c = idx - g * NC;
+    const uint32_t z = (uint32_t)qzeros[idx];
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      const int64_t n = 8 * c + o;
+      zero[n * G + g] = (float)((z >> (4 * awq_slot(o))) & 0xFu);
+      scale[n * G + g] = (float)scales[g * N + n];
+    }
+  }
+}
+
+// Storage layout u8 [N, K/2] -> qweight int32 [K, N/8]; the inverse of
+// awq_to_storage_kernel with the same thread mapping (coalesced word stores).
+__global__ void storage_to_awq_kernel(const uint8_t* __restrict__ packed,
+                                      int32_t* __restrict__ qweight, int64_t N, int64_t K) {
+  const int64_t NC = N >> 3;
+  const int64_t total = (K >> 5) * NC;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t kb = idx / NC, c = idx - kb * NC;
+    u32x4 in[8];
+#pragma unroll
+    for (int o = 0; o < 8; ++o)
+      in[o] = *reinterpret_cast<const u32x4*>(packed + (8 * c + o) * (K >> 1) + (kb << 4));
+    int32_t* dst = qweight + (kb << 5) * NC + c;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int o = 0; o < 8; ++o)
+        w |= ((in[o][t >> 3] >> (4 * (t & 7))) & 0xFu) << (4 * awq_slot(o));
+      dst[(int64_t)t * NC] = (int32_t)w;
+    }
+  }
+}
+
+// zero (PMI_F32 or PMI_U8) and scale fp32 [N, G] -> qzeros int32 [G, N/8] and
+// scales fp16 [G, N]. fp32 zeros are rounded half-to-even first
+// (pare/model/export_awq.py:85); a zero outside [0, 15] after rounding is
+// counted in *bad and packed as 0.
+__global__ void awq_sz_from_rows_kernel(const float* __restrict__ scale,
+                                        const void* __restrict__ zero, int zero_u8,
+                                        int32_t* __restrict__ qzeros, f16* __restrict__ scales,
+                                        int32_t* __restrict__ bad, int64_t N, int64_t G) {
+  const int64_t NC = N >> 3;
+  int local_bad = 0;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < G * NC;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t g = idx / NC, c = idx - g * NC;
+    uint32_t w = 0;
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      const int64_t n = 8 * c + o;
+      uint32_t z;
+      if (zero_u8) {
+        z = ((const uint8_t*)zero)[n * G + g];
+      } else {
+        const float r = rintf(((const float*)zero)[n * G + g]);
+        z = (r >= 0.f && r <= 15.f) ? (uint32_t)(int)r : 16u;  // NaN -> 16
+      }
+      local_bad += z <= 15u ? 0 : 1;
+      w |= (z <= 15u ? z : 0u) << (4 * awq_slot(o));
+      scales[g * N + n] = f32_to_f16_rne(scale[n * G + g]);
+    }
+    qzeros[idx] = (int32_t)w;
+  }
+  if (bad && local_bad) atomicAdd(bad, local_bad);
+}
+
 template <int IN>
 PMI_DEV float load_as_f32(const void* p, int64_t i) {
   if constexpr (IN == PMI_F32) {
@@ -243,6 +358,31 @@ hipError_t launch_sz_group_major(const float* scales, const void* zeros, int zer
                                  int64_t G, hipStream_t stream) {
   hipLaunchKernelGGL(sz_group_major_kernel, dim3(grid_for(N * G)), dim3(kBlock), 0, stream, scales,
                      zeros, zero_u8, scales_gm, zeros_gm, bad, N, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_awq_to_storage(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                                 uint8_t* packed, float* scale, float* zero, int64_t N, int64_t K,
+                                 int64_t gs, hipStream_t stream) {
+  hipLaunchKernelGGL(awq_to_storage_kernel, dim3(grid_for((K / 32) * (N / 8))), dim3(kBlock), 0,
+                     stream, qweight, packed, N, K);
+  if (hipError_t e = hipGetLastError()) return e;
+  const int64_t G = K / gs;
+  hipLaunchKernelGGL(awq_sz_to_rows_kernel, dim3(grid_for(G * (N / 8))), dim3(kBlock), 0, stream,
+                     qzeros, (const f16*)scales, scale, zero, N, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_storage_to_awq(const uint8_t* packed, const float* scale, const void* zero,
+                                 int zero_u8, int32_t* qweight, int32_t* qzeros, void* scales,
+                                 int32_t* bad, int64_t N, int64_t K, int64_t gs,
+                                 hipStream_t stream) {
+  hipLaunchKernelGGL(storage_to_awq_kernel, dim3(grid_for((K / 32) * (N / 8))), dim3(kBlock), 0,
+                     stream, packed, qweight, N, K);
+  if (hipError_t e = hipGetLastError()) return e;
+  const int64_t G = K / gs;
+  hipLaunchKernelGGL(awq_sz_from_rows_kernel, dim3(grid_for(G * (N / 8))), dim3(kBlock), 0, stream,
+                     scale, zero, zero_u8, qzeros, (f16*)scales, bad, N, G);
   return hipGetLastError();
 }
 
