@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 3
+#define PMI_ABI_VERSION 4
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -172,12 +172,53 @@ PMI_API int pmi_dequant_w4a16(const uint8_t* w, int layout, const float* scales,
 /* RTN INT4 quantisation of W[N,K] (fp32, fp16 or bf16) with per-group
  * min/max scales: writes packed (storage layout, u8 [N,K/2]), scale and zero
  * (fp32 [N, K/group_size]). sym=0: asymmetric; sym=1: the reference's
- * symmetric rule on the unsigned grid. Use group_size = K for per-channel.
+ * symmetric rule on the unsigned grid (zero 0: negative weights clamp to code
+ * 0); sym=2: offset-8 symmetric (zero 8, scale = 2 max|w| / 15, no reference
+ * counterpart). Use group_size = K for per-channel.
  * Replaces: compute_scale(..., per_group) + quantize_tensor + pack_int4
  *           pare/core/scale.py:24-137, pare/core/functional.py:46-75,
  *           pare/core/pack.py:29-48, as called by pare/schemes/rtn.py:46-65 */
 PMI_API int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
                      int64_t N, int64_t K, int64_t group_size, int sym, void* stream);
+
+/* ---- GPTQ producer ---------------------------------------------------------
+ * The device half of one GPTQ layer (pare/schemes/gptq.py:156-263). The host
+ * computes the upper Cholesky factor C of the damped (and, with act_order,
+ * permuted) inverse Hessian, calls pmi_gptq_block once per 128-column block
+ * and applies the lazy update W[:, b0+count:] -= E^T C[b0:b0+count, b0+count:]
+ * with a GEMM between blocks, then packs with pmi_gptq_pack. */
+
+/* scale[n*G + g], zero[n*G + g] for every row n from w[n*ldw + col0 ..
+ * col0 + cols - 1] (fp32), with the min/max rule of pmi_rtn_quantize (sym 0,
+ * 1 or 2). Used for groups formed in processing order (act_order with g_idx,
+ * AutoGPTQ desc_act), whose scale comes from the partly updated W.
+ * Replaces: compute_scale on one group   pare/core/scale.py:24-137 */
+PMI_API int pmi_gptq_group_params(const float* w, int64_t ldw, int64_t N, int64_t col0,
+                                  int64_t cols, int sym, float* scale, float* zero, int64_t G,
+                                  int64_t g, void* stream);
+
+/* The column loop of one block, columns b0 .. b0 + count - 1 of w (fp32
+ * [N, K], row-major, 16-byte aligned; w is read, not written). For each
+ * column j in order: q = clamp(rint(w / s + z), 0, 15) with s, z the
+ * scale/zero [N, G] of group colg[j] (int32 [K]; values are clamped into
+ * [0, G)); e = (w - (q - z) s) / C[j, j]; then w[:, j'] -= e * C[j, j'] for
+ * every later column j' of the block, one column at a time. c: fp32 [K, K]
+ * row-major. Writes codes[j*N + n] (u8, column-major [K, N]) and errors[(j-b0)*N
+ * + n] (fp32 [count, N]). b0 and count are multiples of 16, count <= 128.
+ * Replaces: the loop of _gptq_one_layer   pare/schemes/gptq.py:218-249 */
+PMI_API int pmi_gptq_block(const float* w, const float* c, const int32_t* colg,
+                           const float* scale, const float* zero, uint8_t* codes, float* errors,
+                           int64_t N, int64_t K, int64_t G, int64_t b0, int64_t count,
+                           void* stream);
+
+/* codes (u8 [K, N], processed column order) -> packed (storage layout
+ * u8 [N, K/2], original column order): column k was processed at step
+ * inv_perm[k] (int32 [K], nullable = identity; out-of-range entries read
+ * step k). K % 8 == 0.
+ * Replaces: Q_int[:, invperm] + pack_int4   pare/schemes/gptq.py:258-261,
+ *           pare/core/pack.py:29-48 */
+PMI_API int pmi_gptq_pack(const uint8_t* codes, const int32_t* inv_perm, uint8_t* packed,
+                          int64_t N, int64_t K, void* stream);
 
 /* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
  * 2 = MFMA GEMM (group_size % 128 == 0 and K % 256 == 0), 3 = skinny MFMA

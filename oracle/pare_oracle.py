@@ -206,7 +206,15 @@ def rtn_quantize(w: np.ndarray, group_size: int = 128, sym: bool = False,
     """RTN producer (pare/schemes/rtn.py:46-65 + QuantizedLinear.__init__
     linear.py:74-89): returns (packed u8 [N,K/2], scale f32, zero f32)."""
     w = np.asarray(w, dtype=np.float32)
-    scale, zero = compute_scale(w, granularity, group_size, sym)
+    if sym == "offset8":   # symmetric with zero 8 (offset8_scale_zero), per group
+        N, K = w.shape
+        gs = group_size if granularity == "per_group" else K
+        scale, zero = offset8_scale_zero(w.reshape(N, K // gs, gs))
+        scale, zero = scale[..., None], zero[..., None]
+        if granularity != "per_group":
+            scale, zero = scale.reshape(N, 1), zero.reshape(N, 1)
+    else:
+        scale, zero = compute_scale(w, granularity, group_size, sym)
     q = quantize_tensor(w, scale, zero).reshape(w.shape)
     return pack_int4(q), scale, zero
 
@@ -222,7 +230,7 @@ def gidx_from_perm(perm: np.ndarray, group_size: int) -> np.ndarray:
 
 def rtn_quantize_act_order(w: np.ndarray, perm: np.ndarray, group_size: int = 128):
     """Quantise W[:, P] with contiguous groups, return q in the original column
-    order plus g_idx (the layout of BASELINE config 4): (packed, scale, zero, g_idx)."""
+    order plus g_idx (the act_order layout): (packed, scale, zero, g_idx)."""
     w = np.asarray(w, dtype=np.float32)
     perm = np.asarray(perm)
     wp = w[:, perm]
@@ -231,6 +239,156 @@ def rtn_quantize_act_order(w: np.ndarray, perm: np.ndarray, group_size: int = 12
     q = np.empty_like(qp)
     q[:, perm] = qp
     return pack_int4(q), scale, zero, gidx_from_perm(perm, group_size)
+
+
+# ---------------------------------------------------------------------------
+# GPTQ (pare/schemes/gptq.py, pare/calibration/hessian.py)
+# ---------------------------------------------------------------------------
+
+GPTQ_BLOCK = 128   # gptq.py:42
+
+
+def hessian(x: np.ndarray) -> np.ndarray:
+    """H = 2/n * X^T X over n token rows (hessian.py:34-67), float64."""
+    x = np.asarray(x, dtype=np.float64).reshape(-1, np.shape(x)[-1])
+    return (2.0 / x.shape[0]) * (x.T @ x)
+
+
+def offset8_scale_zero(w_group: np.ndarray):
+    """Symmetric INT4 on the unsigned grid with zero point 8 (AutoGPTQ's sym
+    rule): scale = 2 max|w| / 15 over the group (last axis), zero = 8. The
+    reference's own sym rule (scale.py:73-82) puts zero at 0 and so clamps
+    every negative weight to 0."""
+    f32 = np.float32
+    amax = np.maximum(np.max(np.abs(np.asarray(w_group, dtype=f32)), axis=-1), f32(1e-8))
+    scale = (f32(2.0) * amax / f32(15.0)).astype(f32)
+    return scale, np.full_like(scale, f32(8.0))
+
+
+def group_scale_zero(w_group: np.ndarray, sym):
+    """(scale, zero) of each row of w_group [N, gs]: sym False = asymmetric,
+    True = the reference's rule (scale.py:65-91), "offset8" = offset8_scale_zero."""
+    w_group = np.asarray(w_group, dtype=np.float32)
+    if sym == "offset8":
+        return offset8_scale_zero(w_group)
+    s, z = _minmax_to_scale_zero(w_group.min(-1), w_group.max(-1), bool(sym))
+    return s, z
+
+
+def gptq_prepare(H: np.ndarray, damp_percent: float = 0.01, act_order: bool = False):
+    """gptq.py:184-200 in float32: dead columns (diag 0) get diag 1, damping
+    damp_percent * mean(diag) on the diagonal, and with act_order the stable
+    descending order of the damped diagonal. Returns (H damped and permuted,
+    perm, dead mask)."""
+    H = np.array(H, dtype=np.float32)
+    dead = np.diag(H) == 0.0
+    H[dead, dead] = 1.0
+    damp = np.float32(damp_percent) * np.mean(np.diag(H), dtype=np.float32)
+    H[np.diag_indices_from(H)] += np.float32(damp)
+    K = H.shape[0]
+    perm = np.argsort(-np.diag(H), kind="stable") if act_order else np.arange(K)
+    if act_order:
+        H = H[np.ix_(perm, perm)]
+    return H, perm, dead
+
+
+def gptq_cholesky(H: np.ndarray) -> np.ndarray:
+    """Upper Cholesky factor C of H^-1 for a damped H (gptq.py:203-206:
+    cholesky, cholesky_inverse, cholesky upper), computed in float64 and
+    returned as float32."""
+    L = np.linalg.cholesky(np.asarray(H, dtype=np.float64))
+    Linv = np.linalg.inv(L)
+    Hinv = Linv.T @ Linv                       # cholesky_inverse
+    return np.ascontiguousarray(np.linalg.cholesky(Hinv).T, dtype=np.float32)
+
+
+def gptq_columns(Wp: np.ndarray, C: np.ndarray, colg: np.ndarray, scale: np.ndarray,
+                 zero: np.ndarray, group_starts=None, sym=False, group_size: int = 128):
+    """The column loop of gptq.py:215-256 on the permuted float32 W [N, K]:
+    per column j, q = clamp(rint(w / s + z)) with the (scale, zero) of group
+    colg[j]; e = (w - (q - z) s) / C[j, j]; the block's later columns get
+    w -= e * C[j, later] one column at a time (a rounded product, then the
+    subtraction), and the columns right of the block the lazy update
+    E @ C[block, right]. Returns the codes in processed order [N, K].
+
+    group_starts (dynamic groups): scale and zero [N, G] are filled as the loop
+    reaches each group's first column, from W at the start of that column's
+    block (AutoGPTQ's desc_act rule); otherwise they are fixed inputs."""
+    f32 = np.float32
+    W = np.array(Wp, dtype=f32)
+    N, K = W.shape
+    Q = np.zeros((N, K), dtype=np.int32)
+    for b0 in range(0, K, GPTQ_BLOCK):
+        b1 = min(b0 + GPTQ_BLOCK, K)
+        if group_starts is not None:
+            for g0 in range(b0, b1):
+                if g0 % group_size == 0:
+                    g = g0 // group_size
+                    scale[:, g], zero[:, g] = group_scale_zero(W[:, g0:g0 + group_size], sym)
+        Wb = W[:, b0:b1].copy()
+        E = np.zeros_like(Wb)
+        for k in range(b1 - b0):
+            j = b0 + k
+            s, z = scale[:, colg[j]], zero[:, colg[j]]
+            q = np.clip(np.rint(Wb[:, k] / s + z), f32(QMIN), f32(QMAX))
+            Q[:, j] = q.astype(np.int32)
+            e = (Wb[:, k] - (q - z) * s) / C[j, j]
+            E[:, k] = e
+            if k + 1 < b1 - b0:
+                Wb[:, k + 1:] -= (e[:, None] * C[j, j + 1:b1][None, :]).astype(f32)
+        if b1 < K:
+            W[:, b1:] -= (E @ C[b0:b1, b1:]).astype(f32)
+    return Q
+
+
+def gptq_quantize(W: np.ndarray, H: np.ndarray, group_size: int = 128, sym=False,
+                  act_order: bool = False, damp_percent: float = 0.01,
+                  groups: str = "dynamic"):
+    """One GPTQ layer: (packed [N, K/2] storage layout in the original column
+    order, scale [N, G, 1], zero [N, G, 1], g_idx int32 [K] or None).
+
+    groups "reference": the reference's quantize_layer (gptq.py:108-149,
+    156-263): scale/zero from the original W (compute_scale, the reference's
+    sym rule), each column rounded with its original group; no g_idx.
+    groups "dynamic": AutoGPTQ desc_act: groups are runs of group_size columns
+    in processing order, their scale/zero taken from the updated W when the
+    loop reaches them; sym=True means offset-8; with act_order the output
+    carries g_idx[k] = (position of column k in the order) // group_size.
+    act_order sorts columns by descending diag(H) (stable)."""
+    W = np.array(W, dtype=np.float32)
+    N, K = W.shape
+    G = K // group_size
+    W0 = W.copy()
+    Hp, perm, dead = gptq_prepare(H, damp_percent, act_order)
+    W[:, dead] = 0.0
+    C = gptq_cholesky(Hp)
+    Wp = W[:, perm]
+    if groups == "reference":
+        scale, zero = compute_scale(W0, "per_group", group_size, bool(sym))
+        scale, zero = scale[..., 0].copy(), zero[..., 0].copy()
+        colg = (perm // group_size).astype(np.int64)
+        Qp = gptq_columns(Wp, C, colg, scale, zero)
+        g_idx = None
+    elif groups == "dynamic":
+        scale = np.zeros((N, G), dtype=np.float32)
+        zero = np.zeros((N, G), dtype=np.float32)
+        colg = np.arange(K) // group_size
+        sym_rule = "offset8" if sym else False
+        Qp = gptq_columns(Wp, C, colg, scale, zero, group_starts=True, sym=sym_rule,
+                          group_size=group_size)
+        g_idx = gidx_from_perm(perm, group_size) if act_order else None
+    else:
+        raise ValueError(f"groups must be 'reference' or 'dynamic', got {groups!r}")
+    Q = np.empty_like(Qp)
+    Q[:, perm] = Qp
+    return pack_int4(Q), scale[..., None], zero[..., None], g_idx
+
+
+def gptq_objective(W: np.ndarray, W_hat: np.ndarray, H: np.ndarray) -> float:
+    """Layer-output error tr((W - W_hat) H (W - W_hat)^T), the quantity GPTQ
+    minimises (gptq.py:8-10)."""
+    D = np.asarray(W, dtype=np.float64) - np.asarray(W_hat, dtype=np.float64)
+    return float(np.einsum("nk,kl,nl->", D, np.asarray(H, dtype=np.float64), D))
 
 
 # ---------------------------------------------------------------------------

@@ -4,7 +4,8 @@
 Operator API (mirrors pare.kernels.matmul_int4 and pare.core.pack):
   matmul_w4a16, repack_int4_for_kernel, kernel_available / triton_available
 Module: QuantizedLinear (mirrors pare.layers.linear.QuantizedLinear)
-Producer: rtn_quantize (mirrors pare.schemes.rtn on the device)
+Producers: rtn_quantize (pare.schemes.rtn on the device); gptq_quantize,
+     quantize_linear_gptq, HessianAccumulator (pare.schemes.gptq, with g_idx)
 I/O: save_quantized / load_quantized (pare.model.io's on-disk format);
      export_awq / load_awq (the AWQ-GEMM int32 checkpoint of pare.model.export_awq)
 All compute runs in libpare_amd.so (hand-written HIP); there is no CPU fallback.
@@ -12,6 +13,7 @@ All compute runs in libpare_amd.so (hand-written HIP); there is no CPU fallback.
 
 from .awq import export_awq, load_awq
 from .config import QuantConfig, QuantDtype
+from .gptq import HessianAccumulator, gptq_quantize, quantize_linear_gptq
 from .kernels import kernel_available, kernel_choice, matmul_w4a16, triton_available
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .model_io import load_quantized, save_quantized
@@ -20,7 +22,8 @@ from .quant import rtn_quantize
 
 __all__ = [
     "FusedQuantizedLinear", "QuantConfig", "QuantDtype", "QuantizedLinear", "dequantize_int4",
-    "export_awq", "kernel_available", "load_awq",
+    "export_awq", "gptq_quantize", "HessianAccumulator", "kernel_available", "load_awq",
+    "quantize_linear_gptq",
     "kernel_choice", "matmul_w4a16", "perm_from_g_idx", "repack_int4_for_kernel",
     "load_quantized", "rtn_quantize", "save_quantized", "sz_group_major", "triton_available",
     "zeros_to_u8",

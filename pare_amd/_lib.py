@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -42,6 +42,10 @@ SIGNATURES = {
     "pmi_repack_int4_for_kernel": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "pmi_zeros_to_u8": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "pmi_sz_group_major": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "pmi_gptq_group_params": (_i, [_vp, _i64, _i64, _i64, _i64, _i, _vp, _vp, _i64, _i64, _vp]),
+    "pmi_gptq_block": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                            _vp]),
+    "pmi_gptq_pack": (_i, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "pmi_awq_gemm_to_storage": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "pmi_storage_to_awq_gemm": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                      _vp]),

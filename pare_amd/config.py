@@ -69,6 +69,7 @@ class QuantConfig:
     granularity: str = "per_group"
     group_size: int = 128
     sym: bool = False
+    damp_percent: float = 0.01
     act_order: bool = False
 
     def __post_init__(self) -> None:

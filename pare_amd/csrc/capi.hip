@@ -339,12 +339,58 @@ int pmi_rtn_quantize(const void* w, int w_dtype, uint8_t* packed, float* scale, 
     return fail(PMI_ERR_INVALID, "%s: INT4 packing needs an even group_size and K", fn);
   if (w_dtype != PMI_F32 && w_dtype != PMI_F16 && w_dtype != PMI_BF16)
     return fail(PMI_ERR_INVALID, "%s: weight dtype must be PMI_F32, PMI_F16 or PMI_BF16", fn);
-  if (sym != 0 && sym != 1) return fail(PMI_ERR_INVALID, "%s: sym must be 0 or 1", fn);
+  if (sym < 0 || sym > 2) return fail(PMI_ERR_INVALID, "%s: sym must be 0, 1 or 2", fn);
   if (N == 0) return ok();
   if (!w || !packed || !scale || !zero) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
   return from_hip(pmi::launch_rtn(w, w_dtype, packed, scale, zero, N, K, group_size, sym,
                                   (hipStream_t)stream),
                   fn);
+}
+
+// ---- GPTQ producer -----------------------------------------------------------
+
+int pmi_gptq_group_params(const float* w, int64_t ldw, int64_t N, int64_t col0, int64_t cols,
+                          int sym, float* scale, float* zero, int64_t G, int64_t g, void* stream) {
+  const char* fn = "pmi_gptq_group_params";
+  if (N < 0 || cols <= 0 || col0 < 0 || col0 + cols > ldw || G <= 0 || g < 0 || g >= G)
+    return fail(PMI_ERR_INVALID, "%s: need N >= 0, 0 <= col0, col0 + cols <= ldw, 0 <= g < G", fn);
+  if (sym < 0 || sym > 2) return fail(PMI_ERR_INVALID, "%s: sym must be 0, 1 or 2", fn);
+  if (N == 0) return ok();
+  if (!w || !scale || !zero) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  return from_hip(pmi::launch_gptq_group_params(w, ldw, N, col0, cols, sym, scale, zero, G, g,
+                                                (hipStream_t)stream),
+                  fn);
+}
+
+int pmi_gptq_block(const float* w, const float* c, const int32_t* colg, const float* scale,
+                   const float* zero, uint8_t* codes, float* errors, int64_t N, int64_t K,
+                   int64_t G, int64_t b0, int64_t count, void* stream) {
+  const char* fn = "pmi_gptq_block";
+  if (N < 0 || K <= 0 || K % 16 != 0 || G <= 0)
+    return fail(PMI_ERR_INVALID, "%s: need N >= 0, K > 0 with K %% 16 == 0, G > 0", fn);
+  if (b0 < 0 || b0 % 16 != 0 || count <= 0 || count > 128 || count % 16 != 0 || b0 + count > K)
+    return fail(PMI_ERR_INVALID,
+                "%s: the block [b0, b0 + count) must lie in [0, K) with b0 and count multiples "
+                "of 16 and count <= 128 (b0=%lld count=%lld K=%lld)",
+                fn, (long long)b0, (long long)count, (long long)K);
+  if (N == 0) return ok();
+  if (!w || !c || !colg || !scale || !zero || !codes || !errors)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(w, 16)) return fail(PMI_ERR_INVALID, "%s: w must be 16-byte aligned", fn);
+  return from_hip(pmi::launch_gptq_block(w, c, colg, scale, zero, codes, errors, N, K, G, b0,
+                                         (int)count, (hipStream_t)stream),
+                  fn);
+}
+
+int pmi_gptq_pack(const uint8_t* codes, const int32_t* inv_perm, uint8_t* packed, int64_t N,
+                  int64_t K, void* stream) {
+  const char* fn = "pmi_gptq_pack";
+  if (N < 0 || K <= 0 || K % 8 != 0)
+    return fail(PMI_ERR_INVALID, "%s: need N >= 0 and K > 0 with K %% 8 == 0", fn);
+  if (N == 0) return ok();
+  if (!codes || !packed) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(packed, 4)) return fail(PMI_ERR_INVALID, "%s: packed must be 4-byte aligned", fn);
+  return from_hip(pmi::launch_gptq_pack(codes, inv_perm, packed, N, K, (hipStream_t)stream), fn);
 }
 
 // ---- caller-side decoder ops ---------------------------------------------

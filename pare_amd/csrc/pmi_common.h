@@ -135,3 +135,24 @@ PMI_DEV f16x8 b_operand(uint32_t t0, uint32_t t1, f16x2 nz) {
   const u32x4 r = {as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3)};
   return __builtin_bit_cast(f16x8, r);
 }
+
+// (scale, zero) of an INT4 group from its min and max, qmin = 0, qmax = 15.
+// sym 0: asymmetric (pare/core/scale.py:83-91); 1: the reference's symmetric
+// rule on the unsigned grid (scale.py:73-82: zero 0, so negative weights clamp
+// to code 0); 2: offset-8 symmetric, zero 8 and scale 2 max|w| / 15.
+PMI_DEV void scale_zero_from_minmax(float mn, float mx, int sym, float& scale, float& zero) {
+  if (sym == 2) {
+    const float amax = fmaxf(fmaxf(fabsf(mn), fabsf(mx)), 1e-8f);
+    scale = 2.0f * amax / 15.0f;
+    zero = 8.0f;
+  } else if (sym == 1) {
+    const float amax = fmaxf(fmaxf(fabsf(mn), fabsf(mx)), 1e-8f);
+    scale = amax / 15.0f;
+    zero = 0.0f;
+  } else {
+    mn = fminf(mn, 0.0f);
+    mx = fmaxf(mx, 0.0f);
+    scale = fmaxf((mx - mn) / 15.0f, 1e-8f);
+    zero = fminf(fmaxf(rintf(-mn / scale + 0.0f), 0.0f), 15.0f);
+  }
+}

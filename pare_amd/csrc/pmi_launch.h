@@ -132,6 +132,17 @@ hipError_t launch_dequant(const uint8_t* w, int layout, const float* scales, con
                           int zero_u8, const int32_t* idx, void* out, int out_dtype, int64_t N,
                           int64_t K, int64_t gs, hipStream_t stream);
 
+// GPTQ producer (gptq.hip).
+hipError_t launch_gptq_group_params(const float* w, int64_t ldw, int64_t N, int64_t c0,
+                                    int64_t cols, int sym, float* scale, float* zero, int64_t G,
+                                    int64_t g, hipStream_t stream);
+hipError_t launch_gptq_block(const float* w, const float* c, const int32_t* colg,
+                             const float* scale, const float* zero, uint8_t* qt, float* et,
+                             int64_t N, int64_t K, int64_t G, int64_t b0, int count,
+                             hipStream_t stream);
+hipError_t launch_gptq_pack(const uint8_t* qt, const int32_t* inv_perm, uint8_t* packed, int64_t N,
+                            int64_t K, hipStream_t stream);
+
 hipError_t launch_rtn(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
                       int64_t N, int64_t K, int64_t gs, int sym, hipStream_t stream);
 

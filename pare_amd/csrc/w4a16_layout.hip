@@ -3,6 +3,7 @@
 //   zeros    fp32 zero points -> u8, counting values that are not integers in [0,15]
 //   dequant  packed INT4 -> fp16 / bf16 / fp32 weights (bit-exact with the reference)
 //   rtn      fp weights -> (packed, scale, zero) with per-group min/max RTN
+//   awq      AWQ-GEMM int32 words <-> storage layout, fp16 [G,N] <-> fp32 [N,G]
 // All are integer/byte or elementwise work bound by HBM bandwidth; none uses LDS.
 #include "../../include/pare_amd.h"
 #include "pmi_common.h"
@@ -305,18 +306,7 @@ __global__ void rtn_kernel(const void* __restrict__ w, uint8_t* __restrict__ pac
   mx = wave_max(mx);
 
   float scale, zero;
-  if (sym) {
-    const float amax = fmaxf(fmaxf(fabsf(mn), fabsf(mx)), 1e-8f);
-    scale = amax / 15.0f;
-    zero = 0.0f;
-  } else {
-    mn = fminf(mn, 0.0f);
-    mx = fmaxf(mx, 0.0f);
-    scale = (mx - mn) / 15.0f;
-    scale = fmaxf(scale, 1e-8f);
-    zero = rintf(-mn / scale + 0.0f);
-    zero = fminf(fmaxf(zero, 0.0f), 15.0f);
-  }
+  scale_zero_from_minmax(mn, mx, sym, scale, zero);
   if (lane == 0) {
     scale_out[unit] = scale;
     zero_out[unit] = zero;

@@ -22,6 +22,8 @@ def rtn_quantize(weight: torch.Tensor, group_size: int = 128, sym: bool = False,
                  granularity: str = "per_group"):
     """RTN-quantise W [N, K] on the HIP device: (packed, scale, zero).
 
+    sym: False (asymmetric), True (the reference's symmetric rule, zero 0) or
+    "offset8" (symmetric with zero 8 and scale 2·max|w|/15).
     granularity "per_group" uses ``group_size``; "per_channel" one group per
     row; "per_tensor" is not produced by this path (the reference's kernel
     path cannot consume it, pare/kernels/matmul_int4.py:219-225).
@@ -52,7 +54,8 @@ def rtn_quantize(weight: torch.Tensor, group_size: int = 128, sym: bool = False,
     with _DeviceGuard(w.device):
         _lib.check(L.pmi_rtn_quantize(
             w.data_ptr(), _W_DTYPES[w.dtype], packed.data_ptr(), scale.data_ptr(),
-            zero.data_ptr(), N, K, gs, int(bool(sym)), _stream_handle(w.device)),
+            zero.data_ptr(), N, K, gs, 2 if sym == "offset8" else int(bool(sym)),
+            _stream_handle(w.device)),
             "pmi_rtn_quantize")
     if granularity == "per_group":
         return packed, scale.unsqueeze(-1), zero.unsqueeze(-1)

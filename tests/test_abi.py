@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == _lib.ABI_VERSION == 3
+    assert L.pmi_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_kernel_choice(L):
@@ -160,7 +160,7 @@ def test_dequant_validation(L):
 def test_rtn_validation(L):
     rc = L.pmi_rtn_quantize(FAKE, _lib.PMI_F32, FAKE, FAKE, FAKE, 4, 100, 128, 0, None)
     assert rc == _lib.PMI_ERR_INVALID and "divisible" in _lib.last_error()
-    rc = L.pmi_rtn_quantize(FAKE, _lib.PMI_F32, FAKE, FAKE, FAKE, 4, 256, 128, 2, None)
+    rc = L.pmi_rtn_quantize(FAKE, _lib.PMI_F32, FAKE, FAKE, FAKE, 4, 256, 128, 3, None)
     assert rc == _lib.PMI_ERR_INVALID and "sym" in _lib.last_error()
 
 
