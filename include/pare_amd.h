@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 4
+#define PMI_ABI_VERSION 5
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -258,10 +258,23 @@ PMI_API int pmi_rope_kv_f16(const void* qkv, const float* cos, const float* sin,
 
 /* One-token grouped-query attention over cache positions 0..*pos (device
  * int64): out[b, h] = softmax(q[b, h] . k^T * scale) v with KV head h/(H/KV).
- * q, out [B, H, 128] fp16; caches [B, KV, L, 128] fp16; H/KV <= 4. */
+ * q, out [B, H, 128] fp16; caches [B, KV, L, 128] fp16; H/KV <= 4.
+ * workspace (nullable): device scratch of
+ * pmi_decode_attention_workspace_bytes(B, H, KV, L) bytes, 256-byte aligned
+ * and zero-filled before its first use (each call leaves its counters at
+ * zero). With it the positions are split over workgroups of 64 positions
+ * each, combined by the last workgroup of each (b, KV head) in split order;
+ * without it (or when smaller) one workgroup per (b, KV head) runs, for
+ * L up to about 3000. Calls that may run concurrently must not share a
+ * workspace. */
 PMI_API int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cache_v,
                                      const int64_t* pos, void* out, int64_t B, int64_t H,
-                                     int64_t KV, int64_t D, int64_t L, float scale, void* stream);
+                                     int64_t KV, int64_t D, int64_t L, float scale,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of the split pmi_decode_attention_f16 (0 for bad shapes).
+ * Host-only. */
+PMI_API size_t pmi_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t KV, int64_t L);
 
 /* out[r, c] = silu(gate_up[r, c]) * gate_up[r, F + c]; gate_up [rows, 2F],
  * out [rows, F] fp16; F % 8 == 0. */

@@ -425,25 +425,38 @@ int pmi_rope_kv_f16(const void* qkv, const float* cos_t, const float* sin_t, con
                                       KV, D, L, (hipStream_t)stream), fn);
 }
 
+size_t pmi_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t KV, int64_t L) {
+  if (B <= 0 || H <= 0 || KV <= 0 || L <= 0) return 0;
+  return pmi::decode_attention_ws_bytes(B, H, KV, L);
+}
+
 int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cache_v,
                              const int64_t* pos, void* out, int64_t B, int64_t H, int64_t KV,
-                             int64_t D, int64_t L, float scale, void* stream) {
+                             int64_t D, int64_t L, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   const char* fn = "pmi_decode_attention_f16";
   if (B < 0 || H <= 0 || KV <= 0 || H % KV != 0 || L <= 0)
     return fail(PMI_ERR_INVALID, "%s: bad shape", fn);
   if (D != 128 || H / KV > 4)
     return fail(PMI_ERR_UNSUPPORTED, "%s: needs head_dim 128 and at most 4 query heads per KV head",
                 fn);
+  const bool split = workspace && workspace_bytes >= pmi::decode_attention_ws_bytes(B, H, KV, L);
+  if (split && !aligned(workspace, 256))
+    return fail(PMI_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  if (split && pmi::decode_attention_ws_bytes(B, H, KV, L) >= (1ull << 31))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: workspace partials exceed 2 GiB", fn);
   const int64_t group = H / KV, span = (L + 3) / 4;
-  if ((group * 4 * span + group * 4 * (2 + D)) * 4 > 64 * 1024)
-    return fail(PMI_ERR_UNSUPPORTED, "%s: cache length %lld too long for the LDS score buffer", fn,
-                (long long)L);
+  if (!split && (group * 4 * span + group * 4 * (2 + D)) * 4 > 64 * 1024)
+    return fail(PMI_ERR_UNSUPPORTED,
+                "%s: cache length %lld needs the split kernel (pass a workspace of "
+                "pmi_decode_attention_workspace_bytes)", fn, (long long)L);
   if (B == 0) return ok();
   if (!q || !cache_k || !cache_v || !pos || !out) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
   if (!aligned(q, 16) || !aligned(cache_k, 16) || !aligned(cache_v, 16) || !aligned(out, 4))
     return fail(PMI_ERR_INVALID, "%s: q and the caches must be 16-byte aligned", fn);
   if (B * KV * L * D >= (1ll << 31)) return fail(PMI_ERR_UNSUPPORTED, "%s: cache too large", fn);
   return from_hip(pmi::launch_decode_attention(q, cache_k, cache_v, pos, out, B, H, KV, L, scale,
+                                               split ? workspace : nullptr, workspace_bytes,
                                                (hipStream_t)stream), fn);
 }
 

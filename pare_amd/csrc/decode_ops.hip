@@ -244,6 +244,144 @@ __global__ __launch_bounds__(1024) void decode_attention_kernel(
   *reinterpret_cast<f16x2*>(out + ((size_t)b * H + h) * D + 2 * l) = o;
 }
 
+// Decode attention split over the cache positions (flash-decoding), for
+// batches too small to fill the chip with one workgroup per (b, KV head).
+// Workgroup (split s, b * KV + kh) takes positions 64 s .. 64 s + 63, one
+// wave per query head of the group and one lane per position for the
+// scores. It writes the split's partial (max m, sum l, unnormalised P V) to
+// the workspace; the last workgroup of a (b, kh) to arrive, counted with an
+// agent-scope atomic, combines the splits in order (deterministic) and
+// resets the counter. Partials are stored and loaded with the device-scope
+// cache policy (sc1), coherent across the XCDs' L2 caches.
+constexpr int kSplitPos = 64;                   // cache positions per workgroup
+constexpr int kPartFloats = kHeadDim + 4;       // acc[128], m, l, 2 pad (528 bytes)
+constexpr int kSc1 = 16;
+
+__global__ __launch_bounds__(256) void decode_attention_split_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ cache_k, const f16* __restrict__ cache_v,
+    const int64_t* __restrict__ pos, f16* __restrict__ out, int H, int KV, int L, int S,
+    float scale, int* __restrict__ counters, float* __restrict__ part) {
+  constexpr int D = kHeadDim;
+  __shared__ int last_flag;
+  const int sidx = blockIdx.x, bk = blockIdx.y;
+  const int b = bk / KV, kh = bk - (bk / KV) * KV;
+  const int group = H / KV;
+  const int g = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int h = kh * group + g;
+  const int64_t p = *pos;
+  const int len = (int)(p < 0 ? 1 : (p >= L ? L : p + 1));
+  const int j0 = sidx * kSplitPos;
+  const int j1 = min(len, j0 + kSplitPos);  // j1 <= j0: an empty split
+  const f16* kb = cache_k + ((size_t)b * KV + kh) * L * D;
+  const f16* vb = cache_v + ((size_t)b * KV + kh) * L * D;
+  const int64_t part_bytes = (int64_t)gridDim.y * group * S * kPartFloats * 4;
+  const __amdgpu_buffer_rsrc_t rp = rsrc(part, part_bytes);
+  // byte offset of this split's record (wave-uniform)
+  const int rec = __builtin_amdgcn_readfirstlane(((b * H + h) * S + sidx) * kPartFloats * 4);
+
+  float m = -INFINITY, lsum = 0.f;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  const int ps = l >> 4, dc = l & 15;
+  if (j1 > j0) {
+    uint32_t qp[D / 2];
+    const u32x4* q4 = reinterpret_cast<const u32x4*>(q + ((size_t)b * H + h) * D);
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+      const u32x4 v = q4[i];
+      qp[4 * i] = v.x; qp[4 * i + 1] = v.y; qp[4 * i + 2] = v.z; qp[4 * i + 3] = v.w;
+    }
+    // V rows of this lane's positions (j0 + 4k + ps), issued before the scores
+    // so that they are in flight during the K loads and the softmax
+    u32x4 vv[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int j = j0 + 4 * k + ps;
+      vv[k] = *reinterpret_cast<const u32x4*>(vb + (size_t)(j < j1 ? j : j0) * D + 8 * dc);
+    }
+    const int j = j0 + l;
+    const bool live = j < j1;
+    float sc = -INFINITY;
+    if (live) {
+      const u32x4* k4 = reinterpret_cast<const u32x4*>(kb + (size_t)j * D);
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < D / 8; ++i) {
+        const u32x4 kv = k4[i];
+        d = dot2_acc(as_f16x2(kv.x), qp[4 * i], d);
+        d = dot2_acc(as_f16x2(kv.y), qp[4 * i + 1], d);
+        d = dot2_acc(as_f16x2(kv.z), qp[4 * i + 2], d);
+        d = dot2_acc(as_f16x2(kv.w), qp[4 * i + 3], d);
+      }
+      sc = d * scale;
+    }
+    m = wave_max(sc);
+    const float e = live ? __expf(sc - m) : 0.f;
+    lsum = wave_sum(e);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float pk = __shfl(e, 4 * k + ps);  // 0 for positions past j1
+      const f16x8 h8 = __builtin_bit_cast(f16x8, vv[k]);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] = fmaf(pk, (float)h8[x], acc[x]);
+    }
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      acc[x] += __shfl_xor(acc[x], 16);
+      acc[x] += __shfl_xor(acc[x], 32);
+    }
+  }
+  if (l < 16) {
+    const f32x4 a0 = {acc[0], acc[1], acc[2], acc[3]}, a1 = {acc[4], acc[5], acc[6], acc[7]};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, a0), rp, 32 * dc, rec, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, a1), rp, 32 * dc + 16, rec,
+                                           kSc1);
+  } else if (l == 16) {
+    const f32x4 ml = {m, lsum, 0.f, 0.f};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ml), rp, 4 * D, rec, kSc1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&counters[bk], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = old == S - 1;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+
+  // Last to arrive: combine the S splits of head h, dims 2l and 2l + 1.
+  const int rec0 = __builtin_amdgcn_readfirstlane((b * H + h) * S * kPartFloats * 4);
+  float mx = -INFINITY;
+  for (int s = 0; s < S; ++s) {
+    const float ms = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(
+                   rp, 4 * D, __builtin_amdgcn_readfirstlane(rec0 + s * kPartFloats * 4), kSc1));
+    mx = fmaxf(mx, ms);
+  }
+  float tot = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const int off = __builtin_amdgcn_readfirstlane(rec0 + s * kPartFloats * 4);
+    const float ms = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D, off, kSc1));
+    const float ls =
+        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D + 4, off, kSc1));
+    const uint32_t a0 = __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l, off, kSc1);
+    const uint32_t a1 = __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l + 4, off, kSc1);
+    const float f = ms == -INFINITY ? 0.f : __expf(ms - mx);
+    tot = fmaf(ls, f, tot);
+    o0 = fmaf(__builtin_bit_cast(float, a0), f, o0);
+    o1 = fmaf(__builtin_bit_cast(float, a1), f, o1);
+  }
+  const float inv = 1.f / tot;
+  f16x2 o;
+  o[0] = (f16)(o0 * inv);
+  o[1] = (f16)(o1 * inv);
+  *reinterpret_cast<f16x2*>(out + ((size_t)b * H + h) * D + 2 * l) = o;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&counters[bk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // out[r, c] = silu(gu[r, c]) * gu[r, F + c] for c < F.
 __global__ void silu_mul_kernel(const f16* __restrict__ gu, f16* __restrict__ out, int rows,
                                 int F) {
@@ -282,10 +420,26 @@ hipError_t launch_rope_kv(const void* qkv, const float* cos_t, const float* sin_
   return hipGetLastError();
 }
 
+size_t decode_attention_ws_bytes(int64_t B, int64_t H, int64_t KV, int64_t L) {
+  const int64_t S = (L + kSplitPos - 1) / kSplitPos;
+  return decode_attention_counter_bytes(B, KV) + (size_t)(B * H * S * kPartFloats * 4);
+}
+
 hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
                                    const int64_t* pos, void* out, int64_t B, int64_t H,
-                                   int64_t KV, int64_t L, float scale, hipStream_t stream) {
+                                   int64_t KV, int64_t L, float scale, void* workspace,
+                                   size_t ws_bytes, hipStream_t stream) {
   const int group = (int)(H / KV);
+  if (workspace && ws_bytes >= decode_attention_ws_bytes(B, H, KV, L)) {
+    const int S = (int)((L + kSplitPos - 1) / kSplitPos);
+    int* counters = (int*)workspace;
+    float* part = (float*)((char*)workspace + decode_attention_counter_bytes(B, KV));
+    hipLaunchKernelGGL(decode_attention_split_kernel, dim3((unsigned)S, (unsigned)(B * KV)),
+                       dim3(64 * group), 0, stream, (const f16*)q, (const f16*)cache_k,
+                       (const f16*)cache_v, pos, (f16*)out, (int)H, (int)KV, (int)L, S, scale,
+                       counters, part);
+    return hipGetLastError();
+  }
   const int span = (int)((L + kQuarters - 1) / kQuarters);
   const size_t lds = ((size_t)group * kQuarters * span + (size_t)group * kQuarters * (2 + kHeadDim)) * 4;
   hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)(B * KV)),

@@ -108,9 +108,17 @@ hipError_t launch_rope_kv(const void* qkv, const float* cos_t, const float* sin_
                           const int64_t* pos, void* q_out, void* cache_k, void* cache_v,
                           int64_t B, int64_t T, int64_t H, int64_t KV, int64_t D, int64_t L,
                           hipStream_t stream);
+// Split attention workspace: int32 counters [B * KV] (zero between calls,
+// padded to 256 bytes), then the per-split partials.
+inline size_t decode_attention_counter_bytes(int64_t B, int64_t KV) {
+  return ((size_t)(B * KV) * 4 + 255) & ~(size_t)255;
+}
+size_t decode_attention_ws_bytes(int64_t B, int64_t H, int64_t KV, int64_t L);
+// workspace (nullable): too small or null runs the one-workgroup-per-KV-head kernel.
 hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
                                    const int64_t* pos, void* out, int64_t B, int64_t H,
-                                   int64_t KV, int64_t L, float scale, hipStream_t stream);
+                                   int64_t KV, int64_t L, float scale, void* workspace,
+                                   size_t ws_bytes, hipStream_t stream);
 hipError_t launch_silu_mul(const void* gu, void* out, int64_t rows, int64_t F, hipStream_t stream);
 
 hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,

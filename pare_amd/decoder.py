@@ -120,13 +120,37 @@ def rope_kv(qkv, cos, sin, pos, cache_k, cache_v, B, T, H, KV, D):
     return q
 
 
-def decode_attention(q, cache_k, cache_v, pos, scale: float):
-    """q [B, H, 1, D] against cache positions 0..pos -> [B, H, D]."""
+_ATTN_WORKSPACES: dict = {}
+
+
+def _attention_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Zero-filled scratch of the split attention, one per (device, stream):
+    launches on one stream are ordered and each leaves its counters at zero.
+    Allocated by the first (eager) call, so graph captures reuse it."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream)
+    ws = _ATTN_WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
+        _ATTN_WORKSPACES[key] = ws
+    return ws
+
+
+def decode_attention(q, cache_k, cache_v, pos, scale: float, split: bool = True):
+    """q [B, H, 1, D] against cache positions 0..pos -> [B, H, D]. ``split``
+    spreads the positions over workgroups (flash-decoding) through a cached
+    workspace; False runs one workgroup per (sequence, KV head)."""
     B, H, _, D = q.shape
+    KV, L = cache_k.shape[1], cache_k.shape[2]
+    L_ = _lib.lib()
     out = torch.empty(B, H, D, dtype=torch.float16, device=q.device)
-    _check(_lib.lib().pmi_decode_attention_f16(
+    stream = _stream_handle(q.device)
+    ws, nbytes = None, 0
+    if split:
+        nbytes = L_.pmi_decode_attention_workspace_bytes(B, H, KV, L)
+        ws = _attention_workspace(q.device, stream, nbytes)
+    _check(L_.pmi_decode_attention_f16(
         q.data_ptr(), cache_k.data_ptr(), cache_v.data_ptr(), pos.data_ptr(), out.data_ptr(), B, H,
-        cache_k.shape[1], D, cache_k.shape[2], scale, _stream_handle(q.device)),
+        KV, D, L, scale, ws.data_ptr() if ws is not None else None, nbytes, stream),
         "pmi_decode_attention_f16")
     return out
 
