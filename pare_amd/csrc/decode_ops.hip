@@ -351,27 +351,33 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
   __syncthreads();
   if (!last_flag) return;
 
-  // Last to arrive: combine the S splits of head h, dims 2l and 2l + 1.
+  // Last to arrive: combine the S splits of head h in split order, with the
+  // running max rescaling, eight splits per round of loads (each lane reads
+  // the splits' (m, l) and its dims 2l and 2l + 1).
   const int rec0 = __builtin_amdgcn_readfirstlane((b * H + h) * S * kPartFloats * 4);
-  float mx = -INFINITY;
-  for (int s = 0; s < S; ++s) {
-    const float ms = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(
-                   rp, 4 * D, __builtin_amdgcn_readfirstlane(rec0 + s * kPartFloats * 4), kSc1));
-    mx = fmaxf(mx, ms);
-  }
-  float tot = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const int off = __builtin_amdgcn_readfirstlane(rec0 + s * kPartFloats * 4);
-    const float ms = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D, off, kSc1));
-    const float ls =
-        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D + 4, off, kSc1));
-    const uint32_t a0 = __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l, off, kSc1);
-    const uint32_t a1 = __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l + 4, off, kSc1);
-    const float f = ms == -INFINITY ? 0.f : __expf(ms - mx);
-    tot = fmaf(ls, f, tot);
-    o0 = fmaf(__builtin_bit_cast(float, a0), f, o0);
-    o1 = fmaf(__builtin_bit_cast(float, a1), f, o1);
+  float mx = -INFINITY, tot = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float ms[8], ls[8], a0[8], a1[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int sk = min(s0 + k, S - 1);  // past the end: skipped below
+      const int off = __builtin_amdgcn_readfirstlane(rec0 + sk * kPartFloats * 4);
+      ms[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D, off, kSc1));
+      ls[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D + 4, off, kSc1));
+      a0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l, off, kSc1));
+      a1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l + 4, off, kSc1));
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (s0 + k >= S || ms[k] == -INFINITY) continue;  // uniform across the wave
+      const float nm = fmaxf(mx, ms[k]);
+      const float fo = mx == -INFINITY ? 0.f : __expf(mx - nm);
+      const float fn = __expf(ms[k] - nm);
+      tot = fmaf(tot, fo, ls[k] * fn);
+      o0 = fmaf(o0, fo, a0[k] * fn);
+      o1 = fmaf(o1, fo, a1[k] * fn);
+      mx = nm;
+    }
   }
   const float inv = 1.f / tot;
   f16x2 o;
