@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 5
+#define PMI_ABI_VERSION 6
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -149,6 +149,20 @@ PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const
                      const float* scales_gm, const uint8_t* zeros_gm, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* y = (silu(gate) * up) . dequant(W)^T for M <= 4, the down projection of a
+ * gated MLP fused with its activation: gate_up is fp16 [M, 2K] (gate in
+ * columns 0..K-1, up in K..2K-1, the output of a fused gate/up matmul), and
+ * the GEMV forms each activation as pmi_silu_mul_f16 does (silu(gate) rounded
+ * to fp16, times up, rounded to fp16), so y equals pmi_silu_mul_f16 followed
+ * by pmi_matmul_w4a16 bit for bit. w: kernel layout; zeros PMI_U8 [N,G]; no
+ * act_order. Every wave forms its own slice of the activations, so it pays
+ * off at M = 1 (one launch less); from M = 2 on the two launches are faster. No reference counterpart: the reference runs SiLU and the
+ * product as HuggingFace PyTorch ops before QuantizedLinear
+ * (pare/eval/throughput.py:84-126). */
+PMI_API int pmi_matmul_w4a16_glu(const void* gate_up, const uint8_t* w, const float* scales,
+                                 const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,
+                                 int64_t K, int64_t group_size, void* stream);
 
 /* Workspace bytes pmi_matmul_w4a16 uses at full speed for this shape (0 when
  * the chosen kernel needs none). Host-only. No reference counterpart: the

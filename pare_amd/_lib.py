@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -42,6 +42,7 @@ SIGNATURES = {
     "pmi_repack_int4_for_kernel": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "pmi_zeros_to_u8": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "pmi_sz_group_major": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "pmi_matmul_w4a16_glu": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i64, _vp]),
     "pmi_gptq_group_params": (_i, [_vp, _i64, _i64, _i64, _i64, _i, _vp, _vp, _i64, _i64, _vp]),
     "pmi_gptq_block": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                             _vp]),

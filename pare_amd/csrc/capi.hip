@@ -179,6 +179,27 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   return gemm ? 2 : 1;
 }
 
+int pmi_matmul_w4a16_glu(const void* gate_up, const uint8_t* w, const float* scales,
+                         const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,
+                         int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_matmul_w4a16_glu";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (zero_dtype != PMI_U8)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: zero points must be PMI_U8 (got %d)", fn, zero_dtype);
+  if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
+  if (M > 4) return fail(PMI_ERR_UNSUPPORTED, "%s: the gated GEMV takes M <= 4 (got %lld)", fn,
+                         (long long)M);
+  if (M == 0 || N == 0) return ok();
+  if (!gate_up || !w || !scales || !zeros || !y) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(gate_up, 16)) return fail(PMI_ERR_INVALID, "%s: gate_up must be 16-byte aligned", fn);
+  if (!aligned(w, 16)) return fail(PMI_ERR_INVALID, "%s: packed weight must be 16-byte aligned", fn);
+  if (!aligned(scales, 4)) return fail(PMI_ERR_INVALID, "%s: scales must be 4-byte aligned", fn);
+  if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
+  return from_hip(pmi::launch_gemv(gate_up, w, scales, zeros, 1, nullptr, y, M, N, K, group_size,
+                                   (hipStream_t)stream, true),
+                  fn);
+}
+
 size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
                                   int has_perm) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;

@@ -400,7 +400,7 @@ __global__ void silu_mul_kernel(const f16* __restrict__ gu, f16* __restrict__ ou
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float gf = (float)g[e];
-    const float sg = (float)(f16)(gf / (1.f + __expf(-gf)));
+    const float sg = (float)(f16)(gf * __builtin_amdgcn_rcpf(1.f + __expf(-gf)));
     o[e] = (f16)(sg * (float)u[e]);
   }
   *reinterpret_cast<f16x8*>(out + (size_t)r * F + c) = o;

@@ -82,9 +82,11 @@ inline bool gemm_supported(int64_t K, int64_t gs) { return gs % 128 == 0 && K % 
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 
+// glu: x is the fused gate/up output [M, 2K], consumed as silu(gate) * up
+// (u8 zero points, no perm).
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
-                       int64_t K, int64_t gs, hipStream_t stream);
+                       int64_t K, int64_t gs, hipStream_t stream, bool glu = false);
 
 // workspace: zero-filled before first use, left zeroed; may be smaller than
 // gemm_workspace_bytes() (then unsplit) but must hold the counter block and

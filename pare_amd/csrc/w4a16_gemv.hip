@@ -289,7 +289,23 @@ PMI_DEV void reduce_batch(const Batch<U, SPW, ZU8>& bt, const uint32_t (&xp)[SPW
 // with one slice wave the results go straight to y, otherwise each wave
 // parks its per-row partial in LDS and one barrier precedes the fixed-order
 // sum over slice waves (deterministic; no atomics, no workspace).
-template <int MT, int U, int D, int SPW, bool PERM, bool ZU8>
+// silu(g) * u of two fp16 pairs, each half rounded as pmi_silu_mul_f16 rounds
+// it: the gate's silu to fp16 first, then the product.
+PMI_DEV uint32_t glu_pair(uint32_t g, uint32_t u) {
+  const f16x2 gh = as_f16x2(g), uh = as_f16x2(u);
+  f16x2 o;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float gf = (float)gh[e];
+    const float sg = (float)(f16)(gf * __builtin_amdgcn_rcpf(1.f + __expf(-gf)));
+    o[e] = (f16)(sg * (float)uh[e]);
+  }
+  return as_u32(o);
+}
+
+// XM selects the activation source: 0 x [M, K]; 1 x[:, perm] (act_order);
+// 2 the fused gate/up output [M, 2K], consumed as silu(gate) * up.
+template <int MT, int U, int D, int SPW, int XM, bool ZU8>
 __global__ void __launch_bounds__(kMaxWaves * 64)
 w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   const float* __restrict__ scales, const void* __restrict__ zeros,
@@ -323,6 +339,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   int boff[SPW], grp[SPW];
   bool act[SPW];
   uint32_t xa[SPW][MT][8], xb[SPW][MT][8];
+  uint32_t ua[XM == 2 ? SPW : 1][XM == 2 ? MT : 1][8], ub[XM == 2 ? SPW : 1][XM == 2 ? MT : 1][8];
 #pragma unroll
   for (int sp = 0; sp < SPW; ++sp) {
     const int s = ws + sp * slice_waves;
@@ -335,8 +352,15 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     grp[sp] = t;
     const int k_lo = t * gs + j;
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-      load_x_raw<PERM>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
+    for (int m = 0; m < MT; ++m) {
+      if constexpr (XM == 2) {
+        load_x_raw<false>(x + (int64_t)m * 2 * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
+        load_x_raw<false>(x + (int64_t)m * 2 * K + K, perm, k_lo, k_lo + hgs, K, ua[sp][m],
+                          ub[sp][m]);
+      } else {
+        load_x_raw<XM == 1>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
+      }
+    }
   }
 
   const int my_row0 = row0 + wr * U;
@@ -349,6 +373,13 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     for (int sp = 0; sp < SPW; ++sp)
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
+        if constexpr (XM == 2) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xa[sp][m][i] = glu_pair(xa[sp][m][i], ua[sp][m][i]);
+            xb[sp][m][i] = glu_pair(xb[sp][m][i], ub[sp][m][i]);
+          }
+        }
         pair_x(xa[sp][m], xb[sp][m], xp[sp][m]);
         if (!act[sp]) {
 #pragma unroll
@@ -427,19 +458,23 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 template <int MT, int U, int D, int SPW>
 hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                       const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                      int gs, hipStream_t stream) {
+                      int gs, bool glu, hipStream_t stream) {
   const dim3 block(64 * c.slice_waves * c.row_waves);
   const size_t lds = c.lds_bytes;
-#define PMI_GEMV_LAUNCH(P, Z)                                                                  \
-  hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, P, Z>), dim3(c.grid), block, lds, stream, \
-                     (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,      \
+#define PMI_GEMV_LAUNCH(XM, Z)                                                                  \
+  hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
+                     (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,       \
                      c.slice_waves, c.row_waves, c.rows_per_wg)
-  if (perm) {
-    if (zero_u8) PMI_GEMV_LAUNCH(true, true);
-    else PMI_GEMV_LAUNCH(true, false);
+  if (glu) {
+    // the gated form is built for u8 zero points and no permutation only
+    if (!zero_u8 || perm) return hipErrorInvalidValue;
+    PMI_GEMV_LAUNCH(2, true);
+  } else if (perm) {
+    if (zero_u8) PMI_GEMV_LAUNCH(1, true);
+    else PMI_GEMV_LAUNCH(1, false);
   } else {
-    if (zero_u8) PMI_GEMV_LAUNCH(false, true);
-    else PMI_GEMV_LAUNCH(false, false);
+    if (zero_u8) PMI_GEMV_LAUNCH(0, true);
+    else PMI_GEMV_LAUNCH(0, false);
   }
 #undef PMI_GEMV_LAUNCH
   return hipGetLastError();
@@ -454,10 +489,11 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
 template <int MT, int SPW>
 hipError_t launch_ud(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                     int gs, hipStream_t stream) {
+                     int gs, bool glu, hipStream_t stream) {
 #define PMI_GEMV_UD(U_, D_) \
   if (c.rows_per_wave == U_ && c.depth == D_) \
-    return launch_cfg<MT, U_, D_, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream)
+    return launch_cfg<MT, U_, D_, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, glu, \
+                                       stream)
   if constexpr (MT == 1) {
     PMI_GEMV_UD(4, 2);
     PMI_GEMV_UD(2, 3);
@@ -484,10 +520,10 @@ hipError_t launch_ud(const GemvConfig& c, const void* x, const uint8_t* w, const
 template <int MT>
 hipError_t launch_mt(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                     int gs, hipStream_t stream) {
+                     int gs, bool glu, hipStream_t stream) {
   if (c.slices_per_wave == 2)
-    return launch_ud<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
-  return launch_ud<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, stream);
+    return launch_ud<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, glu, stream);
+  return launch_ud<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, glu, stream);
 }
 
 int env_int(const char* name, int dflt) {
@@ -580,14 +616,14 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
 
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
-                       int64_t K, int64_t gs, hipStream_t stream) {
+                       int64_t K, int64_t gs, hipStream_t stream, bool glu) {
   const GemvConfig c = gemv_config(M, N, K);
   const int n = (int)N, k = (int)K, g = (int)gs;
   switch (M) {
-    case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
-    case 2: return launch_mt<2>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
-    case 3: return launch_mt<3>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
-    case 4: return launch_mt<4>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, stream);
+    case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
+    case 2: return launch_mt<2>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
+    case 3: return launch_mt<3>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
+    case 4: return launch_mt<4>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
     default: return hipErrorInvalidValue;
   }
 }

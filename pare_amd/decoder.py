@@ -36,7 +36,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .config import QuantConfig
-from .kernels import _stream_handle
+from .kernels import _stream_handle, matmul_w4a16_glu
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .quant import rtn_quantize
 
@@ -223,7 +223,19 @@ class DecoderLayer(nn.Module):
             a = decode_attention(q, cache_k, cache_v, pos, 1.0 / math.sqrt(cfg.head_dim))
             a = a.reshape(B, 1, cfg.hidden)
         n2, h = add_rmsnorm(h, self.o(a), self.mlp_norm.weight, cfg.rms_eps)
-        return h, self.down(silu_mul(self.gate_up.fused(n2)))
+        gu = self.gate_up.fused(n2)
+        if B * T == 1 and self.down.g_idx is None:
+            # one-token decode: the down GEMV forms silu(gate) * up itself, one
+            # launch less (9.6 us against 11.4 us for silu_mul + GEMV on the
+            # Llama down shape; from two rows on, the per-wave SiLU costs more
+            # than the launch it saves)
+            w_k, z_u8, _, _ = self.down._kernel_buffers()
+            y = matmul_w4a16_glu(gu.reshape(B * T, -1).contiguous(), w_k, self.down.scale, z_u8,
+                                 self.down._group_size())
+            if self.down.bias is not None:
+                y = y + self.down.bias
+            return h, y.reshape(B, T, -1)
+        return h, self.down(silu_mul(gu))
 
 
 class QuantizedDecoder(nn.Module):

@@ -191,6 +191,35 @@ def matmul_w4a16(
     return out
 
 
+def matmul_w4a16_glu(gate_up: torch.Tensor, packed_weight: torch.Tensor, scales: torch.Tensor,
+                     zeros_u8: torch.Tensor, group_size: int) -> torch.Tensor:
+    """Y = (silu(gate) * up) @ dequant(W)^T for M <= 4: the down projection of
+    a gated MLP fused with its activation. ``gate_up`` is the fused gate/up
+    output [M, 2K] fp16; the result equals ``silu_mul`` followed by
+    ``matmul_w4a16`` bit for bit. ``zeros_u8``: uint8 [N, G] zero points."""
+    L = _lib.lib()
+    if not gate_up.is_cuda:
+        raise RuntimeError("matmul_w4a16_glu requires HIP (cuda) tensors.")
+    assert gate_up.dtype == torch.float16 and gate_up.dim() == 2 and gate_up.is_contiguous(), \
+        "gate_up must be a contiguous float16 [M, 2K] tensor"
+    M, K2 = gate_up.shape
+    K = K2 // 2
+    N, K_half = packed_weight.shape
+    assert K2 == 2 * K and K == 2 * K_half, f"gate_up has {K2} columns, expected 2*K={4 * K_half}"
+    assert M <= 4, f"the gated GEMV takes M <= 4, got {M}"
+    z2 = _to_2d(zeros_u8)
+    assert z2.dtype == torch.uint8, "zeros must be uint8 [N, G]"
+    s2 = _to_2d(scales).float().contiguous()
+    dev = gate_up.device
+    out = torch.empty(M, N, device=dev, dtype=torch.float16)
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16_glu(
+            _aligned16(gate_up).data_ptr(), _aligned16(packed_weight.contiguous()).data_ptr(),
+            s2.data_ptr(), z2.contiguous().data_ptr(), _lib.PMI_U8, out.data_ptr(), M, N, K,
+            group_size, _stream_handle(dev)), "pmi_matmul_w4a16_glu")
+    return out
+
+
 _KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4}
 
 

@@ -1,4 +1,4 @@
-"""End-to-end decoder (BASELINE config 5) on a small Llama-shaped config: the
+"""End-to-end decoder on a small Llama-shaped config: the
 HIP path inside a model, graph-captured decode, and the reference's
 dequantize-on-the-fly path as the check (pare/layers/linear.py:101-138)."""
 
@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import pare_amd as P
+from pare_amd import _lib
 from pare_amd.decoder import (DecoderConfig, QuantizedDecoder, add_rmsnorm, decode_attention,
                               decoder_throughput, rope_kv, rope_tables, silu_mul)
 
@@ -162,6 +163,41 @@ def test_decode_attention(B, H, KV, L, p, split):
     err = (out.float() - ref).abs().max().item()
     print(f"[attn] split={split} B={B} H={H} KV={KV} L={L} p={p}: max_abs={err:.3e}", flush=True)
     assert err <= 5e-3
+
+
+@pytest.mark.parametrize("M,N,F", [(1, 4096, 14336), (2, 4096, 14336), (3, 1024, 4096),
+                                   (4, 4096, 14336), (1, 136, 512), (4, 200, 1024)])
+def test_glu_down_matches_silu_then_matmul(M, N, F):
+    """The gated GEMV against silu_mul followed by the plain matmul: the same
+    fp16 activations feed the same kernel, so the outputs are equal bit for bit."""
+    from pare_amd.kernels import matmul_w4a16, matmul_w4a16_glu
+    from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
+
+    g = torch.Generator(device=DEV).manual_seed(M * N + F)
+    gu = (torch.randn(M, 2 * F, generator=g, device=DEV) * 2).half()
+    w = torch.randn(N, F, generator=g, device=DEV) * 0.02
+    packed, s, z = P.rtn_quantize(w, 128)
+    wk = repack_int4_for_kernel(packed, 128)
+    zu = zeros_to_u8(z)
+    got = matmul_w4a16_glu(gu, wk, s, zu, 128)
+    ref = matmul_w4a16(silu_mul(gu), wk, s, zu, 128)
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+
+
+def test_glu_down_rejects_what_it_does_not_run():
+    from pare_amd.kernels import matmul_w4a16_glu
+    from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
+
+    w = torch.randn(256, 512, device=DEV) * 0.02
+    packed, s, z = P.rtn_quantize(w, 128)
+    wk = repack_int4_for_kernel(packed, 128)
+    with pytest.raises(AssertionError, match="M <= 4"):
+        matmul_w4a16_glu(torch.zeros(5, 1024, device=DEV).half(), wk, s, zeros_to_u8(z), 128)
+    L = _lib.lib()
+    assert L.pmi_matmul_w4a16_glu(None, None, None, None, _lib.PMI_F32, None, 1, 256, 512, 128,
+                                  None) == _lib.PMI_ERR_UNSUPPORTED
+    assert L.pmi_matmul_w4a16_glu(None, None, None, None, _lib.PMI_U8, None, 5, 256, 512, 128,
+                                  None) == _lib.PMI_ERR_UNSUPPORTED
 
 
 @pytest.mark.parametrize("rows,F", [(1, 14336), (4, 1024)])
