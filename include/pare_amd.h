@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 6
+#define PMI_ABI_VERSION 7
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -285,6 +285,19 @@ PMI_API int pmi_decode_attention_f16(const void* q, const void* cache_k, const v
                                      const int64_t* pos, void* out, int64_t B, int64_t H,
                                      int64_t KV, int64_t D, int64_t L, float scale,
                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* pmi_rope_kv_f16 and pmi_decode_attention_f16 of one new token in one
+ * launch: qkv [B, (H + 2*KV)*128] fp16 is the token's fused q/k/v row, cos/sin
+ * fp32 [L, 64] the RoPE tables, *pos (device int64) its cache position. Writes
+ * the rotated k and the v into cache_k / cache_v at *pos and out [B, H, 128]
+ * = the attention of the rotated q over positions 0..*pos, equal to the two
+ * separate calls bit for bit. Needs the workspace of
+ * pmi_decode_attention_workspace_bytes (same rules). No reference counterpart. */
+PMI_API int pmi_decode_attention_rope_f16(const void* qkv, const float* cos, const float* sin,
+                                          const int64_t* pos, void* cache_k, void* cache_v,
+                                          void* out, int64_t B, int64_t H, int64_t KV, int64_t D,
+                                          int64_t L, float scale, void* workspace,
+                                          size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of the split pmi_decode_attention_f16 (0 for bad shapes).
  * Host-only. */

@@ -481,6 +481,36 @@ int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cac
                                                (hipStream_t)stream), fn);
 }
 
+int pmi_decode_attention_rope_f16(const void* qkv, const float* cos, const float* sin,
+                                  const int64_t* pos, void* cache_k, void* cache_v, void* out,
+                                  int64_t B, int64_t H, int64_t KV, int64_t D, int64_t L,
+                                  float scale, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const char* fn = "pmi_decode_attention_rope_f16";
+  if (B < 0 || H <= 0 || KV <= 0 || H % KV != 0 || L <= 0)
+    return fail(PMI_ERR_INVALID, "%s: bad shape", fn);
+  if (D != 128 || H / KV > 4)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: needs head_dim 128 and at most 4 query heads per KV head",
+                fn);
+  const size_t need = pmi::decode_attention_ws_bytes(B, H, KV, L);
+  if (!workspace || workspace_bytes < need)
+    return fail(PMI_ERR_INVALID, "%s: needs a workspace of pmi_decode_attention_workspace_bytes "
+                "(%zu) bytes", fn, need);
+  if (!aligned(workspace, 256)) return fail(PMI_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  if (need >= (1ull << 31)) return fail(PMI_ERR_UNSUPPORTED, "%s: workspace partials exceed 2 GiB", fn);
+  if (B == 0) return ok();
+  if (!qkv || !cos || !sin || !pos || !cache_k || !cache_v || !out)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(cache_k, 16) || !aligned(cache_v, 16) || !aligned(out, 4) || !aligned(qkv, 2) ||
+      !aligned(cos, 4) || !aligned(sin, 4))
+    return fail(PMI_ERR_INVALID, "%s: the caches must be 16-byte aligned", fn);
+  if (B * KV * L * D >= (1ll << 31)) return fail(PMI_ERR_UNSUPPORTED, "%s: cache too large", fn);
+  return from_hip(pmi::launch_decode_attention(qkv, cache_k, cache_v, pos, out, B, H, KV, L, scale,
+                                               workspace, workspace_bytes, (hipStream_t)stream,
+                                               cos, sin),
+                  fn);
+}
+
 int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64_t F, void* stream) {
   const char* fn = "pmi_silu_mul_f16";
   if (rows < 0 || F <= 0 || F % 8 != 0)

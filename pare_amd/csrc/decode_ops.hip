@@ -257,12 +257,22 @@ constexpr int kSplitPos = 64;                   // cache positions per workgroup
 constexpr int kPartFloats = kHeadDim + 4;       // acc[128], m, l, 2 pad (528 bytes)
 constexpr int kSc1 = 16;
 
+// ROPE: q is the fused q/k/v row [B, (H + 2 KV) D] of the new token instead
+// of rotated q [B, H, D]. The kernel then does rope_kv_kernel's work itself:
+// every wave rotates its head's q into LDS, and the workgroup whose split holds
+// the new token's cache row rotates its k and writes k and v to the caches,
+// using them from LDS for that row (the same fp16 roundings as rope_kv_kernel,
+// so the result equals rope_kv + attention bit for bit).
+template <bool ROPE>
 __global__ __launch_bounds__(256) void decode_attention_split_kernel(
-    const f16* __restrict__ q, const f16* __restrict__ cache_k, const f16* __restrict__ cache_v,
-    const int64_t* __restrict__ pos, f16* __restrict__ out, int H, int KV, int L, int S,
-    float scale, int* __restrict__ counters, float* __restrict__ part) {
+    const f16* __restrict__ q, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    f16* __restrict__ cache_k, f16* __restrict__ cache_v, const int64_t* __restrict__ pos,
+    f16* __restrict__ out, int H, int KV, int L, int S, float scale, int* __restrict__ counters,
+    float* __restrict__ part) {
   constexpr int D = kHeadDim;
   __shared__ int last_flag;
+  __shared__ __attribute__((aligned(16))) f16 qrot[ROPE ? 4 : 1][D];
+  __shared__ __attribute__((aligned(16))) f16 kvnew[ROPE ? 2 : 1][D];
   const int sidx = blockIdx.x, bk = blockIdx.y;
   const int b = bk / KV, kh = bk - (bk / KV) * KV;
   const int group = H / KV;
@@ -278,6 +288,35 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
   const __amdgpu_buffer_rsrc_t rp = rsrc(part, part_bytes);
   // byte offset of this split's record (wave-uniform)
   const int rec = __builtin_amdgcn_readfirstlane(((b * H + h) * S + sidx) * kPartFloats * 4);
+  const int pc = (int)(p < 0 ? 0 : (p >= L ? L - 1 : p));  // the new token's cache row
+
+  if constexpr (ROPE) {
+    if (j1 > j0) {
+      const f16* src = q + (size_t)b * (H + 2 * KV) * D;
+      const int d = l;  // rotation pair (d, d + D/2)
+      const float c = cos_t[(size_t)pc * (D / 2) + d], sn = sin_t[(size_t)pc * (D / 2) + d];
+      {
+        const float x1 = (float)src[h * D + d], x2 = (float)src[h * D + d + D / 2];
+        qrot[g][d] = (f16)(x1 * c - x2 * sn);
+        qrot[g][d + D / 2] = (f16)(x2 * c + x1 * sn);
+      }
+      if (g == 0 && pc >= j0 && pc < j1) {
+        const float x1 = (float)src[(H + kh) * D + d], x2 = (float)src[(H + kh) * D + d + D / 2];
+        const f16 o1 = (f16)(x1 * c - x2 * sn), o2 = (f16)(x2 * c + x1 * sn);
+        const f16 v1 = src[(H + KV + kh) * D + d], v2 = src[(H + KV + kh) * D + d + D / 2];
+        kvnew[0][d] = o1;
+        kvnew[0][d + D / 2] = o2;
+        kvnew[1][d] = v1;
+        kvnew[1][d + D / 2] = v2;
+        const size_t crow = (((size_t)b * KV + kh) * L + pc) * D;
+        cache_k[crow + d] = o1;
+        cache_k[crow + d + D / 2] = o2;
+        cache_v[crow + d] = v1;
+        cache_v[crow + d + D / 2] = v2;
+      }
+    }
+    __syncthreads();
+  }
 
   float m = -INFINITY, lsum = 0.f;
   float acc[8];
@@ -286,25 +325,30 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
   const int ps = l >> 4, dc = l & 15;
   if (j1 > j0) {
     uint32_t qp[D / 2];
-    const u32x4* q4 = reinterpret_cast<const u32x4*>(q + ((size_t)b * H + h) * D);
+    const u32x4* q4 = ROPE ? reinterpret_cast<const u32x4*>(&qrot[ROPE ? g : 0][0])
+                           : reinterpret_cast<const u32x4*>(q + ((size_t)b * H + h) * D);
 #pragma unroll
     for (int i = 0; i < D / 8; ++i) {
       const u32x4 v = q4[i];
       qp[4 * i] = v.x; qp[4 * i + 1] = v.y; qp[4 * i + 2] = v.z; qp[4 * i + 3] = v.w;
     }
     // V rows of this lane's positions (j0 + 4k + ps), issued before the scores
-    // so that they are in flight during the K loads and the softmax
+    // so that they are in flight during the K loads and the softmax (the new
+    // token's row comes from LDS under ROPE)
     u32x4 vv[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int j = j0 + 4 * k + ps;
-      vv[k] = *reinterpret_cast<const u32x4*>(vb + (size_t)(j < j1 ? j : j0) * D + 8 * dc);
+      const int jj = j < j1 ? j : j0;
+      const f16* vrow = (ROPE && jj == pc) ? &kvnew[ROPE ? 1 : 0][0] : vb + (size_t)jj * D;
+      vv[k] = *reinterpret_cast<const u32x4*>(vrow + 8 * dc);
     }
     const int j = j0 + l;
     const bool live = j < j1;
     float sc = -INFINITY;
     if (live) {
-      const u32x4* k4 = reinterpret_cast<const u32x4*>(kb + (size_t)j * D);
+      const f16* krow = (ROPE && j == pc) ? &kvnew[0][0] : kb + (size_t)j * D;
+      const u32x4* k4 = reinterpret_cast<const u32x4*>(krow);
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < D / 8; ++i) {
@@ -434,18 +478,26 @@ size_t decode_attention_ws_bytes(int64_t B, int64_t H, int64_t KV, int64_t L) {
 hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
                                    const int64_t* pos, void* out, int64_t B, int64_t H,
                                    int64_t KV, int64_t L, float scale, void* workspace,
-                                   size_t ws_bytes, hipStream_t stream) {
+                                   size_t ws_bytes, hipStream_t stream, const float* cos_t,
+                                   const float* sin_t) {
   const int group = (int)(H / KV);
+  const bool rope = cos_t != nullptr;
   if (workspace && ws_bytes >= decode_attention_ws_bytes(B, H, KV, L)) {
     const int S = (int)((L + kSplitPos - 1) / kSplitPos);
     int* counters = (int*)workspace;
     float* part = (float*)((char*)workspace + decode_attention_counter_bytes(B, KV));
-    hipLaunchKernelGGL(decode_attention_split_kernel, dim3((unsigned)S, (unsigned)(B * KV)),
-                       dim3(64 * group), 0, stream, (const f16*)q, (const f16*)cache_k,
-                       (const f16*)cache_v, pos, (f16*)out, (int)H, (int)KV, (int)L, S, scale,
-                       counters, part);
+    const dim3 grid((unsigned)S, (unsigned)(B * KV)), block(64 * group);
+    if (rope)
+      hipLaunchKernelGGL(decode_attention_split_kernel<true>, grid, block, 0, stream, (const f16*)q,
+                         cos_t, sin_t, (f16*)cache_k, (f16*)cache_v, pos, (f16*)out, (int)H,
+                         (int)KV, (int)L, S, scale, counters, part);
+    else
+      hipLaunchKernelGGL(decode_attention_split_kernel<false>, grid, block, 0, stream,
+                         (const f16*)q, nullptr, nullptr, (f16*)cache_k, (f16*)cache_v, pos,
+                         (f16*)out, (int)H, (int)KV, (int)L, S, scale, counters, part);
     return hipGetLastError();
   }
+  if (rope) return hipErrorInvalidValue;  // the fused RoPE needs the split kernel
   const int span = (int)((L + kQuarters - 1) / kQuarters);
   const size_t lds = ((size_t)group * kQuarters * span + (size_t)group * kQuarters * (2 + kHeadDim)) * 4;
   hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)(B * KV)),

@@ -120,7 +120,8 @@ size_t decode_attention_ws_bytes(int64_t B, int64_t H, int64_t KV, int64_t L);
 hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
                                    const int64_t* pos, void* out, int64_t B, int64_t H,
                                    int64_t KV, int64_t L, float scale, void* workspace,
-                                   size_t ws_bytes, hipStream_t stream);
+                                   size_t ws_bytes, hipStream_t stream,
+                                   const float* cos_t = nullptr, const float* sin_t = nullptr);
 hipError_t launch_silu_mul(const void* gu, void* out, int64_t rows, int64_t F, hipStream_t stream);
 
 hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,

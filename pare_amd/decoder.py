@@ -155,6 +155,24 @@ def decode_attention(q, cache_k, cache_v, pos, scale: float, split: bool = True)
     return out
 
 
+def decode_attention_rope(qkv, cos, sin, pos, cache_k, cache_v, scale: float):
+    """RoPE + KV-cache write + attention of one new token in one launch:
+    qkv [B, (H + 2*KV)*D] -> [B, H, D] (equal to rope_kv + decode_attention)."""
+    B = qkv.shape[0]
+    KV, L, D = cache_k.shape[1], cache_k.shape[2], cache_k.shape[3]
+    H = qkv.shape[-1] // D - 2 * KV
+    L_ = _lib.lib()
+    out = torch.empty(B, H, D, dtype=torch.float16, device=qkv.device)
+    stream = _stream_handle(qkv.device)
+    nbytes = L_.pmi_decode_attention_workspace_bytes(B, H, KV, L)
+    ws = _attention_workspace(qkv.device, stream, nbytes)
+    _check(L_.pmi_decode_attention_rope_f16(
+        qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), cache_k.data_ptr(),
+        cache_v.data_ptr(), out.data_ptr(), B, H, KV, D, L, scale, ws.data_ptr(), nbytes, stream),
+        "pmi_decode_attention_rope_f16")
+    return out
+
+
 def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up of a fused [.., 2F] gate/up output."""
     F2 = gu.shape[-1]
@@ -213,6 +231,13 @@ class DecoderLayer(nn.Module):
         B, T, _ = h.shape
         n1, h = add_rmsnorm(h, d, self.attn_norm.weight, cfg.rms_eps)
         qkv = self.qkv.fused(n1)
+        if not causal and T == 1:
+            # one new token: RoPE, the cache write and attention in one launch
+            a = decode_attention_rope(qkv.reshape(B, -1), cos_t, sin_t, pos, cache_k, cache_v,
+                                      1.0 / math.sqrt(cfg.head_dim))
+            n2, h = add_rmsnorm(h, self.o(a.reshape(B, 1, cfg.hidden)), self.mlp_norm.weight,
+                                cfg.rms_eps)
+            return h, self._mlp(n2, B, T)
         q = rope_kv(qkv, cos_t, sin_t, pos, cache_k, cache_v, B, T, cfg.heads, cfg.kv_heads,
                     cfg.head_dim)
         if causal:
@@ -223,6 +248,9 @@ class DecoderLayer(nn.Module):
             a = decode_attention(q, cache_k, cache_v, pos, 1.0 / math.sqrt(cfg.head_dim))
             a = a.reshape(B, 1, cfg.hidden)
         n2, h = add_rmsnorm(h, self.o(a), self.mlp_norm.weight, cfg.rms_eps)
+        return h, self._mlp(n2, B, T)
+
+    def _mlp(self, n2, B: int, T: int):
         gu = self.gate_up.fused(n2)
         if B * T == 1 and self.down.g_idx is None:
             # one-token decode: the down GEMV forms silu(gate) * up itself, one
@@ -234,8 +262,8 @@ class DecoderLayer(nn.Module):
                                  self.down._group_size())
             if self.down.bias is not None:
                 y = y + self.down.bias
-            return h, y.reshape(B, T, -1)
-        return h, self.down(silu_mul(gu))
+            return y.reshape(B, T, -1)
+        return self.down(silu_mul(gu))
 
 
 class QuantizedDecoder(nn.Module):

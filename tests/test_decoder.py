@@ -165,6 +165,29 @@ def test_decode_attention(B, H, KV, L, p, split):
     assert err <= 5e-3
 
 
+@pytest.mark.parametrize("B,H,KV,L,p", [(1, 32, 8, 640, 511), (4, 32, 8, 640, 639), (2, 8, 2, 100, 0),
+                                        (3, 4, 4, 300, 77), (1, 32, 8, 640, 64), (2, 16, 8, 130, 129),
+                                        (1, 8, 8, 200, 500)])
+def test_decode_attention_rope_equals_the_two_launches(B, H, KV, L, p):
+    """RoPE + cache write + attention in one launch against rope_kv followed by
+    decode_attention on copies of the same caches: equal outputs and caches."""
+    from pare_amd.decoder import decode_attention_rope
+
+    D = 128
+    g = torch.Generator(device=DEV).manual_seed(B * L + p + 7)
+    qkv = torch.randn(B, (H + 2 * KV) * D, generator=g, device=DEV).half()
+    ck = torch.randn(B, KV, L, D, generator=g, device=DEV).half()
+    cv = torch.randn(B, KV, L, D, generator=g, device=DEV).half()
+    cos, sin = rope_tables(D, 500000.0, L, DEV)
+    pos = torch.full((1,), p, dtype=torch.long, device=DEV)
+    ck2, cv2 = ck.clone(), cv.clone()
+    q = rope_kv(qkv.view(B, 1, -1), cos, sin, pos, ck2, cv2, B, 1, H, KV, D)
+    ref = decode_attention(q, ck2, cv2, pos, 1 / D ** 0.5)
+    got = decode_attention_rope(qkv, cos, sin, pos, ck, cv, 1 / D ** 0.5)
+    assert torch.equal(ck, ck2) and torch.equal(cv, cv2)
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("M,N,F", [(1, 4096, 14336), (2, 4096, 14336), (3, 1024, 4096),
                                    (4, 4096, 14336), (1, 136, 512), (4, 200, 1024)])
 def test_glu_down_matches_silu_then_matmul(M, N, F):
