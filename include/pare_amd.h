@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 7
+#define PMI_ABI_VERSION 8
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -163,6 +163,22 @@ PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const
 PMI_API int pmi_matmul_w4a16_glu(const void* gate_up, const uint8_t* w, const float* scales,
                                  const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,
                                  int64_t K, int64_t group_size, void* stream);
+
+/* y = (RMSNorm(x + residual) * norm_weight) . dequant(W)^T for M <= 4: a
+ * decoder's residual add and pre-norm fused into the GEMV that consumes them.
+ * x, residual (nullable), h_out: fp16 [M, K]; norm_weight fp16 [K]. With a
+ * residual, h = x + residual (fp16) is written to h_out. Each activation is
+ * formed as pmi_add_rmsnorm_f16 forms it (h rounded to fp16; y = h *
+ * rsqrt(mean(h^2) + eps) * w rounded to fp16); the mean is summed in another
+ * order, so activations can differ from pmi_add_rmsnorm_f16 by one fp16 ulp.
+ * w: kernel layout; zeros PMI_U8 [N,G]; no act_order. Every wave forms the
+ * norm for its rows after one workgroup barrier; it pays off at M = 1. No
+ * reference counterpart (the reference runs the norm in PyTorch,
+ * pare/eval/throughput.py:84-126). */
+PMI_API int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const void* norm_weight,
+                                     float eps, void* h_out, const uint8_t* w, const float* scales,
+                                     const void* zeros, int zero_dtype, void* y, int64_t M,
+                                     int64_t N, int64_t K, int64_t group_size, void* stream);
 
 /* Workspace bytes pmi_matmul_w4a16 uses at full speed for this shape (0 when
  * the chosen kernel needs none). Host-only. No reference counterpart: the

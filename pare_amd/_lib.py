@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -43,6 +43,8 @@ SIGNATURES = {
     "pmi_zeros_to_u8": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "pmi_sz_group_major": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i64, _i64, _vp]),
     "pmi_matmul_w4a16_glu": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "pmi_matmul_w4a16_rmsnorm": (_i, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i, _vp,
+                                      _i64, _i64, _i64, _i64, _vp]),
     "pmi_gptq_group_params": (_i, [_vp, _i64, _i64, _i64, _i64, _i, _vp, _vp, _i64, _i64, _vp]),
     "pmi_gptq_block": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                             _vp]),

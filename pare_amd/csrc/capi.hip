@@ -195,8 +195,43 @@ int pmi_matmul_w4a16_glu(const void* gate_up, const uint8_t* w, const float* sca
   if (!aligned(w, 16)) return fail(PMI_ERR_INVALID, "%s: packed weight must be 16-byte aligned", fn);
   if (!aligned(scales, 4)) return fail(PMI_ERR_INVALID, "%s: scales must be 4-byte aligned", fn);
   if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
+  pmi::GemvXform xf;
+  xf.mode = 2;
   return from_hip(pmi::launch_gemv(gate_up, w, scales, zeros, 1, nullptr, y, M, N, K, group_size,
-                                   (hipStream_t)stream, true),
+                                   (hipStream_t)stream, &xf),
+                  fn);
+}
+
+int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const void* norm_weight,
+                             float eps, void* h_out, const uint8_t* w, const float* scales,
+                             const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,
+                             int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_matmul_w4a16_rmsnorm";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (zero_dtype != PMI_U8)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: zero points must be PMI_U8 (got %d)", fn, zero_dtype);
+  if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
+  if (M > 4) return fail(PMI_ERR_UNSUPPORTED, "%s: the fused GEMV takes M <= 4 (got %lld)", fn,
+                         (long long)M);
+  if (M == 0 || N == 0) return ok();
+  if (!x || !norm_weight || !w || !scales || !zeros || !y)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (residual && !h_out) return fail(PMI_ERR_INVALID, "%s: a residual needs h_out", fn);
+  if (!aligned(x, 16) || (residual && !aligned(residual, 16)) || !aligned(norm_weight, 16) ||
+      (h_out && !aligned(h_out, 16)))
+    return fail(PMI_ERR_INVALID, "%s: x, residual, norm_weight and h_out must be 16-byte aligned",
+                fn);
+  if (!aligned(w, 16)) return fail(PMI_ERR_INVALID, "%s: packed weight must be 16-byte aligned", fn);
+  if (!aligned(scales, 4)) return fail(PMI_ERR_INVALID, "%s: scales must be 4-byte aligned", fn);
+  if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
+  pmi::GemvXform xf;
+  xf.mode = 3;
+  xf.r = residual;
+  xf.w = norm_weight;
+  xf.eps = eps;
+  xf.h_out = h_out;
+  return from_hip(pmi::launch_gemv(x, w, scales, zeros, 1, nullptr, y, M, N, K, group_size,
+                                   (hipStream_t)stream, &xf),
                   fn);
 }
 

@@ -82,11 +82,21 @@ inline bool gemm_supported(int64_t K, int64_t gs) { return gs % 128 == 0 && K % 
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 
-// glu: x is the fused gate/up output [M, 2K], consumed as silu(gate) * up
-// (u8 zero points, no perm).
+// Activation transforms of the GEMV (u8 zero points, no perm):
+//   mode 2: x is the fused gate/up output [M, 2K], consumed as silu(gate) * up;
+//   mode 3: x is the residual stream [M, K], consumed as RMSNorm(x + r) * w
+//           (r nullable; h = x + r written to h_out when r is given).
+struct GemvXform {
+  int mode = 0;
+  const void* r = nullptr;
+  const void* w = nullptr;
+  float eps = 0.f;
+  void* h_out = nullptr;
+};
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
-                       int64_t K, int64_t gs, hipStream_t stream, bool glu = false);
+                       int64_t K, int64_t gs, hipStream_t stream,
+                       const GemvXform* xform = nullptr);
 
 // workspace: zero-filled before first use, left zeroed; may be smaller than
 // gemm_workspace_bytes() (then unsplit) but must hold the counter block and

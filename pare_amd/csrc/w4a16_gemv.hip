@@ -303,15 +303,46 @@ PMI_DEV uint32_t glu_pair(uint32_t g, uint32_t u) {
   return as_u32(o);
 }
 
+// h = x + r per fp16 pair, rounded as add_rmsnorm_kernel rounds it.
+PMI_DEV uint32_t add_pair(uint32_t x, uint32_t r) {
+  const f16x2 xh = as_f16x2(x), rh = as_f16x2(r);
+  f16x2 o;
+  o[0] = (f16)((float)xh[0] + (float)rh[0]);
+  o[1] = (f16)((float)xh[1] + (float)rh[1]);
+  return as_u32(o);
+}
+
+// (f16)(h * inv * w) per fp16 pair, as add_rmsnorm_kernel forms it.
+PMI_DEV uint32_t norm_pair(uint32_t h, uint32_t w, float inv) {
+  const f16x2 hh = as_f16x2(h), wh = as_f16x2(w);
+  f16x2 o;
+  o[0] = (f16)((float)hh[0] * inv * (float)wh[0]);
+  o[1] = (f16)((float)hh[1] * inv * (float)wh[1]);
+  return as_u32(o);
+}
+
+PMI_DEV float sq_pairs(const uint32_t (&v)[8], float acc) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f16x2 h = as_f16x2(v[i]);
+    acc = fmaf((float)h[0], (float)h[0], acc);
+    acc = fmaf((float)h[1], (float)h[1], acc);
+  }
+  return acc;
+}
+
 // XM selects the activation source: 0 x [M, K]; 1 x[:, perm] (act_order);
-// 2 the fused gate/up output [M, 2K], consumed as silu(gate) * up.
+// 2 the fused gate/up output [M, 2K], consumed as silu(gate) * up;
+// 3 RMSNorm(x + r) * w of the residual stream (xf.r nullable), with
+// h = x + r written to xf.h_out by workgroup 0.
 template <int MT, int U, int D, int SPW, int XM, bool ZU8>
 __global__ void __launch_bounds__(kMaxWaves * 64)
 w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   const float* __restrict__ scales, const void* __restrict__ zeros,
                   const int32_t* __restrict__ perm, f16* __restrict__ y, int N, int K, int gs,
-                  int n_slices, int slice_waves, int row_waves, int rows_per_wg) {
+                  int n_slices, int slice_waves, int row_waves, int rows_per_wg, GemvXform xf) {
   extern __shared__ float part[];  // [rows_per_wg][slice_waves][MT] when slice_waves > 1
+  __shared__ float nrm[XM == 3 ? kMaxWaves * 4 : 1];  // per-wave sums of h^2 (XM 3)
   constexpr int VP = Pow2Ceil<U * MT>::value;
   constexpr int LOGV = Log2<VP>::value;
 
@@ -339,7 +370,10 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   int boff[SPW], grp[SPW];
   bool act[SPW];
   uint32_t xa[SPW][MT][8], xb[SPW][MT][8];
-  uint32_t ua[XM == 2 ? SPW : 1][XM == 2 ? MT : 1][8], ub[XM == 2 ? SPW : 1][XM == 2 ? MT : 1][8];
+  constexpr int kXS = XM >= 2 ? SPW : 1, kXM = XM >= 2 ? MT : 1, kNS = XM == 3 ? SPW : 1;
+  uint32_t ua[kXS][kXM][8], ub[kXS][kXM][8];  // up (XM 2) or residual (XM 3)
+  uint32_t wa[kNS][8], wb[kNS][8];            // norm weight (XM 3)
+  int klo[SPW];
 #pragma unroll
   for (int sp = 0; sp < SPW; ++sp) {
     const int s = ws + sp * slice_waves;
@@ -351,9 +385,18 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     boff[sp] = b;
     grp[sp] = t;
     const int k_lo = t * gs + j;
+    klo[sp] = k_lo;
+    if constexpr (XM == 3)
+      load_x_raw<false>(reinterpret_cast<const f16*>(xf.w), perm, k_lo, k_lo + hgs, K, wa[sp],
+                        wb[sp]);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      if constexpr (XM == 2) {
+      if constexpr (XM == 3) {
+        load_x_raw<false>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
+        if (xf.r)
+          load_x_raw<false>(reinterpret_cast<const f16*>(xf.r) + (int64_t)m * K, perm, k_lo,
+                            k_lo + hgs, K, ua[sp][m], ub[sp][m]);
+      } else if constexpr (XM == 2) {
         load_x_raw<false>(x + (int64_t)m * 2 * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
         load_x_raw<false>(x + (int64_t)m * 2 * K + K, perm, k_lo, k_lo + hgs, K, ua[sp][m],
                           ub[sp][m]);
@@ -369,6 +412,61 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   float sx[SPW][MT];
   // Pairs the activations with the nibble order and sums each lane's 32.
   auto setup_x = [&]() {
+    if constexpr (XM == 3) {
+      // h = x + r; the RMS of every activation row over all K columns: each
+      // wave sums h^2 over its slices, the slice waves of row-wave group 0
+      // (which together cover K once) are added after one barrier.
+      float ss[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        ss[m] = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < SPW; ++sp) {
+          if (xf.r) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              xa[sp][m][i] = add_pair(xa[sp][m][i], ua[sp][m][i]);
+              xb[sp][m][i] = add_pair(xb[sp][m][i], ub[sp][m][i]);
+            }
+          }
+          if (act[sp]) ss[m] = sq_pairs(xb[sp][m], sq_pairs(xa[sp][m], ss[m]));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss[m] += __shfl_xor(ss[m], o, 64);
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) nrm[wave * 4 + m] = ss[m];
+      }
+      // LDS writes done (lgkmcnt(0)), then a bare s_barrier: __syncthreads()
+      // would also wait for every weight load in flight (vmcnt(0)) and drain
+      // the ring this prologue overlaps
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      barrier_only();
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float tot = 0.f;
+        for (int q = 0; q < slice_waves; ++q) tot += nrm[q * 4 + m];
+        const float inv = rsqrtf(tot / (float)K + xf.eps);
+#pragma unroll
+        for (int sp = 0; sp < SPW; ++sp) {
+          if (xf.r && blockIdx.x == 0 && wr == 0 && act[sp]) {
+            f16* hrow = reinterpret_cast<f16*>(xf.h_out) + (int64_t)m * K;
+            u32x4* ha = reinterpret_cast<u32x4*>(hrow + klo[sp]);
+            u32x4* hb = reinterpret_cast<u32x4*>(hrow + klo[sp] + hgs);
+            ha[0] = u32x4{xa[sp][m][0], xa[sp][m][1], xa[sp][m][2], xa[sp][m][3]};
+            ha[1] = u32x4{xa[sp][m][4], xa[sp][m][5], xa[sp][m][6], xa[sp][m][7]};
+            hb[0] = u32x4{xb[sp][m][0], xb[sp][m][1], xb[sp][m][2], xb[sp][m][3]};
+            hb[1] = u32x4{xb[sp][m][4], xb[sp][m][5], xb[sp][m][6], xb[sp][m][7]};
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xa[sp][m][i] = norm_pair(xa[sp][m][i], wa[sp][i], inv);
+            xb[sp][m][i] = norm_pair(xb[sp][m][i], wb[sp][i], inv);
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int sp = 0; sp < SPW; ++sp)
 #pragma unroll
@@ -458,17 +556,18 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 template <int MT, int U, int D, int SPW>
 hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                       const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                      int gs, bool glu, hipStream_t stream) {
+                      int gs, const GemvXform& xf, hipStream_t stream) {
   const dim3 block(64 * c.slice_waves * c.row_waves);
   const size_t lds = c.lds_bytes;
 #define PMI_GEMV_LAUNCH(XM, Z)                                                                  \
   hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
                      (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,       \
-                     c.slice_waves, c.row_waves, c.rows_per_wg)
-  if (glu) {
-    // the gated form is built for u8 zero points and no permutation only
+                     c.slice_waves, c.row_waves, c.rows_per_wg, xf)
+  if (xf.mode == 2 || xf.mode == 3) {
+    // the transformed activations are built for u8 zero points and no permutation only
     if (!zero_u8 || perm) return hipErrorInvalidValue;
-    PMI_GEMV_LAUNCH(2, true);
+    if (xf.mode == 2) PMI_GEMV_LAUNCH(2, true);
+    else PMI_GEMV_LAUNCH(3, true);
   } else if (perm) {
     if (zero_u8) PMI_GEMV_LAUNCH(1, true);
     else PMI_GEMV_LAUNCH(1, false);
@@ -489,10 +588,10 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
 template <int MT, int SPW>
 hipError_t launch_ud(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                     int gs, bool glu, hipStream_t stream) {
+                     int gs, const GemvXform& xf, hipStream_t stream) {
 #define PMI_GEMV_UD(U_, D_) \
   if (c.rows_per_wave == U_ && c.depth == D_) \
-    return launch_cfg<MT, U_, D_, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, glu, \
+    return launch_cfg<MT, U_, D_, SPW>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, xf, \
                                        stream)
   if constexpr (MT == 1) {
     PMI_GEMV_UD(4, 2);
@@ -520,10 +619,10 @@ hipError_t launch_ud(const GemvConfig& c, const void* x, const uint8_t* w, const
 template <int MT>
 hipError_t launch_mt(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
-                     int gs, bool glu, hipStream_t stream) {
+                     int gs, const GemvXform& xf, hipStream_t stream) {
   if (c.slices_per_wave == 2)
-    return launch_ud<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, glu, stream);
-  return launch_ud<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, glu, stream);
+    return launch_ud<MT, 2>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, xf, stream);
+  return launch_ud<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, xf, stream);
 }
 
 int env_int(const char* name, int dflt) {
@@ -616,14 +715,15 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
 
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
-                       int64_t K, int64_t gs, hipStream_t stream, bool glu) {
+                       int64_t K, int64_t gs, hipStream_t stream, const GemvXform* xform) {
   const GemvConfig c = gemv_config(M, N, K);
   const int n = (int)N, k = (int)K, g = (int)gs;
+  const GemvXform xf = xform ? *xform : GemvXform{};
   switch (M) {
-    case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
-    case 2: return launch_mt<2>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
-    case 3: return launch_mt<3>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
-    case 4: return launch_mt<4>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, glu, stream);
+    case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, xf, stream);
+    case 2: return launch_mt<2>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, xf, stream);
+    case 3: return launch_mt<3>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, xf, stream);
+    case 4: return launch_mt<4>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, xf, stream);
     default: return hipErrorInvalidValue;
   }
 }

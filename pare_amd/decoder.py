@@ -36,7 +36,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .config import QuantConfig
-from .kernels import _stream_handle, matmul_w4a16_glu
+from .kernels import _stream_handle, kernel_choice, matmul_w4a16_glu, matmul_w4a16_rmsnorm
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .quant import rtn_quantize
 
@@ -229,15 +229,18 @@ class DecoderLayer(nn.Module):
         device). Returns the new (h, d)."""
         cfg = self.cfg
         B, T, _ = h.shape
-        n1, h = add_rmsnorm(h, d, self.attn_norm.weight, cfg.rms_eps)
-        qkv = self.qkv.fused(n1)
         if not causal and T == 1:
-            # one new token: RoPE, the cache write and attention in one launch
+            # one new token: each residual add + RMSNorm runs inside the GEMV that
+            # consumes it where that is the GEMV, and RoPE, the cache write and
+            # attention are one launch
+            qkv, h = self._norm_linear(self.qkv.fused, h, d, self.attn_norm.weight)
             a = decode_attention_rope(qkv.reshape(B, -1), cos_t, sin_t, pos, cache_k, cache_v,
                                       1.0 / math.sqrt(cfg.head_dim))
-            n2, h = add_rmsnorm(h, self.o(a.reshape(B, 1, cfg.hidden)), self.mlp_norm.weight,
-                                cfg.rms_eps)
-            return h, self._mlp(n2, B, T)
+            gu, h = self._norm_linear(self.gate_up.fused, h, self.o(a.reshape(B, 1, cfg.hidden)),
+                                      self.mlp_norm.weight)
+            return h, self._down(gu, B, T)
+        n1, h = add_rmsnorm(h, d, self.attn_norm.weight, cfg.rms_eps)
+        qkv = self.qkv.fused(n1)
         q = rope_kv(qkv, cos_t, sin_t, pos, cache_k, cache_v, B, T, cfg.heads, cfg.kv_heads,
                     cfg.head_dim)
         if causal:
@@ -250,8 +253,30 @@ class DecoderLayer(nn.Module):
         n2, h = add_rmsnorm(h, self.o(a), self.mlp_norm.weight, cfg.rms_eps)
         return h, self._mlp(n2, B, T)
 
+    def _norm_linear(self, lin: QuantizedLinear, h, d, norm_w):
+        """(lin(RMSNorm(h + d) * norm_w), h + d) for one token per sequence: one
+        GEMV launch when the layer runs on the GEMV, else add_rmsnorm + lin."""
+        B, T, K = h.shape
+        M = B * T
+        # one activation row only: with more rows the per-row norm prologue of
+        # every wave costs more than the launch it saves (measured on the
+        # Llama q/k/v GEMV at 4 rows)
+        if M == 1 and lin.g_idx is None and \
+                kernel_choice(M, lin.out_features, K, lin._group_size()) == "gemv":
+            w_k, z_u8, _, _ = lin._kernel_buffers()
+            y, h2 = matmul_w4a16_rmsnorm(h.reshape(M, K), d.reshape(M, K) if d is not None else None,
+                                         norm_w, self.cfg.rms_eps, w_k, lin.scale, z_u8,
+                                         lin._group_size())
+            if lin.bias is not None:
+                y = y + lin.bias
+            return y.reshape(B, T, -1), h2.reshape(B, T, K)
+        n, h = add_rmsnorm(h, d, norm_w, self.cfg.rms_eps)
+        return lin(n), h
+
     def _mlp(self, n2, B: int, T: int):
-        gu = self.gate_up.fused(n2)
+        return self._down(self.gate_up.fused(n2), B, T)
+
+    def _down(self, gu, B: int, T: int):
         if B * T == 1 and self.down.g_idx is None:
             # one-token decode: the down GEMV forms silu(gate) * up itself, one
             # launch less (9.6 us against 11.4 us for silu_mul + GEMV on the

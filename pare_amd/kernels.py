@@ -220,6 +220,46 @@ def matmul_w4a16_glu(gate_up: torch.Tensor, packed_weight: torch.Tensor, scales:
     return out
 
 
+def matmul_w4a16_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor,
+                         eps: float, packed_weight: torch.Tensor, scales: torch.Tensor,
+                         zeros_u8: torch.Tensor, group_size: int):
+    """(Y, h) with h = x + residual (x when residual is None) and
+    Y = (RMSNorm(h) * norm_weight) @ dequant(W)^T, for M <= 4: a decoder's
+    residual add and pre-norm fused into the GEMV. x, residual: fp16 [M, K];
+    norm_weight fp16 [K]; zeros_u8 uint8 [N, G]."""
+    L = _lib.lib()
+    if not x.is_cuda:
+        raise RuntimeError("matmul_w4a16_rmsnorm requires HIP (cuda) tensors.")
+    assert x.dtype == torch.float16 and x.dim() == 2 and x.is_contiguous(), \
+        "x must be a contiguous float16 [M, K] tensor"
+    M, K = x.shape
+    N, K_half = packed_weight.shape
+    assert K == 2 * K_half, f"x has {K} columns, expected K={2 * K_half}"
+    assert M <= 4, f"the fused GEMV takes M <= 4, got {M}"
+    assert norm_weight.dtype == torch.float16 and norm_weight.numel() == K
+    z2 = _to_2d(zeros_u8)
+    assert z2.dtype == torch.uint8, "zeros must be uint8 [N, G]"
+    s2 = _to_2d(scales).float().contiguous()
+    dev = x.device
+    xa = _aligned16(x)
+    r = None
+    h = x
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == torch.float16
+        r = _aligned16(residual.contiguous())
+        h = torch.empty_like(x)   # never aliases x or residual: other workgroups still read them
+    out = torch.empty(M, N, device=dev, dtype=torch.float16)
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16_rmsnorm(
+            xa.data_ptr(), r.data_ptr() if r is not None else None,
+            _aligned16(norm_weight.contiguous()).data_ptr(), eps,
+            h.data_ptr() if r is not None else None,
+            _aligned16(packed_weight.contiguous()).data_ptr(), s2.data_ptr(),
+            z2.contiguous().data_ptr(), _lib.PMI_U8, out.data_ptr(), M, N, K, group_size,
+            _stream_handle(dev)), "pmi_matmul_w4a16_rmsnorm")
+    return out, h
+
+
 _KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4}
 
 

@@ -188,6 +188,35 @@ def test_decode_attention_rope_equals_the_two_launches(B, H, KV, L, p):
     assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 6144, 4096), (2, 28672, 4096), (3, 6144, 4096),
+                                   (4, 6144, 4096), (1, 136, 512), (2, 200, 8192)])
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_rmsnorm_gemv_matches_norm_then_matmul(M, N, K, with_residual):
+    """The GEMV with the residual add + RMSNorm inside against add_rmsnorm
+    followed by the plain matmul: h bit for bit, y within the fp16 ulp the
+    differently ordered mean can move an activation by."""
+    from pare_amd.kernels import matmul_w4a16, matmul_w4a16_rmsnorm
+    from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
+
+    g = torch.Generator(device=DEV).manual_seed(M * N + K + int(with_residual))
+    x = torch.randn(M, K, generator=g, device=DEV).half()
+    r = torch.randn(M, K, generator=g, device=DEV).half() if with_residual else None
+    nw = (1 + 0.1 * torch.randn(K, generator=g, device=DEV)).half()
+    w = torch.randn(N, K, generator=g, device=DEV) * 0.02
+    packed, s, z = P.rtn_quantize(w, 128)
+    wk = repack_int4_for_kernel(packed, 128)
+    zu = zeros_to_u8(z)
+    y, h = matmul_w4a16_rmsnorm(x, r, nw, 1e-5, wk, s, zu, 128)
+    n_ref, h_ref = add_rmsnorm(x, r, nw, 1e-5)
+    y_ref = matmul_w4a16(n_ref, wk, s, zu, 128)
+    assert torch.equal(h, h_ref)
+    err = (y.float() - y_ref.float()).abs().max().item()
+    scale = y_ref.float().abs().max().item()
+    print(f"[rmsnorm-gemv] M={M} N={N} K={K} r={with_residual}: max_abs={err:.3e} (max {scale:.2f})",
+          flush=True)
+    assert err <= 2e-3 * scale + 1e-3
+
+
 @pytest.mark.parametrize("M,N,F", [(1, 4096, 14336), (2, 4096, 14336), (3, 1024, 4096),
                                    (4, 4096, 14336), (1, 136, 512), (4, 200, 1024)])
 def test_glu_down_matches_silu_then_matmul(M, N, F):
