@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 8
+#define PMI_ABI_VERSION 9
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -318,6 +318,17 @@ PMI_API int pmi_decode_attention_rope_f16(const void* qkv, const float* cos, con
 /* Workspace bytes of the split pmi_decode_attention_f16 (0 for bad shapes).
  * Host-only. */
 PMI_API size_t pmi_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t KV, int64_t L);
+
+/* Greedy decoding's argmax: out[r * out_stride] (int64) = index of the largest
+ * value of x[r, 0:n] (fp16, rows 16-byte aligned, n % 8 == 0), the first one
+ * on ties, NaN counted as largest (torch.argmax's rule). workspace: device
+ * scratch of pmi_argmax_workspace_bytes(rows, n) bytes, 256-byte aligned and
+ * zero-filled before its first use; each call leaves it zero-filled again.
+ * Calls that may run concurrently must not share it. */
+PMI_API int pmi_argmax_f16(const void* x, int64_t rows, int64_t n, int64_t* out,
+                           int64_t out_stride, void* workspace, size_t workspace_bytes,
+                           void* stream);
+PMI_API size_t pmi_argmax_workspace_bytes(int64_t rows, int64_t n);
 
 /* out[r, c] = silu(gate_up[r, c]) * gate_up[r, F + c]; gate_up [rows, 2F],
  * out [rows, F] fp16; F % 8 == 0. */

@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -68,6 +68,8 @@ SIGNATURES = {
                                            _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                                            _vp]),
     "pmi_decode_attention_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
+    "pmi_argmax_f16": (_i, [_vp, _i64, _i64, _vp, _i64, _vp, ctypes.c_size_t, _vp]),
+    "pmi_argmax_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
     "pmi_silu_mul_f16": (_i, [_vp, _vp, _i64, _i64, _vp]),
 }
 

@@ -546,6 +546,30 @@ int pmi_decode_attention_rope_f16(const void* qkv, const float* cos, const float
                   fn);
 }
 
+size_t pmi_argmax_workspace_bytes(int64_t rows, int64_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  return pmi::argmax_ws_bytes(rows, n);
+}
+
+int pmi_argmax_f16(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t out_stride,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "pmi_argmax_f16";
+  if (rows < 0 || n <= 0 || n % 8 != 0 || n >= (1ll << 31) || out_stride < 1)
+    return fail(PMI_ERR_INVALID, "%s: need rows >= 0, 0 < n < 2^31 with n %% 8 == 0, out_stride >= 1",
+                fn);
+  if (rows == 0) return ok();
+  if (rows > 65535) return fail(PMI_ERR_UNSUPPORTED, "%s: at most 65535 rows", fn);
+  const size_t need = pmi::argmax_ws_bytes(rows, n);
+  if (!workspace || workspace_bytes < need)
+    return fail(PMI_ERR_INVALID, "%s: needs a zero-filled workspace of pmi_argmax_workspace_bytes "
+                "(%zu) bytes", fn, need);
+  if (!x || !out) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(x, 16) || !aligned(out, 8) || !aligned(workspace, 256))
+    return fail(PMI_ERR_INVALID, "%s: x 16-byte, out 8-byte and workspace 256-byte aligned", fn);
+  return from_hip(pmi::launch_argmax(x, rows, n, out, out_stride, workspace, (hipStream_t)stream),
+                  fn);
+}
+
 int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64_t F, void* stream) {
   const char* fn = "pmi_silu_mul_f16";
   if (rows < 0 || F <= 0 || F % 8 != 0)

@@ -432,6 +432,100 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
     __hip_atomic_store(&counters[bk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Greedy token choice: out[r * out_stride] = the index of the largest value of
+// x[r, 0:n] (the first one on ties; NaN counts as largest, as torch.argmax
+// treats it). Workgroup (chunk c, row r) scans 8192 values with 16-byte loads;
+// its (value, index) goes to the workspace with device-scope (sc1) stores and
+// the last workgroup of the row, counted with an agent-scope atomic, combines
+// the chunks and resets the counter.
+constexpr int kArgChunk = 8192;
+
+PMI_DEV bool arg_better(float v, int i, float b, int bi) {
+  if (bi < 0) return true;
+  if (v != v) return b == b || i < bi;  // NaN beats numbers; the first NaN wins
+  if (b != b) return false;
+  return v > b || (v == b && i < bi);
+}
+
+PMI_DEV void arg_wave_reduce(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(v, o);
+    const int oi = __shfl_xor(i, o);
+    if (oi >= 0 && arg_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const f16* __restrict__ x, int n, int chunks,
+                                                     int64_t* __restrict__ out, int64_t out_stride,
+                                                     int* __restrict__ counters,
+                                                     float* __restrict__ part) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  __shared__ int last_flag;
+  const int c = blockIdx.x, r = blockIdx.y, t = threadIdx.x, l = t & 63, w = t >> 6;
+  const f16* row = x + (size_t)r * n;
+  const int c0 = c * kArgChunk, c1 = min(n, c0 + kArgChunk);
+  float best = 0.f;
+  int bi = -1;
+#pragma unroll
+  for (int k = 0; k < kArgChunk / 2048; ++k) {
+    const int i0 = c0 + (k * 256 + t) * 8;
+    if (i0 < c1) {  // n % 8 == 0: a chunk of 8 is whole
+      const f16x8 v8 = *reinterpret_cast<const f16x8*>(row + i0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (arg_better((float)v8[e], i0 + e, best, bi)) {
+          best = (float)v8[e];
+          bi = i0 + e;
+        }
+    }
+  }
+  arg_wave_reduce(best, bi);
+  if (l == 0) {
+    sv[w] = best;
+    si[w] = bi;
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rp = rsrc(part, (int64_t)gridDim.y * chunks * 8);
+  if (t == 0) {
+    for (int q = 1; q < 4; ++q)
+      if (si[q] >= 0 && arg_better(sv[q], si[q], best, bi)) {
+        best = sv[q];
+        bi = si[q];
+      }
+    const int off = (r * chunks + c) * 8;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), rp, off, 0, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)bi, rp, off + 4, 0, kSc1);
+    __builtin_amdgcn_s_waitcnt(0);
+    const int old = __hip_atomic_fetch_add(&counters[r], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = old == chunks - 1;
+  }
+  __syncthreads();
+  if (!last_flag || w != 0) return;
+  // last to arrive: lane q takes chunks q, q + 64, ...
+  float v = 0.f;
+  int vi = -1;
+  for (int q = l; q < chunks; q += 64) {
+    const int off = (r * chunks + q) * 8;
+    const float qv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, kSc1));
+    const int qi = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, off + 4, 0, kSc1);
+    if (qi >= 0 && arg_better(qv, qi, v, vi)) {
+      v = qv;
+      vi = qi;
+    }
+  }
+  arg_wave_reduce(v, vi);
+  if (l == 0) {
+    out[(int64_t)r * out_stride] = vi;
+    __hip_atomic_store(&counters[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // out[r, c] = silu(gu[r, c]) * gu[r, F + c] for c < F.
 __global__ void silu_mul_kernel(const f16* __restrict__ gu, f16* __restrict__ out, int rows,
                                 int F) {
@@ -504,6 +598,21 @@ hipError_t launch_decode_attention(const void* q, const void* cache_k, const voi
                      dim3(64 * group * kQuarters), lds, stream, (const f16*)q,
                      (const f16*)cache_k, (const f16*)cache_v, pos, (f16*)out, (int)H, (int)KV,
                      (int)L, scale);
+  return hipGetLastError();
+}
+
+size_t argmax_ws_bytes(int64_t rows, int64_t n) {
+  const int64_t chunks = (n + kArgChunk - 1) / kArgChunk;
+  return decode_attention_counter_bytes(rows, 1) + (size_t)(rows * chunks * 8);
+}
+
+hipError_t launch_argmax(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t out_stride,
+                         void* workspace, hipStream_t stream) {
+  const int chunks = (int)((n + kArgChunk - 1) / kArgChunk);
+  int* counters = (int*)workspace;
+  float* part = (float*)((char*)workspace + decode_attention_counter_bytes(rows, 1));
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)chunks, (unsigned)rows), dim3(256), 0, stream,
+                     (const f16*)x, (int)n, chunks, out, out_stride, counters, part);
   return hipGetLastError();
 }
 

@@ -132,6 +132,11 @@ hipError_t launch_decode_attention(const void* q, const void* cache_k, const voi
                                    int64_t KV, int64_t L, float scale, void* workspace,
                                    size_t ws_bytes, hipStream_t stream,
                                    const float* cos_t = nullptr, const float* sin_t = nullptr);
+// Greedy argmax over fp16 rows; workspace: int32 counters [rows] (zero
+// between calls, 256-byte padded), then (value, index) per (row, chunk).
+size_t argmax_ws_bytes(int64_t rows, int64_t n);
+hipError_t launch_argmax(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t out_stride,
+                         void* workspace, hipStream_t stream);
 hipError_t launch_silu_mul(const void* gu, void* out, int64_t rows, int64_t F, hipStream_t stream);
 
 hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* perm, int64_t N,

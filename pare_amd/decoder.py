@@ -173,6 +173,30 @@ def decode_attention_rope(qkv, cos, sin, pos, cache_k, cache_v, scale: float):
     return out
 
 
+_ARGMAX_WORKSPACES: dict = {}
+
+
+def argmax_into(x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[r] = argmax of row r of x [rows, n] fp16 (the first index on ties),
+    in one launch through a cached zero-filled workspace (allocated by the
+    first, eager call so that graph captures reuse it). ``out``: int64 with one
+    element per row at a constant stride (e.g. a [rows, 1] token buffer)."""
+    rows, n = x.shape
+    assert out.dtype == torch.int64 and out.numel() == rows
+    L_ = _lib.lib()
+    stream = _stream_handle(x.device)
+    nbytes = L_.pmi_argmax_workspace_bytes(rows, n)
+    key = (x.device.index if x.device.index is not None else torch.cuda.current_device(), stream)
+    ws = _ARGMAX_WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 12), dtype=torch.uint8, device=x.device)
+        _ARGMAX_WORKSPACES[key] = ws
+    stride = out.stride(0) if out.dim() >= 1 and rows > 1 else 1
+    _check(L_.pmi_argmax_f16(x.data_ptr(), rows, n, out.data_ptr(), stride, ws.data_ptr(),
+                             nbytes, stream), "pmi_argmax_f16")
+    return out
+
+
 def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up of a fused [.., 2F] gate/up output."""
     F2 = gu.shape[-1]
@@ -350,9 +374,16 @@ class QuantizedDecoder(nn.Module):
         mask = torch.zeros(L, dtype=torch.bool, device=dev)
 
         def step():
+            # the step's greedy token replaces its input token (the fused path
+            # runs the argmax in the graph, after the embedding has read tok)
             if not self.fused_ops:
                 mask.copy_(ar <= pos)
-            return self.forward_tokens(tok, cos, sin, cache, pos, mask, False)[:, -1]
+                logits = self.forward_tokens(tok, cos, sin, cache, pos, mask, False)[:, -1]
+                tok.copy_(logits.argmax(-1, keepdim=True))
+                return logits
+            logits = self.forward_tokens(tok, cos, sin, cache, pos, mask, False)[:, -1]
+            argmax_into(logits.contiguous(), tok)
+            return logits
 
         graph = None
         if use_graph:
@@ -366,7 +397,7 @@ class QuantizedDecoder(nn.Module):
                 step()
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, stream=s):
-                    logits_static = step()
+                    step()
             torch.cuda.current_stream(dev).wait_stream(s)
             for ck, cv in cache:
                 ck.zero_()
@@ -376,18 +407,17 @@ class QuantizedDecoder(nn.Module):
         t0 = time.perf_counter()
         logits = self.forward_tokens(prompt, cos, sin, cache, torch.arange(P, device=dev), None,
                                      True)[:, -1]
-        out[:, 0] = logits.argmax(-1)
+        tok.copy_(logits.argmax(-1, keepdim=True))
+        out[:, 0] = tok[:, 0]
         torch.cuda.synchronize(dev)
         t1 = time.perf_counter()
         for i in range(1, n_generate):
-            tok.copy_(out[:, i - 1:i])
             pos.fill_(P + i - 1)
             if graph is not None:
                 graph.replay()
-                logits = logits_static
             else:
-                logits = step()
-            out[:, i] = logits.argmax(-1)
+                step()
+            out[:, i] = tok[:, 0]
         torch.cuda.synchronize(dev)
         t2 = time.perf_counter()
         return out, {"prefill_s": t1 - t0, "decode_s": t2 - t1, "elapsed_s": t2 - t0}

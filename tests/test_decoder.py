@@ -252,6 +252,30 @@ def test_glu_down_rejects_what_it_does_not_run():
                                   None) == _lib.PMI_ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("rows,n", [(1, 128256), (4, 128256), (3, 2000), (2, 8), (1, 16392)])
+def test_argmax_matches_torch(rows, n):
+    from pare_amd.decoder import argmax_into
+
+    g = torch.Generator(device=DEV).manual_seed(rows * n)
+    x = torch.randn(rows, n, generator=g, device=DEV).half()
+    # ties: the maximum twice in row 0, the first must win
+    m = x[0].max()
+    x[0, n // 3] = m + 1
+    x[0, n // 2] = m + 1
+    for _ in range(2):   # the workspace counters must be back at zero
+        out = torch.full((rows, 1), -7, dtype=torch.long, device=DEV)
+        argmax_into(x, out)
+        assert torch.equal(out[:, 0], x.argmax(-1)), (out[:, 0], x.argmax(-1))
+    assert out[0, 0].item() == n // 3
+    # NaN counts as the largest value, the first one wins
+    if n >= 16:
+        x[0, 5] = float("nan")
+        x[0, 9] = float("nan")
+        out = torch.empty(rows, dtype=torch.long, device=DEV)
+        argmax_into(x, out)
+        assert out[0].item() == 5
+
+
 @pytest.mark.parametrize("rows,F", [(1, 14336), (4, 1024)])
 def test_silu_mul(rows, F):
     g = torch.Generator(device=DEV).manual_seed(rows + F)
