@@ -21,6 +21,7 @@ struct GemvConfig {
 
 struct GemmConfig {
   int m_tiles;      // 16-row MFMA activation tiles per workgroup (1, 2 or 4)
+  int n_t;          // 16-row weight tiles per compute wave (4: 128-row tiles, 2: 64-row)
   int n_tiles;      // 128-row weight tiles
   int grid_m;       // activation row blocks of 16 * m_tiles
   int splits;       // workgroups sharing one tile's K range

@@ -1,12 +1,13 @@
 // Split-K MFMA INT4 W4A16 GEMM for M > 4, gfx950 (v_mfma_f32_16x16x32_f16).
 //
 // Work layout. A workgroup is 4 compute waves and 4 producer waves (two waves
-// per SIMD) and owns 128 weight rows (a "tile") for up to 64 activation rows
-// (MT MFMA row tiles of 16), over a contiguous range of "units". A unit is 128
+// per SIMD) and owns 128 weight rows (a "tile"; 64 with NT = 2) for up to 64
+// activation rows (MT MFMA row tiles of 16), over a contiguous range of
+// "units". A unit is 128
 // columns of K: 64 bytes of every packed row (kernel layout), i.e. columns
 // k0+64c+b (low nibble of byte b) and k0+gs/2+64c+b (high nibble), b < 64, of
 // the group starting at k0. Units are consumed in pairs: compute wave w takes
-// weight rows 64*(w&1)..+63 (four 16-row MFMA tiles) of the pair's unit w>>1,
+// weight rows 16 NT (w&1)..+16 NT - 1 (NT 16-row MFMA tiles) of the pair's unit w>>1,
 // so each wave reads from LDS only the activations of its own units and every
 // activation fragment it reads feeds four weight tiles. The two k-parities
 // are added through LDS at the end. The producer waves only issue the copies
@@ -71,13 +72,14 @@ constexpr int kZBytes = kBN * 4;        // zero-point words of one unit
 // halves one unit would give.
 constexpr int kWLines = kBN * 128;                              // weight bytes of a pair
 constexpr int kWPair = kWLines + 2 * (kSBytes + kZBytes);       // weight slot of a pair
-template <int MT>
+template <int MT, int NT>
 struct Tiling {
   static constexpr int R = 16 * MT;                             // activation rows
   static constexpr int kX = R * 256;                            // activation tile of a unit
   static constexpr int PW = MT == 4 ? 5 : 6;                    // weight pairs in the ring
   static constexpr int PX = MT == 4 ? 2 : 3;                    // activation pairs in the ring
-  static constexpr int kWCopies = 12;                           // per weight producer per pair
+  // per weight producer per pair: 2 NT copies of 8 rows, NT scale/zero copies
+  static constexpr int kWCopies = 3 * NT;
   static constexpr int kXCopies = 4 * MT;                       // per activation producer per pair
 };
 
@@ -104,10 +106,15 @@ PMI_DEV void static_for(F&& f) {
 
 // SZT: scales and zero points come from the group-major copies (one unit's
 // 128 rows are 512 + 128 contiguous bytes) instead of a gather over 128 rows
-// of the [N, G] arrays.
-template <int MT, bool ZU8, bool SZT>
+// of the [N, G] arrays. NT: 16-row weight tiles per compute wave, 4 (tiles of
+// 128 rows) or 2 (tiles of 64 rows, twice the tiles for the same N: with
+// MT = 4 one pass over the CUs without a K split at 33-64 activation rows).
+template <int MT, bool ZU8, bool SZT, int NT>
 __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
-  using T = Tiling<MT>;
+  constexpr int kNT = NT, kBN = 32 * NT, R2 = 16 * NT, HALVES = NT / 2;
+  constexpr int kSBytes = kBN * 4, kZBytes = kBN * 4;
+  constexpr int kWLines = kBN * 128, kWPair = kWLines + 2 * (kSBytes + kZBytes);
+  using T = Tiling<MT, NT>;
   constexpr int R = T::R, kX = T::kX, PW = T::PW, PX = T::PX;
   constexpr int kWC = T::kWCopies, kXC = T::kXCopies;
   static_assert(PW >= 2 && (PW - 1) * kWC < 64 && PX >= 2 && (PX - 1) * kXC < 64,
@@ -165,29 +172,29 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
     for (int j = 0; j < kNT; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (wprod) {
-    // ---- weight producer pw: rows 64*pw .. +63 as 8 copies of 8 rows x 128
-    // bytes (lane l: row 8i + l/8, chunk l%8 of the LDS row, which holds the
-    // pair's chunk (l%8) ^ (row%8)), and the scale (pw 0) or zero-point (pw 1)
-    // words of rows 0..63 and 64..127 of both units
+    // ---- weight producer pw: rows R2*pw .. +R2-1 as 2 NT copies of 8 rows x
+    // 128 bytes (lane l: row 8i + l/8, chunk l%8 of the LDS row, which holds
+    // the pair's chunk (l%8) ^ (row%8)), and the scale (pw 0) or zero-point
+    // (pw 1) words of the tile's rows, 64 per copy, of both units
     const __amdgpu_buffer_rsrc_t rw = rsrc(a.w, (int64_t)N * row_bytes);
-    int vl[8];
+    int vl[2 * NT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rloc = 64 * pw + 8 * i + (l >> 3);
+    for (int i = 0; i < 2 * NT; ++i) {
+      const int rloc = R2 * pw + 8 * i + (l >> 3);
       int n = tile * kBN + rloc;
       n = n < N ? n : N - 1;
       vl[i] = n * row_bytes + 16 * ((l & 7) ^ (rloc & 7));
     }
     const bool scale = pw == 0;
     __amdgpu_buffer_rsrc_t rsz;
-    int gmul, vsz[2];
+    int gmul, vsz[HALVES];
     if constexpr (SZT) {
       // scales: rows h*64 + l; zero bytes: rows h*64 + 4l .. +3 (lanes 16..63
       // repeat lanes 0..15; rows past N are clamped into the array, N % 4 == 0)
       rsz = scale ? rsrc(a.s_gm, (int64_t)G * N * 4) : rsrc(a.z_gm, (int64_t)G * N);
       gmul = scale ? 4 * N : N;  // bytes per group
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < HALVES; ++h) {
         int n = scale ? tile * kBN + 64 * h + l : tile * kBN + 64 * h + 4 * (l & 15);
         const int nmax = scale ? N - 1 : N - 4;
         n = n < nmax ? n : nmax;
@@ -200,7 +207,7 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
                   : rsrc(a.z, ZU8 ? (((int64_t)N * G + 3) & ~(int64_t)3) : (int64_t)N * G * 4);
       gmul = (scale || !ZU8) ? 4 : 1;  // bytes per (row, group) entry
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < HALVES; ++h) {
         int n = tile * kBN + 64 * h + l;
         n = n < N ? n : N - 1;
         vsz[h] = n * G * gmul;
@@ -213,13 +220,14 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
       u0 = u0 < u_end - 2 ? u0 : u_end - 2;
       const int woff = __builtin_amdgcn_readfirstlane(u0 * 64);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) copy_to_lds<16>(rw, base + (64 * pw + 8 * i) * 128, vl[i], woff);
+      for (int i = 0; i < 2 * NT; ++i)
+        copy_to_lds<16>(rw, base + (R2 * pw + 8 * i) * 128, vl[i], woff);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int g = (u0 + e) / upg;
         uint8_t* sz = base + kWLines + e * (kSBytes + kZBytes) + pw * kSBytes;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < HALVES; ++h) {
           if constexpr (SZT)
             copy_to_lds<4>(rsz, sz + h * 256, vsz[h], __builtin_amdgcn_readfirstlane(g * gmul));
           else
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
     int zrow[kNT];
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
-      int n = tile * kBN + 64 * rh + 16 * j + ln;
+      int n = tile * kBN + R2 * rh + 16 * j + ln;
       n = n < N ? n : N - 1;
       zrow[j] = n * G;
     }
@@ -298,13 +306,13 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
         float sc[kNT];
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
-          const int row = 64 * rh + 16 * j + ln;
+          const int row = R2 * rh + 16 * j + ln;
           // 16 bytes of this unit: chunk 4*kp + kq of the row's 128, swizzled
           w[j] = *reinterpret_cast<const u32x4*>(wb + row * 128 + 16 * ((4 * kp + kq) ^ (row & 7)));
           sc[j] = *reinterpret_cast<const float*>(szb + 4 * row);
           uint32_t z;
           if constexpr (SZT) {
-            z = szb[kSBytes + 256 * rh + 16 * j + ln];  // rows 64h + 4l.. at 256h + 4l
+            z = szb[kSBytes + 256 * (row >> 6) + (row & 63)];  // rows 64h + 4l.. at 256h + 4l
           } else {
             const uint32_t zw = *reinterpret_cast<const uint32_t*>(szb + kSBytes + 4 * row);
             z = ZU8 ? (zw >> (((zrow[j] + g) & 3) * 8)) & 0xFFu
@@ -365,7 +373,7 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
   }
 
   // ---- epilogue (waves of k parity 0 hold the sums) ------------------------
-  const int n0 = tile * kBN + 64 * rh + ln;
+  const int n0 = tile * kBN + R2 * rh + ln;
   const int m0 = mb * R + 4 * kq;
   if (a.splits > 1) {
     // Partial tile of split sp: [row half][mt][j][lane] x 16 bytes (each lane's
@@ -482,14 +490,17 @@ int device_cus() {
 constexpr size_t kCounterBytes = kWsCounterBytes;
 constexpr int64_t kMaxCounters = kCounterBytes / 4;
 
-template <int MT>
+template <int MT, int NT>
 hipError_t launch_mt(const GemmConfig& c, const GemmArgs& a, int zero_u8, hipStream_t stream) {
   if (a.s_gm)
-    hipLaunchKernelGGL((w4a16_gemm_kernel<MT, true, true>), dim3(c.grid), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_gemm_kernel<MT, true, true, NT>), dim3(c.grid), dim3(kThreads), 0,
+                       stream, a);
   else if (zero_u8)
-    hipLaunchKernelGGL((w4a16_gemm_kernel<MT, true, false>), dim3(c.grid), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_gemm_kernel<MT, true, false, NT>), dim3(c.grid), dim3(kThreads), 0,
+                       stream, a);
   else
-    hipLaunchKernelGGL((w4a16_gemm_kernel<MT, false, false>), dim3(c.grid), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_gemm_kernel<MT, false, false, NT>), dim3(c.grid), dim3(kThreads), 0,
+                       stream, a);
   return hipGetLastError();
 }
 
@@ -510,12 +521,21 @@ GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_per
   // pass over the CUs (it needs fewer K splits, whose partial tiles are added
   // at the end); otherwise one 64-row block, which reads the weights once.
   static const int env_mt = env_int("PMI_GEMM_MT", 0);
+  static const int env_nt = env_int("PMI_GEMM_NT", 0);
   const int64_t n_tiles = (N + kBN - 1) / kBN;
-  c.m_tiles = M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 64 && 2 * n_tiles <= device_cus() ? 2 : 4));
+  // 33..64 rows with N <= 16384: one 64-row block over 64-row weight tiles
+  // (NT = 2): twice the tiles of 128-row ones, and every B operand built once
+  // for four activation tiles instead of two. Measured on MI355X at M = 64
+  // (48 weight copies beyond the MALL): o/q 12.2 us against 12.9 us for two
+  // 32-row blocks, fused q/k/v 13.8 against 14.7, gate 20.0 against 20.3.
+  const bool wide64 = M > 32 && M <= 64 && N <= 16384;
+  c.m_tiles = M <= 16 ? 1 : (M <= 32 ? 2 : (wide64 ? 4 : (M <= 64 && 2 * n_tiles <= device_cus() ? 2 : 4)));
   if (env_mt == 1 || env_mt == 2 || env_mt == 4) c.m_tiles = env_mt;
   const int64_t bm = 16 * c.m_tiles;
   c.grid_m = (int)((M + bm - 1) / bm);
-  c.n_tiles = (int)((N + kBN - 1) / kBN);
+  c.n_t = c.m_tiles == 4 && (env_nt == 2 || (env_nt == 0 && wide64)) ? 2 : 4;
+  const int64_t bn = 32 * c.n_t;
+  c.n_tiles = (int)((N + bn - 1) / bn);
   const int64_t units = K / 128;
   const int64_t tiles = (int64_t)c.n_tiles * c.grid_m;
   static const int env_s = env_int("PMI_GEMM_SPLITS", 0);
@@ -527,7 +547,7 @@ GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_per
   c.splits = (int)s;
   c.grid = (int)(tiles * c.splits);
   c.ws_perm = has_perm ? ws_perm_bytes(M, K) : 0;
-  c.ws_split = c.splits > 1 ? ws_align((size_t)tiles * c.splits * bm * kBN * 4) : 0;
+  c.ws_split = c.splits > 1 ? ws_align((size_t)tiles * c.splits * bm * bn * 4) : 0;
   return c;
 }
 
@@ -577,9 +597,10 @@ hipError_t launch_gemm(const void* x, const uint8_t* w, const float* scales, con
   a.splits = c.splits;
   a.n_tiles = c.n_tiles;
   a.grid_m = c.grid_m;
-  if (c.m_tiles == 1) return launch_mt<1>(c, a, zero_u8, stream);
-  if (c.m_tiles == 2) return launch_mt<2>(c, a, zero_u8, stream);
-  return launch_mt<4>(c, a, zero_u8, stream);
+  if (c.m_tiles == 1) return launch_mt<1, 4>(c, a, zero_u8, stream);
+  if (c.m_tiles == 2) return launch_mt<2, 4>(c, a, zero_u8, stream);
+  if (c.n_t == 2) return launch_mt<4, 2>(c, a, zero_u8, stream);
+  return launch_mt<4, 4>(c, a, zero_u8, stream);
 }
 
 }  // namespace pmi
