@@ -328,14 +328,16 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm64_kernel(Gemm64Args a)
     }
     __syncthreads();
     if (!last_flag || !lead) return;
-    // Last to arrive: add the partials in split order (deterministic).
+    // Last to arrive: add the partials in split order (deterministic). Every
+    // split's partial, this one's included, is in the workspace; the loads of
+    // kB splits are issued together (one round trip per kB splits).
+    constexpr int kB = MT >= 2 ? 2 : 4;
     f32x16 tot[MT];
-    for (int q = 0; q < a.splits; ++q) {
-      f32x16 part[MT];
-      if (q == sp) {
+    for (int q0 = 0; q0 < a.splits; q0 += kB) {
+      f32x16 part[kB][MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) part[mt] = acc[mt];
-      } else {
+      for (int sb = 0; sb < kB; ++sb) {
+        const int q = q0 + sb < a.splits ? q0 + sb : a.splits - 1;  // past the end: loaded, not added
         const int soff = __builtin_amdgcn_readfirstlane(q * kPartBytes);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -344,11 +346,15 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm64_kernel(Gemm64Args a)
             const f32x4 v = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, vlane + (mt * 4 + b) * 1024, soff, kSc1));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) part[mt][4 * b + e] = v[e];
+            for (int e = 0; e < 4; ++e) part[sb][mt][4 * b + e] = v[e];
           }
       }
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) tot[mt] = q == 0 ? part[mt] : tot[mt] + part[mt];
+      for (int sb = 0; sb < kB; ++sb) {
+        if (q0 + sb >= a.splits) break;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) tot[mt] = q0 + sb == 0 ? part[sb][mt] : tot[mt] + part[sb][mt];
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = tot[mt];

@@ -74,8 +74,12 @@ def _loops(body: str) -> list[str]:
 
 def test_every_gemm_variant_compiled(gemm_asm):
     names = _kernels(gemm_asm)
-    # MT in {1, 2, 4} x {fp32 zeros, u8 zeros, group-major scales/zeros}
-    assert len(names) == 9, sorted(names)
+    # MT in {1, 2, 4} x {fp32 zeros, u8 zeros, group-major scales/zeros} with
+    # 128-row weight tiles (NT = 4), and MT = 4 again with 64-row tiles (NT = 2)
+    tiles = sorted(re.search(r"gemm_kernelILi(\d)ELb(\d)ELb(\d)ELi(\d)E", n).groups() for n in names)
+    expect = sorted([(mt, z, g, "4") for mt in "124" for z, g in (("0", "0"), ("1", "0"), ("1", "1"))]
+                    + [("4", z, g, "2") for z, g in (("0", "0"), ("1", "0"), ("1", "1"))])
+    assert tiles == expect, sorted(names)
 
 
 def test_gemm_compute_loop_never_waits_for_copies(gemm_asm):
