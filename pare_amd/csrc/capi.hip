@@ -159,11 +159,14 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   const int forced = g_kernel_override.load();
   if (forced) return forced;
   // Measured on MI355X (gate/up/down and q/k/v/o shapes): the GEMV wins up to
-  // M = 2, and up to M = 4 for N < 8192, where the GEMM's K splits cost more
-  // than its matrix cores save; the skinny kernel wins over the GEMM for
-  // N <= 8192 while the activations fit its LDS.
+  // M = 2, and up to M = 4 for N < 8192 with K <= 8192, where the GEMM's K
+  // splits cost more than its matrix cores save. With long rows the GEMV's
+  // four activation rows cost more than the splits: down_proj at M = 4 takes
+  // 16.5 against 15.0 us (4096 x 14336) and 31.9 against 16.2 us (3584 x
+  // 18944; 20.2 against 16.2 at M = 3). The skinny kernel wins over the GEMM
+  // for N <= 8192 while the activations fit its LDS.
   const bool gemm = pmi::gemm_supported(K, group_size);
-  if (M <= 2 || (M <= 4 && (N < 8192 || !gemm))) return 1;
+  if (M <= 2 || (M <= 4 && ((N < 8192 && K <= 8192) || !gemm))) return 1;
   if (M >= 5 && N <= 8192 && pmi::skinny_supported(M, N, K, group_size)) return 3;
   // The register-streamed GEMM beats the MFMA GEMM by 3-8 % from M = 128 on
   // (Llama and Qwen shapes up to M = 512), and at 33-64 rows when its 128-row

@@ -3,7 +3,8 @@
 Mirrors pare/kernels/matmul_int4.py:183-248 (``matmul_w4a16``,
 ``triton_available``) with the Triton kernel replaced by hand-written HIP
 kernels for gfx950 behind libpare_amd.so:
-  - M <= 4: split-K GEMV (w4a16_gemv.hip), HBM-bandwidth bound;
+  - M <= 2, or M <= 4 with N < 8192 and K <= 8192: split-K GEMV
+    (w4a16_gemv.hip), HBM-bandwidth bound;
   - M <= 16 with the activations within 64 KiB of LDS and group size % 128 == 0:
     the skinny MFMA kernel (w4a16_skinny.hip);
   - otherwise: MFMA GEMM (w4a16_gemm.hip) for group sizes that are multiples

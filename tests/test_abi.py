@@ -56,7 +56,10 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128) == 2   # 64.1 KiB of padded activations
     assert L.pmi_matmul_kernel_choice(8, 4096, 18944, 128) == 2   # 296 KiB of activations
     assert L.pmi_matmul_kernel_choice(16, 4096, 4096, 128) == 2   # 128 KiB of activations
-    assert L.pmi_matmul_kernel_choice(4, 4096, 14336, 128) == 1   # GEMV
+    assert L.pmi_matmul_kernel_choice(4, 4096, 14336, 128) == 2   # long rows: MFMA GEMM
+    assert L.pmi_matmul_kernel_choice(3, 3584, 18944, 128) == 2
+    assert L.pmi_matmul_kernel_choice(4, 6144, 4096, 128) == 1    # GEMV
+    assert L.pmi_matmul_kernel_choice(3, 4096, 8192, 128) == 1
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 64) == 1     # group size not % 128
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1

@@ -220,9 +220,10 @@ def test_rmsnorm_gemv_matches_norm_then_matmul(M, N, K, with_residual):
 @pytest.mark.parametrize("M,N,F", [(1, 4096, 14336), (2, 4096, 14336), (3, 1024, 4096),
                                    (4, 4096, 14336), (1, 136, 512), (4, 200, 1024)])
 def test_glu_down_matches_silu_then_matmul(M, N, F):
-    """The gated GEMV against silu_mul followed by the plain matmul: the same
-    fp16 activations feed the same kernel, so the outputs are equal bit for bit."""
-    from pare_amd.kernels import matmul_w4a16, matmul_w4a16_glu
+    """The gated GEMV against silu_mul followed by the plain matmul on the GEMV:
+    the same fp16 activations feed the same kernel, so the outputs are equal bit
+    for bit. (Dispatch alone would send M = 4 at K = 14336 to the MFMA GEMM.)"""
+    from pare_amd.kernels import force_kernel, matmul_w4a16, matmul_w4a16_glu
     from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
 
     g = torch.Generator(device=DEV).manual_seed(M * N + F)
@@ -232,7 +233,8 @@ def test_glu_down_matches_silu_then_matmul(M, N, F):
     wk = repack_int4_for_kernel(packed, 128)
     zu = zeros_to_u8(z)
     got = matmul_w4a16_glu(gu, wk, s, zu, 128)
-    ref = matmul_w4a16(silu_mul(gu), wk, s, zu, 128)
+    with force_kernel("gemv"):
+        ref = matmul_w4a16(silu_mul(gu), wk, s, zu, 128)
     assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
 
 
