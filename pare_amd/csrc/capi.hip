@@ -346,12 +346,17 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   if (choice == 2)
     return from_hip(pmi::launch_gemm(x, w, scales, zeros, zu8, scales_gm, zeros_gm, perm, y, M, N,
                                      K, group_size, workspace, workspace_bytes, s), fn);
-  // GEMV, four activation rows per launch. With act_order and room in the
-  // workspace, X[:, perm] is gathered once and the GEMV reads it directly;
-  // otherwise every wave gathers its own activation columns.
+  // GEMV, four activation rows per launch. With act_order, every workgroup
+  // stages X in LDS and gathers X[:, perm] from there when the rows fit
+  // (64 KiB); otherwise X[:, perm] is gathered once into the workspace by a
+  // launch of its own, or, without room in the workspace, every lane gathers
+  // its columns from global memory.
   const uint16_t* xp = (const uint16_t*)x;
   uint16_t* yp = (uint16_t*)y;
-  if (perm && workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
+  pmi::GemvXform perm_xf;
+  perm_xf.mode = 4;
+  const bool perm_lds = perm && pmi::gemv_perm_lds_ok(M, N, K);
+  if (perm && !perm_lds && workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
     uint16_t* xg = (uint16_t*)((uint8_t*)workspace + pmi::kWsCounterBytes);
     hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
     if (e != hipSuccess) return from_hip(e, fn);
@@ -361,7 +366,7 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   for (int64_t m = 0; m < M; m += 4) {
     const int64_t mt = M - m < 4 ? M - m : 4;
     hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, perm, yp + m * N, mt, N, K,
-                                    group_size, s);
+                                    group_size, s, perm_lds ? &perm_xf : nullptr);
     if (e != hipSuccess) return from_hip(e, fn);
   }
   return ok();

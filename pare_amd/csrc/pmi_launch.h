@@ -83,10 +83,19 @@ inline bool gemm_supported(int64_t K, int64_t gs) { return gs % 128 == 0 && K % 
 GemmConfig gemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool has_perm);
 
-// Activation transforms of the GEMV (u8 zero points, no perm):
+// Activation transforms of the GEMV (modes 2 and 3: u8 zero points, no perm):
 //   mode 2: x is the fused gate/up output [M, 2K], consumed as silu(gate) * up;
 //   mode 3: x is the residual stream [M, K], consumed as RMSNorm(x + r) * w
-//           (r nullable; h = x + r written to h_out when r is given).
+//           (r nullable; h = x + r written to h_out when r is given);
+//   mode 4: act_order, x[:, perm] gathered from a copy of x staged in LDS by
+//           each workgroup (needs gemv_perm_lds_fits), instead of every lane
+//           gathering from global memory.
+constexpr int kGemvLdsChunks = 8;  // 16-byte activation chunks staged per thread (mode 4)
+inline bool gemv_perm_lds_fits(int64_t mt, int64_t K, int64_t threads) {
+  return K % 8 == 0 && mt * K * 2 <= 64 * 1024 && mt * K / 8 <= kGemvLdsChunks * threads;
+}
+// Mode 4 fits every launch of an M-row GEMV (launched four rows at a time).
+bool gemv_perm_lds_ok(int64_t M, int64_t N, int64_t K);
 struct GemvXform {
   int mode = 0;
   const void* r = nullptr;

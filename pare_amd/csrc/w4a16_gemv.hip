@@ -85,6 +85,18 @@ PMI_DEV void load_x_raw(const f16* __restrict__ xrow, const int32_t* __restrict_
   }
 }
 
+// act_order through LDS (XM 4): the permuted column indices of this lane's
+// chunk (k_lo..k_lo+15, k_hi..k_hi+15), clamped into [0, K); the activations
+// themselves are staged in LDS by the whole workgroup and gathered from there.
+PMI_DEV void load_perm(const int32_t* __restrict__ perm, int k_lo, int k_hi, int K, int (&pl)[16],
+                       int (&ph)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    pl[i] = perm_col(perm, k_lo + i, K);
+    ph[i] = perm_col(perm, k_hi + i, K);
+  }
+}
+
 // Reorders the raw pairs so xp[4i+c] lines up with nibble pair c of weight
 // word i: (x0,x2), (x1,x3) from the low half, the same from the high half.
 PMI_DEV void pair_x(const uint32_t (&a)[8], const uint32_t (&b)[8], uint32_t (&xp)[16]) {
@@ -331,7 +343,9 @@ PMI_DEV float sq_pairs(const uint32_t (&v)[8], float acc) {
   return acc;
 }
 
-// XM selects the activation source: 0 x [M, K]; 1 x[:, perm] (act_order);
+// XM selects the activation source: 0 x [M, K]; 1 x[:, perm] (act_order),
+// gathered by every lane from global memory; 4 the same, x staged in LDS once
+// per workgroup (16-byte loads) and gathered from there;
 // 2 the fused gate/up output [M, 2K], consumed as silu(gate) * up;
 // 3 RMSNorm(x + r) * w of the residual stream (xf.r nullable), with
 // h = x + r written to xf.h_out by workgroup 0.
@@ -373,6 +387,8 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   constexpr int kXS = XM >= 2 ? SPW : 1, kXM = XM >= 2 ? MT : 1, kNS = XM == 3 ? SPW : 1;
   uint32_t ua[kXS][kXM][8], ub[kXS][kXM][8];  // up (XM 2) or residual (XM 3)
   uint32_t wa[kNS][8], wb[kNS][8];            // norm weight (XM 3)
+  constexpr int kPS = XM == 4 ? SPW : 1;
+  int pl[kPS][16], ph[kPS][16];                // permuted columns (XM 4)
   int klo[SPW];
 #pragma unroll
   for (int sp = 0; sp < SPW; ++sp) {
@@ -400,9 +416,27 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         load_x_raw<false>(x + (int64_t)m * 2 * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
         load_x_raw<false>(x + (int64_t)m * 2 * K + K, perm, k_lo, k_lo + hgs, K, ua[sp][m],
                           ub[sp][m]);
+      } else if constexpr (XM == 4) {
+        if (m == 0) load_perm(perm, k_lo, k_lo + hgs, K, pl[sp], ph[sp]);
       } else {
         load_x_raw<XM == 1>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
       }
+    }
+  }
+  // XM 4: the MT activation rows ([MT, K], contiguous) in 16-byte chunks, at
+  // most kXCh per thread (the host checks MT * K / 8 <= kXCh * blockDim.x),
+  // loaded here and written to LDS after the first weight batch is issued.
+  constexpr int kXCh = XM == 4 ? kGemvLdsChunks : 1;
+  u32x4 xst[kXCh];
+  const int n_xch = MT * K / 8;
+  f16* lds_x = reinterpret_cast<f16*>(
+      reinterpret_cast<uint8_t*>(part) +
+      (((slice_waves > 1 ? rows_per_wg * slice_waves * MT * 4 : 0) + 15) & ~15));
+  if constexpr (XM == 4) {
+#pragma unroll
+    for (int i = 0; i < kXCh; ++i) {
+      const int c = (int)threadIdx.x + i * (int)blockDim.x;
+      xst[i] = c < n_xch ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
@@ -411,6 +445,32 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   uint32_t xp[SPW][MT][16];
   float sx[SPW][MT];
   // Pairs the activations with the nibble order and sums each lane's 32.
+  // XM 4: stage the activations in LDS, then gather this lane's columns
+  auto stage_x = [&]() {
+    if constexpr (XM == 4) {
+#pragma unroll
+      for (int i = 0; i < kXCh; ++i) {
+        const int c = (int)threadIdx.x + i * (int)blockDim.x;
+        if (c < n_xch) reinterpret_cast<u32x4*>(lds_x)[c] = xst[i];
+      }
+      // own LDS writes done (lgkmcnt(0)), then a bare s_barrier (no vmcnt
+      // wait: the weight batches stay in flight)
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      barrier_only();
+      const uint16_t* xs = reinterpret_cast<const uint16_t*>(lds_x);
+#pragma unroll
+      for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xa[sp][m][i] = (uint32_t)xs[m * K + pl[sp][2 * i]] |
+                           ((uint32_t)xs[m * K + pl[sp][2 * i + 1]] << 16);
+            xb[sp][m][i] = (uint32_t)xs[m * K + ph[sp][2 * i]] |
+                           ((uint32_t)xs[m * K + ph[sp][2 * i + 1]] << 16);
+          }
+    }
+  };
   auto setup_x = [&]() {
     if constexpr (XM == 3) {
       // h = x + r; the RMS of every activation row over all K columns: each
@@ -513,6 +573,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     Batch<U, SPW, ZU8> bt;
     load_batch<U, SPW, ZU8>(bt, rs, my_row0, row_last, row_bytes, G, boff, grp);
     __builtin_amdgcn_sched_barrier(0);
+    stage_x();
     setup_x();
     finish(bt, 0);
     for (int b = 1; b < n_batches; ++b) {
@@ -526,6 +587,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
       load_batch<U, SPW, ZU8>(ring[d], rs, my_row0 + d * stride, row_last, row_bytes, G, boff,
                               grp);
     __builtin_amdgcn_sched_barrier(0);
+    stage_x();
     setup_x();
     // Steady state, unrolled by D so every ring slot is a fixed register set.
     // Each step issues its load unconditionally (past the last batch it
@@ -558,7 +620,11 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
                       const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
                       int gs, const GemvXform& xf, hipStream_t stream) {
   const dim3 block(64 * c.slice_waves * c.row_waves);
-  const size_t lds = c.lds_bytes;
+  // XM 4 (xf.mode 4): the activation rows staged in LDS after the partials
+  const bool perm_lds = perm && xf.mode == 4;
+  if (perm_lds && !gemv_perm_lds_fits(MT, K, (int)block.x)) return hipErrorInvalidValue;
+  const size_t lds = perm_lds ? (((size_t)c.lds_bytes + 15) & ~(size_t)15) + (size_t)MT * K * 2
+                              : (size_t)c.lds_bytes;
 #define PMI_GEMV_LAUNCH(XM, Z)                                                                  \
   hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
                      (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,       \
@@ -568,6 +634,9 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
     if (!zero_u8 || perm) return hipErrorInvalidValue;
     if (xf.mode == 2) PMI_GEMV_LAUNCH(2, true);
     else PMI_GEMV_LAUNCH(3, true);
+  } else if (perm_lds) {
+    if (zero_u8) PMI_GEMV_LAUNCH(4, true);
+    else PMI_GEMV_LAUNCH(4, false);
   } else if (perm) {
     if (zero_u8) PMI_GEMV_LAUNCH(1, true);
     else PMI_GEMV_LAUNCH(1, false);
@@ -711,6 +780,16 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
   if (rows <= stride && lanes_x <= 4) c.depth = 1;  // one batch per wave: no ring
   c.lds_bytes = c.slice_waves > 1 ? (int)(rows * c.slice_waves * mt * 4) : 0;
   return c;
+}
+
+bool gemv_perm_lds_ok(int64_t M, int64_t N, int64_t K) {
+  const int64_t full = M < 4 ? M : 4, rem = M > 4 ? M % 4 : 0;
+  for (const int64_t mt : {full, rem}) {
+    if (mt == 0) continue;
+    const GemvConfig c = gemv_config(mt, N, K);
+    if (!gemv_perm_lds_fits(mt, K, 64 * c.slice_waves * c.row_waves)) return false;
+  }
+  return true;
 }
 
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,

@@ -442,10 +442,35 @@ def test_matmul_act_order(M, N, K, kernel):
     _check_out(y, ref, f"act_order M={M} N={N} K={K} kernel={name}")
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 3584, 3584), (2, 3584, 3584), (1, 3584, 18944),
+                                   (1, 512, 3584), (4, 4096, 8192)])
+def test_gemv_act_order_lds_gather_equals_pregathered(M, N, K):
+    """Where the activation rows fit 64 KiB of LDS, every GEMV workgroup stages X
+    there and gathers X[:, perm] from it. Against the same GEMV on X[:, perm]
+    gathered beforehand: same products, same order, identical bits."""
+    gs = 128
+    rng = np.random.default_rng(M + N + K)
+    w = _w(N, K, M + 7)
+    packed, s, z, g = O.rtn_quantize_act_order(w, rng.permutation(K), gs)
+    x = _x(M, K, 11).to(DEV)
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+    print(f"[case] act_order gemv lds M={M} N={N} K={K}", flush=True)
+    with force_kernel("gemv"):
+        y = P.matmul_w4a16(x, wk, _cuda(s), _cuda(z), gs, perm=pm)
+        y_pre = P.matmul_w4a16(x.index_select(1, pm.long()).contiguous(), wk, _cuda(s), _cuda(z), gs)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_pre.view(torch.int16))
+    ref = O.linear_fp32(x.float().cpu().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
+    _check_out(y, ref, f"act_order gemv lds M={M} N={N} K={K}")
+
+
 @pytest.mark.parametrize("M", [1, 3, 6])
 def test_gemv_act_order_gathered_equals_in_kernel_gather(M):
     """With a workspace the GEMV reads X[:, perm] gathered once; without one each
-    wave gathers its own columns. Same products, same order: identical bits."""
+    wave gathers its own columns (from LDS at M = 1, where the row fits 64 KiB;
+    from global memory at M = 3 and 6, where four rows do not). Same products,
+    same order: identical bits."""
     N, K, gs = 3584, 18944, 128
     rng = np.random.default_rng(M + 40)
     w = _w(N, K, M + 41)
