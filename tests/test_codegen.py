@@ -119,7 +119,8 @@ def gemv_asm(tmp_path_factory) -> str:
 def _gemv_kernels(asm: str) -> dict[tuple, str]:
     """Body of every w4a16_gemv_kernel<MT, U, D, SPW, XM, ZU8> instantiation,
     keyed by (MT, U, D, SPW, XM, ZU8, mangled name). XM: 0 plain activations,
-    1 act_order gather, 2 silu(gate) * up."""
+    1 act_order gather from global memory, 2 silu(gate) * up, 3 residual add +
+    RMSNorm, 4 act_order gather from activations staged in LDS."""
     out = {}
     pat = r"^(_ZN\S*w4a16_gemv_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d)ELb(\d)E\S*):"
     for m in re.finditer(pat, asm, re.M):
