@@ -220,10 +220,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--kernel-only", choices=["gate_up_m1", "gate_m64", "copy", "e2e_bs1"],
+    ap.add_argument("--kernel-only",
+                    choices=["gate_up_m1", "gate_m64", "copy", "e2e_bs1", "e2e_bs4"],
                     default=None,
-                    help="run only one kernel loop (for rocprofv3 counter passes); e2e_bs1: "
-                         "the end-to-end decoder at batch 1, 32 tokens")
+                    help="run only one kernel loop (for rocprofv3 counter passes); e2e_bs1 / "
+                         "e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens")
     ap.add_argument("--sweep", action="store_true", help="also run the gate_proj M sweep")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoder leg")
     args = ap.parse_args()
@@ -244,12 +245,13 @@ def main():
     L = _lib.lib()
     stream = torch.cuda.Stream(dev)
 
-    if args.kernel_only == "e2e_bs1":
+    if args.kernel_only in ("e2e_bs1", "e2e_bs4"):
         from pare_amd.decoder import DecoderConfig, QuantizedDecoder, decoder_throughput
 
+        batch = 1 if args.kernel_only == "e2e_bs1" else 4
         model = QuantizedDecoder(DecoderConfig(), dev, seed=0)
-        r = decoder_throughput(model, batch=1, prompt_len=512, n_generate=32)
-        log(f"e2e_bs1: {r['decode_ms_per_step']} ms/step decode")
+        r = decoder_throughput(model, batch=batch, prompt_len=512, n_generate=32)
+        log(f"{args.kernel_only}: {r['decode_ms_per_step']} ms/step decode")
         return
 
     if args.kernel_only == "copy":
