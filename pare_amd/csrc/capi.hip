@@ -250,6 +250,8 @@ size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
     return split + perm ? pmi::kWsCounterBytes + perm + split : 0;
   }
   // the GEMV reads act_order activations gathered once into the workspace
+  // where its rows do not fit LDS (the size is reported either way, so that a
+  // caller's workspace covers a forced or fallback launch)
   if ((choice == 1 || choice == 4) && has_perm)
     return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
   return 0;
