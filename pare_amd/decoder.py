@@ -342,19 +342,27 @@ class QuantizedDecoder(nn.Module):
                  torch.zeros(shape, dtype=torch.float16, device=self.embed.device))
                 for _ in range(cfg.layers)]
 
-    def forward_tokens(self, tokens, cos, sin, cache, pos, mask, causal: bool):
+    def forward_tokens(self, tokens, cos, sin, cache, pos, mask, causal: bool,
+                       last_only: bool = False):
         """Logits [B, T, vocab] of ``tokens`` [B, T] at cache positions ``pos``
-        (a prefill, ``causal``, writes positions 0..T-1)."""
+        (a prefill, ``causal``, writes positions 0..T-1). With ``last_only`` the
+        final norm and lm_head run on the last position only: [B, 1, vocab],
+        all a greedy prefill needs."""
         x = F.embedding(tokens, self.embed)
         if self.fused_ops:
             d = None
             for layer, (ck, cv) in zip(self.layers, cache):
                 x, d = layer.forward_fused(x, d, cos, sin, ck, cv, pos, causal)
+            if last_only:
+                x = x[:, -1:].contiguous()
+                d = d[:, -1:].contiguous() if d is not None else None
             n, _ = add_rmsnorm(x, d, self.norm.weight, self.cfg.rms_eps)
             return F.linear(n, self.lm_head)
         c, s = cos.index_select(0, pos), sin.index_select(0, pos)
         for layer, (ck, cv) in zip(self.layers, cache):
             x = layer(x, c, s, ck, cv, pos, mask, causal)
+        if last_only:
+            x = x[:, -1:]
         return F.linear(self.norm(x), self.lm_head)
 
     @torch.no_grad()
@@ -406,7 +414,7 @@ class QuantizedDecoder(nn.Module):
 
         t0 = time.perf_counter()
         logits = self.forward_tokens(prompt, cos, sin, cache, torch.arange(P, device=dev), None,
-                                     True)[:, -1]
+                                     True, last_only=True)[:, -1]
         tok.copy_(logits.argmax(-1, keepdim=True))
         out[:, 0] = tok[:, 0]
         torch.cuda.synchronize(dev)

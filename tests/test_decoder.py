@@ -42,6 +42,24 @@ def test_graph_decode_matches_eager(model):
 
 
 @pytest.mark.parametrize("batch,seq", [(1, 16), (3, 40)])
+def test_prefill_last_only_logits(model, batch, seq):
+    """A greedy prefill's logits of the last position only (final norm and
+    lm_head on that row) against the last row of the full prefill."""
+    g = torch.Generator(device=DEV).manual_seed(seq + 1)
+    toks = torch.randint(0, SMALL.vocab, (batch, seq), generator=g, device=DEV)
+    cos, sin = model.rope_tables(seq)
+    pos = torch.arange(seq, device=DEV)
+    with torch.no_grad():
+        full = model.forward_tokens(toks, cos, sin, model.new_cache(batch, seq), pos, None, True)
+        last = model.forward_tokens(toks, cos, sin, model.new_cache(batch, seq), pos, None, True,
+                                    last_only=True)
+    assert last.shape == (batch, 1, SMALL.vocab)
+    err = (last[:, 0].float() - full[:, -1].float()).abs().max().item()
+    assert err <= 2e-3 * full[:, -1].float().abs().max().item() + 1e-3, err
+    assert torch.equal(last[:, 0].argmax(-1), full[:, -1].argmax(-1))
+
+
+@pytest.mark.parametrize("batch,seq", [(1, 16), (3, 40)])
 def test_prefill_logits_match_dequant_path(model, batch, seq):
     """Kernel path vs the reference's dequant path (fp16 F.linear on
     dequantize()), same model and inputs: logits within tolerance."""
