@@ -295,8 +295,10 @@ PMI_API int pmi_rope_kv_f16(const void* qkv, const float* cos, const float* sin,
  * zero). With it the positions are split over workgroups of 64 positions
  * each, combined by the last workgroup of each (b, KV head) in split order;
  * without it (or when smaller) one workgroup per (b, KV head) runs, for
- * L up to about 3000. Calls that may run concurrently must not share a
- * workspace. */
+ * L up to about 3000. The workspace starts with a fixed 16 KiB block of
+ * counters (one per (b, KV head), so the split needs B * KV <= 4096) that no
+ * shape's partials overlap: one workspace may serve calls of any shapes in
+ * turn. Calls that may run concurrently must not share a workspace. */
 PMI_API int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cache_v,
                                      const int64_t* pos, void* out, int64_t B, int64_t H,
                                      int64_t KV, int64_t D, int64_t L, float scale,
@@ -315,8 +317,8 @@ PMI_API int pmi_decode_attention_rope_f16(const void* qkv, const float* cos, con
                                           int64_t L, float scale, void* workspace,
                                           size_t workspace_bytes, void* stream);
 
-/* Workspace bytes of the split pmi_decode_attention_f16 (0 for bad shapes).
- * Host-only. */
+/* Workspace bytes of the split pmi_decode_attention_f16 (0 for bad shapes and
+ * for B * KV > 4096, where the split is unavailable). Host-only. */
 PMI_API size_t pmi_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_t KV, int64_t L);
 
 /* Greedy decoding's argmax: out[r * out_stride] (int64) = index of the largest
@@ -324,7 +326,9 @@ PMI_API size_t pmi_decode_attention_workspace_bytes(int64_t B, int64_t H, int64_
  * on ties, NaN counted as largest (torch.argmax's rule). workspace: device
  * scratch of pmi_argmax_workspace_bytes(rows, n) bytes, 256-byte aligned and
  * zero-filled before its first use; each call leaves it zero-filled again.
- * Calls that may run concurrently must not share it. */
+ * It starts with the same fixed 16 KiB counter block (one per row, rows <=
+ * 4096), so one workspace may serve calls of any shapes in turn. Calls that
+ * may run concurrently must not share it. */
 PMI_API int pmi_argmax_f16(const void* x, int64_t rows, int64_t n, int64_t* out,
                            int64_t out_stride, void* workspace, size_t workspace_bytes,
                            void* stream);

@@ -36,6 +36,7 @@ from . import _lib
 from .config import QuantConfig, kernel_group_size
 from .kernels import _DeviceGuard, _stream_handle, _to_2d
 from .linear import QuantizedLinear
+from .model_io import replace_module
 
 AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)   # pare/model/export_awq.py:37-39
 CONFIG_FILE = "config.json"
@@ -142,8 +143,9 @@ def to_awq_linear(ql: QuantizedLinear, group_size: int | None = None) -> AwqGemm
     gs = group_size or kernel_group_size(ql.config, ql.in_features)
     out_f, in_f = ql.out_features, ql.in_features
     if in_f % gs != 0 or out_f % 8 != 0:
-        raise ValueError(f"AWQ export needs in_features ({in_f}) divisible by group_size ({gs}) "
-                         f"and out_features ({out_f}) divisible by 8.")
+        raise ValueError(f"AWQ-GEMM packs eight output columns per int32 word and whole groups "
+                         f"per row: out_features={out_f} must be a multiple of 8 and "
+                         f"in_features={in_f} a multiple of group_size={gs}")
     if ql.g_idx is not None:
         raise ValueError("AWQ-GEMM has no g_idx: act_order layers cannot be exported")
     home = ql.packed_weight.device
@@ -155,14 +157,6 @@ def to_awq_linear(ql: QuantizedLinear, group_size: int | None = None) -> AwqGemm
     if ql.bias is not None:
         m.bias = ql.bias.data.half().to(home)
     return m
-
-
-def _set_submodule(model: nn.Module, dotted: str, new: nn.Module) -> None:
-    parent = model
-    parts = dotted.split(".")
-    for p in parts[:-1]:
-        parent = getattr(parent, p)
-    setattr(parent, parts[-1], new)
 
 
 def awq_quantization_config(group_size: int) -> dict:
@@ -181,13 +175,13 @@ def export_awq(model: nn.Module, save_dir, tokenizer=None) -> str:
     ``config.json`` that holds ``quantization_config``."""
     qls = [(n, m) for n, m in model.named_modules() if isinstance(m, QuantizedLinear)]
     if not qls:
-        raise ValueError("No QuantizedLinear layers found. Quantize with a 4-bit scheme first.")
+        raise ValueError("export_awq: the model holds no INT4 QuantizedLinear layer to export")
     sizes = {kernel_group_size(m.config, m.in_features) for _, m in qls}
     if len(sizes) != 1:
         raise ValueError(f"AWQ checkpoints have one group size; the layers use {sorted(sizes)}")
     gs = sizes.pop()
     for name, m in qls:
-        _set_submodule(model, name, to_awq_linear(m, gs))
+        replace_module(model, name, to_awq_linear(m, gs))
     qcfg = awq_quantization_config(gs)
     save_dir = str(save_dir)
     if hasattr(model, "save_pretrained") and hasattr(model, "config"):
@@ -271,7 +265,7 @@ def load_awq(model: nn.Module, path, use_kernel: bool = True, device="cuda") -> 
         pre = name + "."
         ql = from_awq_tensors(tensors[pre + "qweight"], tensors[pre + "qzeros"],
                               tensors[pre + "scales"], tensors.get(pre + "bias"), gs, use_kernel)
-        _set_submodule(model, name, ql)
+        replace_module(model, name, ql)
     prefixes = tuple(n + "." for n in layers)
     rest = {k: v for k, v in tensors.items() if not k.startswith(prefixes)}
     model.load_state_dict(rest, strict=False)

@@ -10,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -49,18 +50,39 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; cannot build libpare_amd.so")
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
-    """Compiles every HIP source into ``pare_amd/libpare_amd.so`` (always rebuilds)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [_hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{REPO_DIR / 'include'}",
-           *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+def _run(cmd: list[str], verbose: bool) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
-    if verbose and res.stderr.strip():
-        print(res.stderr, file=sys.stderr)
+    return res.stderr
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
+    """Compiles every HIP source into ``pare_amd/libpare_amd.so`` (always rebuilds).
+
+    Each source is compiled to an object of its own in parallel (``_build/``
+    at the repository root, ignored by git), then the objects are linked."""
+    hipcc = _hipcc()
+    obj_dir = REPO_DIR / "_build"
+    obj_dir.mkdir(exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"] + list(extra_flags or [])
+    inc = f"-I{REPO_DIR / 'include'}"
+    jobs = []
+    for src in SOURCES:
+        obj = obj_dir / (Path(src).stem + ".o")
+        jobs.append((obj, [hipcc, *flags, inc, "-c", str(CSRC / src), "-o", str(obj)]))
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "0") or 0) or os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        logs = list(pool.map(lambda j: _run(j[1], verbose), jobs))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    logs.append(_run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC",
+                      *[str(o) for o, _ in jobs], "-o", str(tmp)], verbose))
+    if verbose:
+        for log in logs:
+            if log.strip():
+                print(log, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -39,26 +39,31 @@ class QuantDtype(Enum):
     def is_float(self) -> bool:
         return self.value.is_float
 
+    def _code_range(self) -> tuple[int, int]:
+        if self.value.is_float:
+            raise TypeError(f"{self.name} is a floating-point format: it has no integer code range")
+        n = self.bits
+        return (-(1 << (n - 1)), (1 << (n - 1)) - 1) if self.value.signed else (0, (1 << n) - 1)
+
     @property
     def qmin(self) -> int:
-        if self.value.is_float:
-            raise TypeError("float dtypes have no integer qmin/qmax")
-        return -(2 ** (self.bits - 1)) if self.value.signed else 0
+        return self._code_range()[0]
 
     @property
     def qmax(self) -> int:
-        if self.value.is_float:
-            raise TypeError("float dtypes have no integer qmin/qmax")
-        return (2 ** (self.bits - 1) - 1) if self.value.signed else 2 ** self.bits - 1
+        return self._code_range()[1]
 
     @classmethod
     def from_bits(cls, bits: int, *, signed: bool = False) -> "QuantDtype":
-        mapping = {(2, False): cls.INT2, (3, False): cls.INT3, (4, False): cls.INT4,
-                   (8, True): cls.INT8}
-        key = (bits, signed or bits == 8)
-        if key not in mapping:
-            raise ValueError(f"No standard dtype for bits={bits}, signed={signed}")
-        return mapping[key]
+        """The integer format of `bits` bits: INT8 (signed) for 8 whatever
+        `signed` says; the 2-, 3- and 4-bit formats exist unsigned only."""
+        if bits == 8:
+            return cls.INT8
+        if not signed:
+            for member in (cls.INT2, cls.INT3, cls.INT4):
+                if member.bits == bits:
+                    return member
+        raise ValueError(f"QuantDtype.from_bits: no integer format with bits={bits}, signed={signed}")
 
 
 @dataclass
@@ -72,15 +77,18 @@ class QuantConfig:
     damp_percent: float = 0.01
     act_order: bool = False
 
+    _SCHEMES = ("rtn", "gptq", "awq", "smoothquant")
+    _GRANULARITIES = ("per_tensor", "per_channel", "per_group")
+
     def __post_init__(self) -> None:
+        checks = (("scheme", self.scheme, self._SCHEMES),
+                  ("granularity", self.granularity, self._GRANULARITIES),
+                  ("bits", self.bits, (2, 3, 4, 8)))
+        for field, value, allowed in checks:
+            if value not in allowed:
+                raise ValueError(f"QuantConfig.{field}={value!r} is not one of {allowed}")
         if self.dtype is None:
             self.dtype = QuantDtype.from_bits(self.bits)
-        if self.scheme not in {"rtn", "gptq", "awq", "smoothquant"}:
-            raise ValueError(f"Unknown scheme: {self.scheme!r}")
-        if self.granularity not in {"per_tensor", "per_channel", "per_group"}:
-            raise ValueError(f"Unknown granularity: {self.granularity!r}")
-        if self.bits not in {2, 3, 4, 8}:
-            raise ValueError(f"Unsupported bits: {self.bits}")
 
     @property
     def effective_dtype(self) -> QuantDtype:

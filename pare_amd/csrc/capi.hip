@@ -506,10 +506,11 @@ int pmi_decode_attention_f16(const void* q, const void* cache_k, const void* cac
   if (D != 128 || H / KV > 4)
     return fail(PMI_ERR_UNSUPPORTED, "%s: needs head_dim 128 and at most 4 query heads per KV head",
                 fn);
-  const bool split = workspace && workspace_bytes >= pmi::decode_attention_ws_bytes(B, H, KV, L);
+  const size_t need = pmi::decode_attention_ws_bytes(B, H, KV, L);  // 0: B * KV too large
+  const bool split = workspace && need && workspace_bytes >= need;
   if (split && !aligned(workspace, 256))
     return fail(PMI_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
-  if (split && pmi::decode_attention_ws_bytes(B, H, KV, L) >= (1ull << 31))
+  if (split && need >= (1ull << 31))
     return fail(PMI_ERR_UNSUPPORTED, "%s: workspace partials exceed 2 GiB", fn);
   const int64_t group = H / KV, span = (L + 3) / 4;
   if (!split && (group * 4 * span + group * 4 * (2 + D)) * 4 > 64 * 1024)
@@ -538,6 +539,9 @@ int pmi_decode_attention_rope_f16(const void* qkv, const float* cos, const float
     return fail(PMI_ERR_UNSUPPORTED, "%s: needs head_dim 128 and at most 4 query heads per KV head",
                 fn);
   const size_t need = pmi::decode_attention_ws_bytes(B, H, KV, L);
+  if (!need)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: B * KV = %lld exceeds the %lld split counters", fn,
+                (long long)(B * KV), (long long)pmi::kOpsMaxCounters);
   if (!workspace || workspace_bytes < need)
     return fail(PMI_ERR_INVALID, "%s: needs a workspace of pmi_decode_attention_workspace_bytes "
                 "(%zu) bytes", fn, need);
@@ -568,7 +572,8 @@ int pmi_argmax_f16(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t
     return fail(PMI_ERR_INVALID, "%s: need rows >= 0, 0 < n < 2^31 with n %% 8 == 0, out_stride >= 1",
                 fn);
   if (rows == 0) return ok();
-  if (rows > 65535) return fail(PMI_ERR_UNSUPPORTED, "%s: at most 65535 rows", fn);
+  if (rows > pmi::kOpsMaxCounters)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: at most %lld rows", fn, (long long)pmi::kOpsMaxCounters);
   const size_t need = pmi::argmax_ws_bytes(rows, n);
   if (!workspace || workspace_bytes < need)
     return fail(PMI_ERR_INVALID, "%s: needs a zero-filled workspace of pmi_argmax_workspace_bytes "

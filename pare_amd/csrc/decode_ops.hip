@@ -565,8 +565,9 @@ hipError_t launch_rope_kv(const void* qkv, const float* cos_t, const float* sin_
 }
 
 size_t decode_attention_ws_bytes(int64_t B, int64_t H, int64_t KV, int64_t L) {
+  if (B * KV > kOpsMaxCounters) return 0;
   const int64_t S = (L + kSplitPos - 1) / kSplitPos;
-  return decode_attention_counter_bytes(B, KV) + (size_t)(B * H * S * kPartFloats * 4);
+  return kOpsCounterBytes + (size_t)(B * H * S * kPartFloats * 4);
 }
 
 hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
@@ -576,10 +577,11 @@ hipError_t launch_decode_attention(const void* q, const void* cache_k, const voi
                                    const float* sin_t) {
   const int group = (int)(H / KV);
   const bool rope = cos_t != nullptr;
-  if (workspace && ws_bytes >= decode_attention_ws_bytes(B, H, KV, L)) {
+  const size_t need = decode_attention_ws_bytes(B, H, KV, L);
+  if (workspace && need && ws_bytes >= need) {
     const int S = (int)((L + kSplitPos - 1) / kSplitPos);
     int* counters = (int*)workspace;
-    float* part = (float*)((char*)workspace + decode_attention_counter_bytes(B, KV));
+    float* part = (float*)((char*)workspace + kOpsCounterBytes);
     const dim3 grid((unsigned)S, (unsigned)(B * KV)), block(64 * group);
     if (rope)
       hipLaunchKernelGGL(decode_attention_split_kernel<true>, grid, block, 0, stream, (const f16*)q,
@@ -602,15 +604,16 @@ hipError_t launch_decode_attention(const void* q, const void* cache_k, const voi
 }
 
 size_t argmax_ws_bytes(int64_t rows, int64_t n) {
+  if (rows > kOpsMaxCounters) return 0;
   const int64_t chunks = (n + kArgChunk - 1) / kArgChunk;
-  return decode_attention_counter_bytes(rows, 1) + (size_t)(rows * chunks * 8);
+  return kOpsCounterBytes + (size_t)(rows * chunks * 8);
 }
 
 hipError_t launch_argmax(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t out_stride,
                          void* workspace, hipStream_t stream) {
   const int chunks = (int)((n + kArgChunk - 1) / kArgChunk);
   int* counters = (int*)workspace;
-  float* part = (float*)((char*)workspace + decode_attention_counter_bytes(rows, 1));
+  float* part = (float*)((char*)workspace + kOpsCounterBytes);
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)chunks, (unsigned)rows), dim3(256), 0, stream,
                      (const f16*)x, (int)n, chunks, out, out_stride, counters, part);
   return hipGetLastError();

@@ -130,11 +130,14 @@ hipError_t launch_rope_kv(const void* qkv, const float* cos_t, const float* sin_
                           const int64_t* pos, void* q_out, void* cache_k, void* cache_v,
                           int64_t B, int64_t T, int64_t H, int64_t KV, int64_t D, int64_t L,
                           hipStream_t stream);
-// Split attention workspace: int32 counters [B * KV] (zero between calls,
-// padded to 256 bytes), then the per-split partials.
-inline size_t decode_attention_counter_bytes(int64_t B, int64_t KV) {
-  return ((size_t)(B * KV) * 4 + 255) & ~(size_t)255;
-}
+// Workspaces of the split attention and the argmax start with a fixed block of
+// int32 counters (zero between calls) that no shape's partials ever overlap:
+// a workspace shared by calls of different shapes keeps every counter of
+// every shape at zero. Counter i serves (sequence, KV head) i, or row i.
+constexpr size_t kOpsCounterBytes = 16 * 1024;
+constexpr int64_t kOpsMaxCounters = kOpsCounterBytes / 4;
+// Split attention workspace: the counter block, then the per-split partials.
+// 0 when B * KV exceeds the counter block (the split kernel is then unavailable).
 size_t decode_attention_ws_bytes(int64_t B, int64_t H, int64_t KV, int64_t L);
 // workspace (nullable): too small or null runs the one-workgroup-per-KV-head kernel.
 hipError_t launch_decode_attention(const void* q, const void* cache_k, const void* cache_v,
@@ -142,8 +145,8 @@ hipError_t launch_decode_attention(const void* q, const void* cache_k, const voi
                                    int64_t KV, int64_t L, float scale, void* workspace,
                                    size_t ws_bytes, hipStream_t stream,
                                    const float* cos_t = nullptr, const float* sin_t = nullptr);
-// Greedy argmax over fp16 rows; workspace: int32 counters [rows] (zero
-// between calls, 256-byte padded), then (value, index) per (row, chunk).
+// Greedy argmax over fp16 rows; workspace: the counter block, then (value,
+// index) per (row, chunk). 0 when rows exceed the counter block.
 size_t argmax_ws_bytes(int64_t rows, int64_t n);
 hipError_t launch_argmax(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t out_stride,
                          void* workspace, hipStream_t stream);

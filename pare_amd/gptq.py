@@ -46,32 +46,39 @@ BLOCK = 128   # pare/schemes/gptq.py:42
 
 
 class HessianAccumulator:
-    """Running H = 2/n · Σ XᵀX over token rows (pare/calibration/hessian.py:19-73),
-    accumulated in fp32 with one GEMM per batch on the activations' device."""
+    """GPTQ's per-layer input statistic H = (2/n) XᵀX, gathered batch by batch
+    without keeping the batches (the role of pare/calibration/hessian.py:19-73,
+    with the same ``H`` / ``n_tokens`` attributes and ``accumulate`` /
+    ``finalize`` / ``reset`` calls).
+
+    ``H`` is the un-normalised Gram sum in fp32 on the device of the first
+    batch: the first batch's Gram matrix becomes it, later ones are added to
+    it. Token rows are the input flattened over its leading dims; a batch is
+    [tokens, features] or [batch, seq, features].
+    """
 
     def __init__(self) -> None:
+        self.reset()
+
+    def reset(self) -> None:
         self.H: torch.Tensor | None = None
         self.n_tokens = 0
 
     def accumulate(self, x: torch.Tensor) -> None:
-        x = x.detach().float()
-        if x.dim() == 3:
-            x = x.reshape(-1, x.shape[-1])
-        elif x.dim() != 2:
-            raise ValueError(f"Expected 2-D or 3-D activation, got shape {tuple(x.shape)}")
-        if self.H is None:
-            self.H = torch.zeros(x.shape[1], x.shape[1], device=x.device, dtype=torch.float32)
-        self.H.addmm_(x.T, x)
-        self.n_tokens += x.shape[0]
+        if x.dim() not in (2, 3):
+            raise ValueError("HessianAccumulator.accumulate takes [tokens, features] or "
+                             f"[batch, seq, features] activations, not shape {tuple(x.shape)}")
+        rows = x.detach().reshape(-1, x.shape[-1]).to(torch.float32)
+        gram = rows.mT @ rows
+        self.H = gram if self.H is None else self.H.add_(gram)
+        self.n_tokens += rows.shape[0]
 
     def finalize(self) -> torch.Tensor:
-        if self.H is None or self.n_tokens == 0:
-            raise RuntimeError("HessianAccumulator has no samples — did you forget to call accumulate()?")
-        return self.H * (2.0 / self.n_tokens)
-
-    def reset(self) -> None:
-        self.H = None
-        self.n_tokens = 0
+        """(2 / n_tokens) · H as a new tensor; RuntimeError before any batch."""
+        if not self.n_tokens:
+            raise RuntimeError("HessianAccumulator.finalize: no samples accumulated yet "
+                               "(call accumulate with calibration activations first)")
+        return self.H.mul(2.0 / self.n_tokens)
 
 
 def _cholesky_chain(H: torch.Tensor, damp: float) -> torch.Tensor:

@@ -6,8 +6,11 @@ buffers ``<layer>.packed_weight`` / ``.scale`` / ``.zero`` / ``.bias`` and all
 non-quantized parameters) and ``pare_config.json`` (``{"pare_version": ..,
 "quantized_layers": {name: {bits, scheme, granularity, group_size, sym,
 smooth_alpha, in_features, out_features, quantize_inputs, has_bias}}}``).
-Directories written by the reference load here and the reverse holds for INT4
-layers.
+Directories written by the reference load here. The reverse holds for INT4
+layers without g_idx only: the reference's loader ignores ``<layer>.g_idx``
+and dequantizes act_order layers with contiguous groups, which gives wrong
+weights without an error, so ``save_quantized`` warns when it writes such a
+layer.
 
 Differences from the reference, all additive:
   - ``load_quantized`` sets ``use_kernel`` on every loaded layer (the
@@ -26,6 +29,7 @@ Only safetensors and JSON are read: nothing in a checkpoint is executed.
 from __future__ import annotations
 
 import json
+import warnings
 from pathlib import Path
 
 import torch
@@ -68,8 +72,14 @@ def save_quantized(model: nn.Module, path, kernel_layout: bool = False) -> None:
             if kernel_layout:
                 w_k = m._kernel_buffers()[0]
                 extra[name + ".packed_weight_kernel"] = w_k
+    act_order = [n for n, meta in layers.items() if meta["has_g_idx"]]
+    if act_order:
+        warnings.warn(f"save_quantized: {len(act_order)} act_order layer(s) (first: {act_order[0]}) "
+                      "carry g_idx; the reference's load_quantized ignores it and would "
+                      "dequantize them with contiguous groups", stacklevel=2)
     if not layers:
-        raise ValueError("No QuantizedLinear layers found in model. Quantize the model first.")
+        raise ValueError("save_quantized: the model holds no QuantizedLinear layer to save "
+                         "(quantize it before saving)")
     # one copy per storage (tied weights, pare/model/io.py:92-107)
     seen: set[int] = set()
     tensors: dict[str, torch.Tensor] = {}
@@ -86,11 +96,10 @@ def save_quantized(model: nn.Module, path, kernel_layout: bool = False) -> None:
     (path / PARE_CONFIG_FILE).write_text(json.dumps(meta, indent=2))
 
 
-def _set_submodule(parent: nn.Module, dotted: str, new: nn.Module) -> None:
-    parts = dotted.split(".")
-    for p in parts[:-1]:
-        parent = getattr(parent, p)
-    setattr(parent, parts[-1], new)
+def replace_module(root: nn.Module, dotted: str, new: nn.Module) -> None:
+    """Puts `new` in place of the submodule at dotted path `dotted` of `root`."""
+    parent_name, _, leaf = dotted.rpartition(".")
+    setattr(root.get_submodule(parent_name), leaf, new)
 
 
 def load_quantized(model: nn.Module, path, use_kernel: bool = True, device=None) -> nn.Module:
@@ -120,7 +129,7 @@ def load_quantized(model: nn.Module, path, use_kernel: bool = True, device=None)
         w_k = tensors.get(pre + "packed_weight_kernel")
         if stored_layout and w_k is not None and ql.packed_weight.is_cuda:
             ql.adopt_kernel_layout(w_k)
-        _set_submodule(model, name, ql)
+        replace_module(model, name, ql)
     prefixes = tuple(n + "." for n in layers)
     rest = {k: v for k, v in tensors.items() if not k.startswith(prefixes)}
     model.load_state_dict(rest, strict=False)

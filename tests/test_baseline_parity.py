@@ -1,0 +1,372 @@
+"""Parity of every BASELINE workload at the size and in the configuration that
+bench.py runs it, against the CPU oracle.
+
+The layers are built by bench.py's own builders (device RTN, kernel-layout
+repack, u8 zero points, group-major scale/zero copies, fused q/k/v and gate/up
+buffers, act_order permutations) and launched through bench.py's own
+``launch`` (the C ABI, with the bench's shared workspace), so what is checked
+here is exactly what is timed. Each layer's buffers are first checked
+byte-for-byte against the oracle's quantisation of the same seeded weights;
+outputs are then checked against the oracle's fp32-accumulated reference
+(``O.linear_fp32`` on ``O.dequantize_packed`` / ``O.dequantize_gidx``) at
+rtol = atol = 1e-2, and at M = 1 also against the reference's own fp16
+dequantize-on-the-fly forward (pare/layers/linear.py:101-138, restated in
+``O.dequant_path_forward_torch``). Max-abs errors are printed per case.
+
+Configs: C1 single 4096x4096 layer with the stated seeds; C2
+the Llama-3.1-8B decode set at M = 1 (seven linears and the two fused
+launches); C3 gate_proj at M in {1, 2, 4, 8, 16, 32, 64, 128}; C4 the
+Qwen2.5-7B act_order layers at M in {1, 16}; C5 the 32-layer decoder; plus the
+reference harness's M = 512 and 2048 (pare benchmarks/bench_triton_kernel.py:
+67-97) on the Llama shapes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+import pare_amd as P
+from oracle import pare_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+RTOL = ATOL = 1e-2
+GS = 128
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _bench_workspace():
+    """bench.py's shared launch workspace, sized as main() sizes it."""
+    L = P._lib.lib()
+    shapes = [(N, K) for _, N, K in bench.LLAMA] + [(6144, 4096), (28672, 4096)]
+    ws = max(L.pmi_matmul_workspace_bytes(M, N, K, GS, p)
+             for M in (1, 2, 4, 8, 16, 32, 64, 128, 512, 2048) for N, K in shapes for p in (0, 1))
+    ws = max(ws, max(L.pmi_matmul_workspace_bytes(M, N, K, GS, 1)
+                     for M in (1, 16) for _, N, K in bench.QWEN))
+    bench.WORKSPACE[:] = [torch.zeros(max(ws, 1 << 20), dtype=torch.uint8, device=DEV)]
+    yield
+    bench.WORKSPACE.clear()
+    torch.cuda.empty_cache()
+
+
+def _ref_fp32(x: torch.Tensor, w_hat: np.ndarray) -> np.ndarray:
+    """fp32-accumulated x @ W16^T (the weights rounded to fp16 first, as the
+    reference's dequant path does); torch's CPU GEMM for the large shapes."""
+    w16 = torch.from_numpy(np.ascontiguousarray(w_hat, dtype=np.float32)).half().float()
+    return (x.float().cpu() @ w16.T).numpy()
+
+
+def _check(y: torch.Tensor, ref: np.ndarray, what: str) -> float:
+    got = y.float().cpu().numpy()
+    err = np.abs(got - ref)
+    print(f"[baseline] {what}: max_abs={err.max():.3e} max|ref|={np.abs(ref).max():.3e}", flush=True)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert (err <= ATOL + RTOL * np.abs(ref)).all(), f"{what}: max_abs={err.max():.4e}"
+    return float(err.max())
+
+
+def _oracle_decoder_layer(seed: int):
+    """The oracle's quantisation of bench.make_decoder_layer(seed)'s weights
+    (regenerated from the same device generator seeds): name -> (packed storage
+    layout, scale [N,G,1], zero [N,G,1])."""
+    out = {}
+    for i, (name, N, K) in enumerate(bench.LLAMA):
+        g = torch.Generator(device=DEV).manual_seed(seed + i)
+        w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).cpu().numpy()
+        out[name] = O.rtn_quantize(w, GS)
+    return out
+
+
+def _assert_buf_matches(buf, packed, s, z):
+    """Bench buffers == the oracle's bytes: kernel-layout codes, fp32 scale
+    bits, u8 zero points."""
+    N = packed.shape[0]
+    assert (buf.w.cpu().numpy() == O.repack_int4_for_kernel(packed, GS)).all(), buf.name
+    assert (buf.s.cpu().numpy().view(np.uint32) == s.reshape(N, -1).view(np.uint32)).all(), buf.name
+    assert (buf.z.cpu().numpy() == z.reshape(N, -1).astype(np.uint8)).all(), buf.name
+
+
+def _launch(buf, x: torch.Tensor) -> torch.Tensor:
+    M = x.shape[0]
+    y = torch.empty(M, buf.N, dtype=torch.float16, device=DEV)
+    bench.launch(P._lib.lib(), buf, x.to(DEV).contiguous(), y, M,
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.fixture(scope="module")
+def llama_layer():
+    """bench.py's decoder layer 0 (seed 0) with its group-major copies built,
+    and the oracle's buffers and dequantized weights for it."""
+    fused, single = bench.make_decoder_layer(0, DEV)
+    for b in fused + single:
+        b.gm()
+    ref = _oracle_decoder_layer(0)
+    w_hat = {name: O.dequantize_packed(*ref[name]) for name in ref}
+    torch.cuda.synchronize()
+    return {b.name: b for b in fused + single}, ref, w_hat
+
+
+# ---------------------------------------------------------------------------
+# C1: single 4096x4096 layer, stated seeds, through the module
+# ---------------------------------------------------------------------------
+
+def test_c1_single_layer_stated_seeds():
+    """W = (randn(4096, 4096, seed 0) * 0.02).half(), RTN INT4 asym g128 on
+    W.float(); x = randn(1, 4096, seed 1).half()."""
+    W = (torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)) * 0.02).half()
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1)).half()
+    packed, s, z = O.rtn_quantize(W.float().numpy(), GS)
+    lin = torch.nn.Linear(4096, 4096, bias=False)
+    lin.weight.data = W.float()
+    ql = P.QuantizedLinear.from_linear(lin.to(DEV), P.QuantConfig(bits=4, group_size=GS))
+    ql.use_kernel = True
+    assert (ql.packed_weight.cpu().numpy() == packed).all()
+    assert (ql.scale.cpu().numpy().view(np.uint32) == s.view(np.uint32)).all()
+    assert (ql.zero.cpu().numpy() == z).all()
+    w_hat = O.dequantize_packed(packed, s, z)
+    dq = ql.dequantize(torch.float16).cpu().numpy()
+    assert (dq.view(np.uint16) == w_hat.astype(np.float16).view(np.uint16)).all()
+    y = ql(x.to(DEV))
+    _check(y, _ref_fp32(x, w_hat), "C1 4096x4096 M=1 vs fp32")
+    ref16 = O.dequant_path_forward_torch(x, torch.from_numpy(packed), torch.from_numpy(s),
+                                         torch.from_numpy(z)).float().numpy()
+    _check(y, ref16, "C1 4096x4096 M=1 vs reference fp16 dequant path")
+
+
+# ---------------------------------------------------------------------------
+# C2: the Llama-3.1-8B decode set at M = 1, as the bench launches it
+# ---------------------------------------------------------------------------
+
+_FUSED_PARTS = dict(bench.FUSED)
+
+
+@pytest.mark.parametrize("name", [n for n, _, _ in bench.LLAMA] + ["qkv", "gate_up"])
+def test_c2_decode_layer_m1(llama_layer, name):
+    bufs, ref, w_hat = llama_layer
+    parts = _FUSED_PARTS.get(name, (name,))
+    for p in parts:
+        _assert_buf_matches(bufs[p], *ref[p])
+    buf = bufs[name]
+    wh = np.concatenate([w_hat[p] for p in parts])
+    x = torch.randn(1, buf.K, generator=torch.Generator().manual_seed(17 + buf.N)).half()
+    y = _launch(buf, x)
+    _check(y, _ref_fp32(x, wh), f"C2 {name} {buf.N}x{buf.K} M=1 u8 ({P.kernel_choice(1, buf.N, buf.K, GS)})")
+    packed = np.concatenate([ref[p][0] for p in parts])
+    s = np.concatenate([ref[p][1] for p in parts])
+    z = np.concatenate([ref[p][2] for p in parts])
+    ref16 = O.dequant_path_forward_torch(x, torch.from_numpy(packed), torch.from_numpy(s),
+                                         torch.from_numpy(z)).float().numpy()
+    _check(y, ref16, f"C2 {name} M=1 vs reference fp16 dequant path")
+
+
+def test_c2_modules_fused_and_single_m1():
+    """The same decode set through QuantizedLinear / FusedQuantizedLinear (the
+    decoder's configuration: u8 zeros and group-major copies built by the
+    module) at M = 1."""
+    ref = _oracle_decoder_layer(300)
+    qcfg = P.QuantConfig(bits=4, group_size=GS)
+    mods = {}
+    for name, N, K in bench.LLAMA:
+        packed, s, z = ref[name]
+        mods[name] = P.QuantizedLinear(torch.from_numpy(packed).to(DEV), torch.from_numpy(s).to(DEV),
+                                       torch.from_numpy(z).to(DEV), qcfg, None, K, N, use_kernel=True)
+    for group in (("q", "k", "v"), ("gate", "up"), ("o",), ("down",)):
+        K = mods[group[0]].in_features
+        x = torch.randn(1, K, generator=torch.Generator().manual_seed(K + len(group))).half()
+        outs = P.FusedQuantizedLinear([mods[n] for n in group])(x.to(DEV))
+        for n, y in zip(group, outs):
+            _check(y, _ref_fp32(x, O.dequantize_packed(*ref[n])), f"C2 module {n} in {'+'.join(group)}")
+            _check(mods[n](x.to(DEV)), _ref_fp32(x, O.dequantize_packed(*ref[n])), f"C2 module {n}")
+
+
+def test_c2_rmsnorm_gemv_gate_up_m1(llama_layer):
+    """The decoder's batch-1 gate/up launch (residual add + RMSNorm fused into
+    the N = 28672 GEMV) against an fp32 norm rounded to fp16, then the oracle."""
+    from pare_amd.kernels import matmul_w4a16_rmsnorm
+
+    bufs, _, w_hat = llama_layer
+    buf = bufs["gate_up"]
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(1, 4096, generator=g).half()
+    r = torch.randn(1, 4096, generator=g).half()
+    nw = (1 + 0.1 * torch.randn(4096, generator=g)).half()
+    y, h = matmul_w4a16_rmsnorm(x.to(DEV), r.to(DEV), nw.to(DEV), 1e-5, buf.w, buf.s, buf.z, GS)
+    h_ref = (x.float() + r.float()).half()
+    assert torch.equal(h.cpu(), h_ref)
+    hf = h_ref.float()
+    a = (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5) * nw.float()).half()
+    _check(y, _ref_fp32(a, np.concatenate([w_hat["gate"], w_hat["up"]])),
+           "C2 rmsnorm GEMV gate_up 28672x4096 M=1")
+
+
+def test_c2_glu_down_m1(llama_layer):
+    """The decoder's batch-1 down launch (SiLU(gate)*up formed in the GEMV)
+    against fp32 SiLU rounded as the kernel rounds, then the oracle."""
+    from pare_amd.kernels import matmul_w4a16_glu
+
+    bufs, _, w_hat = llama_layer
+    buf = bufs["down"]
+    gu = (torch.randn(1, 2 * 14336, generator=torch.Generator().manual_seed(43)) * 2).half()
+    y = matmul_w4a16_glu(gu.to(DEV), buf.w, buf.s, buf.z, GS)
+    gate, up = gu[:, :14336].float(), gu[:, 14336:].float()
+    a = ((gate * torch.sigmoid(gate)).half().float() * up).half()
+    _check(y, _ref_fp32(a, w_hat["down"]), "C2 glu GEMV down 4096x14336 M=1")
+
+
+# ---------------------------------------------------------------------------
+# C3: gate_proj at every M of the sweep, automatic dispatch
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 64, 128])
+def test_c3_gate_sweep(llama_layer, M):
+    bufs, _, w_hat = llama_layer
+    buf = bufs["gate"]
+    x = torch.randn(M, 4096, generator=torch.Generator().manual_seed(100 + M)).half()
+    _check(_launch(buf, x), _ref_fp32(x, w_hat["gate"]),
+           f"C3 gate 14336x4096 M={M} ({P.kernel_choice(M, 14336, 4096, GS)})")
+
+
+# ---------------------------------------------------------------------------
+# the reference harness's M (128 * bs, bs in {1, 4, 16}) on the Llama shapes
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("name", ["q", "gate", "down", "gate_up"])
+def test_prefill_sizes(llama_layer, name, M):
+    bufs, _, w_hat = llama_layer
+    buf = bufs[name]
+    wh = np.concatenate([w_hat[p] for p in _FUSED_PARTS.get(name, (name,))])
+    x = torch.randn(M, buf.K, generator=torch.Generator().manual_seed(M + buf.N)).half()
+    _check(_launch(buf, x), _ref_fp32(x, wh),
+           f"{name} {buf.N}x{buf.K} M={M} ({P.kernel_choice(M, buf.N, buf.K, GS)})")
+
+
+# ---------------------------------------------------------------------------
+# C4: Qwen2.5-7B act_order layers at M = 1 and 16, as the bench builds them
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("qi", range(len(bench.QWEN)))
+def test_c4_qwen_act_order(qi):
+    name, N, K = bench.QWEN[qi]
+    seed = 7000 + 100 * qi
+    buf = bench.make_act_order_layer(N, K, seed, DEV)
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    w = torch.randn(N, K, generator=g, device=DEV) * 0.02
+    perm = torch.randperm(K, generator=g, device=DEV).cpu().numpy()
+    assert (buf.perm.cpu().numpy() == perm).all()
+    packed_p, s, z = O.rtn_quantize(w.cpu().numpy()[:, perm], GS)   # groups in permuted order
+    _assert_buf_matches(buf, packed_p, s, z)
+    q = np.empty((N, K), dtype=np.int64)
+    q[:, perm] = O.unpack_int4(packed_p)
+    w_hat = O.dequantize_gidx(q, s, z, O.gidx_from_perm(perm, GS))
+    for M in (1, 16):
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(M + qi)).half()
+        _check(_launch(buf, x), _ref_fp32(x, w_hat),
+               f"C4 qwen {name} {N}x{K} act_order M={M} ({P.kernel_choice(M, N, K, GS)})")
+
+
+# ---------------------------------------------------------------------------
+# C5: the 32-layer Llama-3.1-8B-shaped decoder of the end-to-end bench
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def full_decoder():
+    from pare_amd.decoder import DecoderConfig, QuantizedDecoder
+
+    model = QuantizedDecoder(DecoderConfig(), DEV, seed=0)
+    yield model
+    del model
+    torch.cuda.empty_cache()
+
+
+def _set_kernel(model, on: bool):
+    for m in model.modules():
+        if isinstance(m, P.QuantizedLinear):
+            m.use_kernel = on
+
+
+def test_c5_full_decoder_prefill_matches_dequant_path(full_decoder):
+    """Kernel path against the reference's dequantize-on-the-fly path (fp16
+    F.linear on dequantize()) through all 32 layers: logits of a 24-token
+    prompt at batch 2."""
+    model = full_decoder
+    g = torch.Generator(device=DEV).manual_seed(3)
+    toks = torch.randint(0, model.cfg.vocab, (2, 24), generator=g, device=DEV)
+    cos, sin = model.rope_tables(24)
+    pos = torch.arange(24, device=DEV)
+    with torch.no_grad():
+        a = model.forward_tokens(toks, cos, sin, model.new_cache(2, 24), pos, None, True).float()
+        _set_kernel(model, False)
+        try:
+            b = model.forward_tokens(toks, cos, sin, model.new_cache(2, 24), pos, None, True).float()
+        finally:
+            _set_kernel(model, True)
+    err = (a - b).abs().max().item()
+    scale = b.abs().max().item()
+    agree = (a.argmax(-1) == b.argmax(-1)).float().mean().item()
+    print(f"[baseline] C5 32-layer prefill kernel vs dequant path: max_abs={err:.3e} "
+          f"(max |logit| {scale:.3e}), argmax agreement {agree:.3f}", flush=True)
+    assert err <= 1e-2 + 2e-2 * scale
+    assert agree >= 0.9
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_c5_full_decoder_graph_decode_equals_eager(full_decoder, batch):
+    model = full_decoder
+    g = torch.Generator(device=DEV).manual_seed(10 + batch)
+    prompt = torch.randint(0, model.cfg.vocab, (batch, 32), generator=g, device=DEV)
+    eager, _ = model.generate(prompt, 8, use_graph=False)
+    graph, _ = model.generate(prompt, 8, use_graph=True)
+    print(f"[baseline] C5 batch={batch} tokens {graph[0].tolist()}", flush=True)
+    assert torch.equal(eager, graph)
+
+
+# ---------------------------------------------------------------------------
+# the reference's throughput gate (pare tests/test_triton_kernel.py:252-283)
+# ---------------------------------------------------------------------------
+
+def test_speed_gate_kernel_vs_dequant_path_bs4():
+    """The fused kernel at least 1.5x faster than the same module's
+    dequantize-on-the-fly forward (use_kernel=False: HIP dequant to fp16, then
+    torch's fp16 GEMM) on 4096x4096 at "BS=4" (x [4*128, 4096], M = 512), with
+    the reference's 3 warmup and 10 timed calls, timed on the host around a
+    synchronize as the reference does; the median of 5 such rounds."""
+    import statistics
+    import time
+
+    lin = torch.nn.Linear(4096, 4096, bias=False)
+    torch.nn.init.normal_(lin.weight, std=0.02, generator=torch.Generator().manual_seed(0))
+    ql = P.QuantizedLinear.from_linear(lin.to(DEV), P.QuantConfig(bits=4, group_size=GS))
+    x = torch.randn(4 * 128, 4096, generator=torch.Generator(device=DEV).manual_seed(1),
+                    device=DEV).half()
+
+    def bench_ms(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / 10 * 1e3
+
+    def dq():
+        ql.use_kernel = False
+        return ql(x)
+
+    def kern():
+        ql.use_kernel = True
+        return ql(x)
+
+    with torch.no_grad():
+        ms_dq = statistics.median(bench_ms(dq) for _ in range(5))
+        ms_k = statistics.median(bench_ms(kern) for _ in range(5))
+    print(f"[gate] M=512 4096x4096: dequant path {ms_dq * 1e3:.1f} us, kernel {ms_k * 1e3:.1f} us, "
+          f"speedup {ms_dq / ms_k:.2f}x", flush=True)
+    assert ms_dq / ms_k >= 1.5, f"speedup {ms_dq / ms_k:.2f}x < 1.5x"

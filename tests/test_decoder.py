@@ -305,3 +305,45 @@ def test_silu_mul(rows, F):
     ref = torch.nn.functional.silu(gf[:, :F]) * gf[:, F:]
     err = (got.float() - ref).abs() / (ref.abs() + 1e-3)
     assert err.max().item() <= 2e-3, err.max().item()
+
+
+def _attention_ref(q, ck, cv, p):
+    """fp32 attention of q [B, H, 1, D] over cache positions 0..p."""
+    B, H, _, D = q.shape
+    grp = H // ck.shape[1]
+    kf = ck[:, :, :p + 1].float().repeat_interleave(grp, dim=1)
+    vf = cv[:, :, :p + 1].float().repeat_interleave(grp, dim=1)
+    sc = (q.float() * (1 / D ** 0.5)) @ kf.transpose(-1, -2).contiguous()
+    return (torch.softmax(sc, -1) @ vf)[:, :, 0]
+
+
+def test_shared_workspaces_alternate_large_and_small_shapes():
+    """One stream, one cached workspace per op, shapes alternating between many
+    counters (B * KV = 128, 72 argmax rows) and few: each call's counters must
+    start at zero whatever the previous shape's partials wrote. Checked against
+    fp32 references for split attention, attention with fused RoPE and argmax."""
+    from pare_amd.decoder import argmax_into, decode_attention_rope
+
+    D, H, KV, L = 128, 32, 8, 200
+    g = torch.Generator(device=DEV).manual_seed(99)
+    cos, sin = rope_tables(D, 500000.0, L, DEV)
+    for B in (16, 1, 16, 2, 16):
+        p = 150 if B > 1 else 40
+        pos = torch.full((1,), p, dtype=torch.long, device=DEV)
+        q = torch.randn(B, H, 1, D, generator=g, device=DEV).half()
+        ck = torch.randn(B, KV, L, D, generator=g, device=DEV).half()
+        cv = torch.randn(B, KV, L, D, generator=g, device=DEV).half()
+        err = (decode_attention(q, ck, cv, pos, 1 / D ** 0.5).float() - _attention_ref(q, ck, cv, p))
+        assert err.abs().max().item() <= 5e-3, (B, err.abs().max().item())
+        qkv = torch.randn(B, (H + 2 * KV) * D, generator=g, device=DEV).half()
+        ck2, cv2 = ck.clone(), cv.clone()
+        qr = rope_kv(qkv.view(B, 1, -1), cos, sin, pos, ck2, cv2, B, 1, H, KV, D)
+        got = decode_attention_rope(qkv, cos, sin, pos, ck, cv, 1 / D ** 0.5)
+        err = (got.float() - _attention_ref(qr, ck2, cv2, p)).abs().max().item()
+        assert err <= 5e-3, ("rope", B, err)
+        rows = 72 if B > 2 else B
+        x = torch.randn(rows, 4000, generator=g, device=DEV).half()
+        out = torch.full((rows,), -1, dtype=torch.long, device=DEV)
+        argmax_into(x, out)
+        assert torch.equal(out, x.argmax(-1)), ("argmax", rows)
+        print(f"[workspace] B={B} argmax rows={rows} ok", flush=True)

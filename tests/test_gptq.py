@@ -193,12 +193,33 @@ class TestOracleGptq:
             objs[act_order] = O.gptq_objective(W, w_hat, H)
         assert objs[True] <= objs[False] * 1.05, objs
 
+    def test_offset8_known_answers(self):
+        """Hand-derived offset-8 groups (zero 8, scale 2 max|w| / 15, codes
+        clamp(rint(w / s + 8), 0, 15) with ties to even).
+        Row 0: max|w| = 7.5, so the scale is exactly 1.0 and the codes are
+        w + 8 rounded: -7.5 -> 0.5 -> 0; 7.5 -> 15.5 -> 16 -> clamped 15;
+        -0.5 -> 7.5 -> 8; 0.5 -> 8.5 -> 8; 1.5 -> 9.5 -> 10; -3.2 -> 4.8 -> 5;
+        2.49 -> 10.49 -> 10; -6.5 -> 1.5 -> 2; 6.5 -> 14.5 -> 14; 0 -> 8.
+        Row 1: max|w| = 0.375, scale 0.05 -> fp32 0x3D4CCCCD (13421773 * 2^-28).
+        0.375 / s rounds to 7.5 in fp32 -> 15.5 -> 16 -> 15; -0.375 -> 0;
+        0.1 (fp32 13421773 * 2^-27) / s = 2 exactly -> 10; -0.125 / s rounds
+        to -2.5 -> 5.5 -> 6."""
+        w = np.zeros((2, 32), np.float32)
+        w[0, :10] = [-7.5, 7.5, 0.0, -0.5, 0.5, 1.5, -3.2, 2.49, -6.5, 6.5]
+        w[1, :4] = [0.375, -0.375, 0.1, -0.125]
+        packed, s, z = O.rtn_quantize(w, 32, sym="offset8")
+        assert s.reshape(2).view(np.uint32).tolist() == [0x3F800000, 0x3D4CCCCD]
+        assert z.reshape(2).tolist() == [8.0, 8.0]
+        q = O.unpack_int4(packed)
+        assert q[0, :10].tolist() == [0, 15, 8, 8, 8, 10, 5, 10, 2, 14]
+        assert (q[0, 10:] == 8).all()
+        assert q[1, :4].tolist() == [15, 0, 10, 6]
+        assert (q[1, 4:] == 8).all()
+
     def test_offset8_sym(self):
         W, H, _ = _layer(8, 128, seed=6)
         p, s, z, _ = O.gptq_quantize(W, H, 64, sym=True)
         assert (z == 8).all()
-        amax = np.abs(W.reshape(8, 2, 64)).max(-1)
-        np.testing.assert_array_equal(s[..., 0], (np.float32(2.0) * amax / np.float32(15.0)).astype(np.float32))
         # the reference's rule would clamp every negative weight to code 0
         q = _codes(p)
         assert (q[W < -0.05] < 8).all()

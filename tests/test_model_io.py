@@ -105,3 +105,46 @@ def test_roundtrip_gpu_forward(tmp_path, kernel_layout):
         assert dst.proj._packed_weight_kernel is not None
     y1 = dst.proj(x)
     assert torch.equal(y0, y1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act_order", [False, True])
+@pytest.mark.parametrize("kernel_layout", [False, True])
+def test_reloaded_layer_matches_oracle(tmp_path, kernel_layout, act_order):
+    """A layer written by save_quantized and read back by load_quantized (with
+    and without the stored kernel layout, with and without g_idx) against the
+    oracle: dequantized weights bit-exact, forward within rtol/atol 1e-2 of the
+    fp32-accumulated reference."""
+    import warnings
+
+    dev = torch.device("cuda:0")
+    N, K, gs = 192, 512, 128
+    w = (torch.randn(N, K, generator=torch.Generator().manual_seed(11)) * 0.02).numpy()
+    g_idx = None
+    if act_order:
+        perm = np.random.default_rng(5).permutation(K)
+        packed, s, z, g_idx = O.rtn_quantize_act_order(w, perm, gs)
+        w_hat = O.dequantize_gidx(O.unpack_int4(packed), s, z, g_idx)
+    else:
+        packed, s, z = O.rtn_quantize(w, gs)
+        w_hat = O.dequantize_packed(packed, s, z)
+    m = Tiny(K, N)
+    m.proj = P.QuantizedLinear(torch.from_numpy(packed), torch.from_numpy(s), torch.from_numpy(z),
+                               P.QuantConfig(bits=4, group_size=gs), None, K, N,
+                               g_idx=torch.from_numpy(g_idx) if act_order else None)
+    m = m.to(dev)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        save_quantized(m, tmp_path, kernel_layout=kernel_layout)
+    assert any("g_idx" in str(c.message) for c in caught) == act_order
+    dst = load_quantized(Tiny(K, N), tmp_path, device=dev).to(dev)
+    assert (dst.proj.g_idx is not None) == act_order
+    dq = dst.proj.dequantize(torch.float16).cpu().numpy()
+    assert (dq.view(np.uint16) == w_hat.astype(np.float16).view(np.uint16)).all()
+    x = torch.randn(5, K, generator=torch.Generator().manual_seed(12)).half()
+    y = dst.proj(x.to(dev)).float().cpu().numpy()
+    ref = O.linear_fp32(x.float().numpy(), w_hat)
+    err = np.abs(y - ref)
+    print(f"[reload] kernel_layout={kernel_layout} act_order={act_order}: max_abs={err.max():.3e}",
+          flush=True)
+    assert (err <= 1e-2 + 1e-2 * np.abs(ref)).all()
