@@ -150,6 +150,26 @@ PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* pmi_matmul_w4a16 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, kernels and results as
+ * pmi_matmul_w4a16 given a workspace of pmi_matmul_workspace_bytes() bytes.
+ * The scratch is a fixed 16 MiB array the library holds on each GPU it runs
+ * on until the process ends (found with hipGetSymbolAddress on the first call
+ * on a device, which also clears its counter block: make that first call
+ * outside graph capture). Shapes whose pmi_matmul_workspace_bytes() exceeds
+ * 16 MiB (large-M act_order layers) fail with PMI_ERR_UNSUPPORTED. Allocates
+ * nothing. Every call on one GPU shares that GPU's scratch, so calls that
+ * may overlap on one GPU (other streams, other threads) race; calls on one
+ * stream are ordered and safe.
+ * No reference counterpart: an allocation-free form of
+ *           matmul_w4a16  pare/kernels/matmul_int4.py:183-243, for the callers above. */
+PMI_API int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w,
+                                     const float* scales, const void* zeros, int zero_dtype,
+                                     const int32_t* perm, const float* scales_gm,
+                                     const uint8_t* zeros_gm, void* y, int y_dtype, int64_t M,
+                                     int64_t N, int64_t K, int64_t group_size, void* stream);
+
 /* y = (silu(gate) * up) . dequant(W)^T for M <= 4, the down projection of a
  * gated MLP fused with its activation: gate_up is fp16 [M, 2K] (gate in
  * columns 0..K-1, up in K..2K-1, the output of a fused gate/up matmul), and

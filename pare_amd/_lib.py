@@ -54,6 +54,8 @@ SIGNATURES = {
                                      _vp]),
     "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i64,
                              _i64, _vp, ctypes.c_size_t, _vp]),
+    "pmi_matmul_w4a16_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64,
+                                      _i64, _i64, _vp]),
     "pmi_matmul_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i]),
     "pmi_dequant_w4a16": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _vp]),
     "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),

@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "pmi_launch.h"
 
@@ -370,6 +371,94 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, perm, yp + m * N, mt, N, K,
                                     group_size, s, perm_lds ? &perm_xf : nullptr);
     if (e != hipSuccess) return from_hip(e, fn);
+  }
+  return ok();
+}
+
+}  // extern "C"
+
+// ---- allocation-free matmul ---------------------------------------------------
+// The scratch of pmi_matmul_w4a16_noalloc: a file-scope device array, one copy
+// per GPU, held until the process ends. In host code `scratch` only names the
+// symbol; its device address on the current GPU comes from
+// hipGetSymbolAddress, once per device, and only that address is ever passed
+// to a kernel. Layout as a pmi_matmul_w4a16 workspace: the split-K counter
+// block first (zero between calls; cleared by a fill kernel the first time a
+// device is used), then the act_order gather of X and the partial tiles.
+namespace {
+constexpr size_t kScratchBytes = 16u << 20;
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+__global__ void scratch_clear_kernel(uint32_t* p, int words) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device (set up on first use,
+// with its counter block cleared on `stream` ahead of the caller's launches).
+int scratch_ptr(void** out, hipStream_t stream, const char* fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return from_hip(e, fn);
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: device %d is beyond the %d devices served", fn, dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return from_hip(e, fn);
+    if (!p) return fail(PMI_ERR_HIP, "%s: hipGetSymbolAddress gave a null address", fn);
+    const int words = (int)(pmi::kWsCounterBytes / 4);
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
+                       (uint32_t*)p, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e, fn);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PMI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w, const float* scales,
+                             const void* zeros, int zero_dtype, const int32_t* perm,
+                             const float* scales_gm, const uint8_t* zeros_gm, void* y,
+                             int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                             void* stream) {
+  const char* fn = "pmi_matmul_w4a16_noalloc";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
+  if (M == 0 || N == 0) return ok();
+  const size_t need = pmi_matmul_workspace_bytes(M, N, K, group_size, perm != nullptr);
+  if (need > kScratchBytes)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: this shape needs %zu bytes of scratch (M=%lld N=%lld "
+                "K=%lld%s), more than the library's fixed %zu; call pmi_matmul_w4a16 with a "
+                "workspace of pmi_matmul_workspace_bytes() bytes", fn, need, (long long)M,
+                (long long)N, (long long)K, perm ? ", act_order" : "", kScratchBytes);
+  void* ws = nullptr;
+  if (need) {
+    if (int rc = scratch_ptr(&ws, (hipStream_t)stream, fn)) return rc;
+  }
+  const int rc = pmi_matmul_w4a16(x, x_dtype, w, scales, zeros, zero_dtype, perm, scales_gm,
+                                  zeros_gm, y, y_dtype, M, N, K, group_size, ws,
+                                  need ? kScratchBytes : 0, stream);
+  if (rc) {
+    // keep the message, name this entry point
+    char msg[sizeof(g_err)];
+    snprintf(msg, sizeof(msg), "%s", g_err);
+    return fail(rc, "%s: %s", fn, msg);
   }
   return ok();
 }
