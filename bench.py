@@ -17,11 +17,17 @@ The seven-launch step (one launch per QuantizedLinear) is reported beside it.
 Printed JSON line: value = aggregate algorithmic HBM throughput (GB/s) of the
 step; "roofline" is that of the dominant kernel (the fused gate/up GEMV),
 "cpu_baseline" the reference's dequantize-on-the-fly path restated on the
-host CPU (oracle, timed on a bounded sample), "detail" per-shape µs / GB/s, the
-seven-launch step, the M=64 MFMA GEMM TFLOP/s, the Qwen2.5-7B act_order
-layers (g_idx from a seeded permutation, M = 1 and 16)
-and the end-to-end decoder (configs[4]: 512-token prompt, 128 greedy tokens at
-batch 1 and 4, the reference's tok/s definition).
+host CPU (oracle, timed on a bounded sample, with the kernel's max-abs error
+against the fp32-accumulated oracle for config 1 and each config-2 linear),
+"detail" per-shape µs / GB/s, the seven-launch step, the M=64 MFMA GEMM
+TFLOP/s, the gate_proj M sweep (configs[2]: µs, GB/s, TFLOP/s and both roofline
+fractions per M), measured achievable peaks (read floor of the gate/up weights,
+1 GiB read and copy, torch fp16 GEMM), the reference's own 4096x4096 shapes at
+M = 128/512/2048 beside the dequant path, the Qwen2.5-7B act_order layers
+(configs[3]: g_idx from a seeded permutation, M = 1 and 16) and the end-to-end
+decoder (configs[4]: 512-token prompt, 128 greedy tokens at batch 1 and 4, the
+reference's tok/s definition; with the library's decode ops and with PyTorch
+SDPA attention).
 
 Algorithmic bytes per call: N*K/2 (INT4 codes) + N*G*(4 + 1) (fp32 scale +
 u8 zero, the format the kernels read) + M*K*2 (x) + M*N*2 (y); FLOPs 2*M*N*K.
@@ -179,38 +185,186 @@ def time_graph(g, reps, stream):
     return start.elapsed_time(end) / reps
 
 
-def cpu_baseline(max_threads=16):
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(dev=None):
     """The reference's dequantize-on-the-fly forward on the host CPU, op for op
     (oracle.dequant_path_forward_torch), on one decoder layer's seven linears at
-    M=1: 1 warmup + 3 timed passes per layer, median per layer."""
+    M=1, on every core this process may run on: 2 warmup + 5 timed passes per
+    layer, median per layer. Outside its timed loops the same inputs also run
+    through the HIP kernel (when `dev` is given) for each linear's max-abs error
+    against the fp32-accumulated oracle, and likewise config 1 (4096x4096,
+    weights seed 0, x seed 1)."""
     import torch
 
     from oracle import pare_oracle as O
 
-    threads = min(len(os.sched_getaffinity(0)), max_threads)
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     total_bytes, total_s = 0, 0.0
+    max_abs = {}
     g = torch.Generator().manual_seed(1234)
+
+    def kernel_err(name, x, packed, s, z):
+        import pare_amd as P
+
+        if dev is None:
+            return
+        wk = P.repack_int4_for_kernel(torch.from_numpy(packed).to(dev), GS)
+        y = P.matmul_w4a16(x.to(dev), wk, torch.from_numpy(s).to(dev),
+                           P.zeros_to_u8(torch.from_numpy(z).to(dev)), GS).float().cpu().numpy()
+        ref = O.linear_fp32(x.float().numpy(), O.dequantize_packed(packed, s, z))
+        max_abs[name] = float(f"{abs(y - ref).max():.4g}")
+
     for name, N, K in LLAMA:
         w = (torch.randn(N, K, generator=g) * 0.02).numpy()
         packed, s, z = O.rtn_quantize(w, GS)
         tp, ts, tz = torch.from_numpy(packed), torch.from_numpy(s), torch.from_numpy(z)
         x = torch.randn(1, K, generator=g).to(torch.float16)
-        O.dequant_path_forward_torch(x, tp, ts, tz)
+        for _ in range(2):
+            O.dequant_path_forward_torch(x, tp, ts, tz)
         times = []
-        for _ in range(3):
+        for _ in range(5):
             t0 = time.perf_counter()
             O.dequant_path_forward_torch(x, tp, ts, tz)
             times.append(time.perf_counter() - t0)
         total_s += statistics.median(times)
         total_bytes += layer_bytes(N, K, 1, 4, 4)
+        kernel_err(name, x, packed, s, z)
+    w1 = (torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)) * 0.02).half()
+    x1 = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1)).half()
+    kernel_err("C1", x1, *O.rtn_quantize(w1.float().numpy(), GS))
     return {"value": round(total_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": "one Llama-3.1-8B decoder layer's 7 INT4 g128 linears at M=1 through the "
                       "oracle's op-for-op restatement of the reference dequant path "
-                      "(unpack->float->(q-z)*s->fp16->F.linear) on the host CPU; median of 3 "
-                      "after 1 warmup per layer; bytes in the reference layout (fp32 s+z)",
-            "ms_per_layer_set": round(total_s * 1e3, 2)}
+                      "(unpack->float->(q-z)*s->fp16->F.linear) on the host CPU, all affinity "
+                      "cores; median of 5 after 2 warmups per layer; bytes in the reference "
+                      "layout (fp32 s+z)",
+            "cpu_model": _cpu_model(),
+            "ms_per_layer_set": round(total_s * 1e3, 2),
+            "kernel_max_abs_vs_fp32_oracle": max_abs}
+
+
+def measured_peaks(L, dev, stream, gate_up_bufs):
+    """Achievable rates on this box, next to the vendor peaks: the read floor of
+    the fused gate/up weights (pmi_read_probe over the same 32 x 58.7 MB set the
+    GEMV streams, at several grids), a 1 GiB streaming read, a 1 GiB device
+    copy, and torch's fp16 GEMM (hipBLASLt) at the M = 64 gate shape and 8192^3."""
+    import torch
+
+    out = {}
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    wbytes = gate_up_bufs[0].w.numel()
+    floor = {}
+    for per_cu in (1, 2, 4, 8):
+        grid = n_cu * per_cu
+
+        def rd(s, grid=grid):
+            for _ in range(2):
+                for b in gate_up_bufs:
+                    rc = L.pmi_read_probe(b.w.data_ptr(), wbytes, grid, sink.data_ptr(), s)
+                    assert rc == 0
+        gr = capture(rd, stream)
+        gr.replay()
+        us = time_graph(gr, 5, stream) * 1e3 / (2 * len(gate_up_bufs))
+        floor[f"grid_{grid}"] = {"us": round(us, 2), "GB/s": round(wbytes / (us * 1e-6) / 1e9, 1)}
+        del gr
+    best = min(floor.values(), key=lambda r: r["us"])
+    out["read_floor_gate_up_weights"] = {"bytes_per_launch": wbytes, "best": best, **floor}
+    big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    big2 = torch.empty_like(big)
+
+    def rd_big(s):
+        for _ in range(4):
+            assert L.pmi_read_probe(big.data_ptr(), big.numel(), 8 * n_cu, sink.data_ptr(), s) == 0
+    gb = capture(rd_big, stream)
+    gb.replay()
+    ms = time_graph(gb, 3, stream) / 4
+    out["stream_read_1GiB_GBs"] = round(big.numel() / (ms * 1e-3) / 1e9, 1)
+    del gb
+    with torch.cuda.stream(stream):
+        big2.copy_(big)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(5):
+            big2.copy_(big)
+        t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / 5
+    out["copy_1GiB_GBs_read_plus_write"] = round(2 * big.numel() / (ms * 1e-3) / 1e9, 1)
+    del big, big2
+    for (m, n, k) in ((64, 14336, 4096), (8192, 8192, 8192)):
+        a = torch.randn(m, k, device=dev).half()
+        b = torch.randn(n, k, device=dev).half()
+        c = torch.empty(m, n, device=dev).half()
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                torch.matmul(a, b.t(), out=c)
+            torch.cuda.synchronize()
+            reps = 20 if m < 8192 else 5
+            t0.record(stream)
+            for _ in range(reps):
+                torch.matmul(a, b.t(), out=c)
+            t1.record(stream)
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / reps
+        out[f"torch_fp16_gemm_{m}x{n}x{k}"] = {"us": round(us, 2),
+                                               "TFLOP/s": round(2 * m * n * k / (us * 1e-6) / 1e12, 1)}
+        del a, b, c
+    torch.cuda.empty_cache()
+    return out
+
+
+def reference_shapes(dev, stream):
+    """The only per-layer figures the reference publishes (README.md:138-142):
+    4096x4096 INT4 g128 at "BS" 1, 4, 16 of x [bs, 128, 4096], i.e. M = 128, 512,
+    2048, kernel against the same module's dequantize-on-the-fly forward
+    (use_kernel=False: HIP dequant to fp16, then torch's fp16 GEMM). Each path
+    is captured as a graph of 10 calls and replayed."""
+    import torch
+    import torch.nn as nn
+
+    import pare_amd as P
+
+    lin = nn.Linear(4096, 4096, bias=False)
+    nn.init.normal_(lin.weight, std=0.02, generator=torch.Generator().manual_seed(0))
+    ql = P.QuantizedLinear.from_linear(lin.to(dev), P.QuantConfig(bits=4, group_size=GS))
+    rows = {}
+    for bs in (1, 4, 16):
+        M = 128 * bs
+        x = torch.randn(M, 4096, device=dev).half()
+        res = {"M": M}
+        for path, flag in (("kernel", True), ("dequant_path", False)):
+            ql.use_kernel = flag
+            with torch.cuda.stream(stream):
+                ql(x)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for _ in range(10):
+                    ql(x)
+            g.replay()
+            us = time_graph(g, 5, stream) * 1e3 / 10
+            res[f"{path}_us"] = round(us, 2)
+            del g
+        res["speedup"] = round(res["dequant_path_us"] / res["kernel_us"], 2)
+        res["kernel_TFLOP/s"] = round(2 * M * 4096 * 4096 / (res["kernel_us"] * 1e-6) / 1e12, 1)
+        res["kernel"] = P.kernel_choice(M, 4096, 4096, GS)
+        rows[f"bs{bs}"] = res
+        log(f"  reference shape 4096x4096 M={M}: {res}")
+    ql.use_kernel = True
+    return rows
 
 
 def main():
@@ -221,11 +375,14 @@ def main():
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only",
-                    choices=["gate_up_m1", "gate_m64", "copy", "e2e_bs1", "e2e_bs4"],
+                    choices=["gate_up_m1", "gate_m64", "gate", "read_floor", "copy", "e2e_bs1",
+                             "e2e_bs4"],
                     default=None,
-                    help="run only one kernel loop (for rocprofv3 counter passes); e2e_bs1 / "
-                         "e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens")
-    ap.add_argument("--sweep", action="store_true", help="also run the gate_proj M sweep")
+                    help="run only one kernel loop (for rocprofv3 counter passes): gate_up_m1 "
+                         "the fused gate/up GEMV; gate the gate_proj launches at --m rows "
+                         "(gate_m64: --m 64); read_floor the plain read of the gate/up weights; "
+                         "e2e_bs1 / e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens")
+    ap.add_argument("--m", type=int, default=64, help="activation rows of --kernel-only gate")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoder leg")
     args = ap.parse_args()
 
@@ -317,14 +474,23 @@ def main():
     torch.cuda.synchronize()
 
     if args.kernel_only:
+        m_rows = 64 if args.kernel_only == "gate_m64" else args.m
+        assert 1 <= m_rows <= M_MAX, f"--m must be in 1..{M_MAX}"
+        sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+        n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
         with torch.cuda.stream(stream):
             for _ in range(5):
                 if args.kernel_only == "gate_up_m1":
                     gate_up_loop(stream.cuda_stream, 1)
+                elif args.kernel_only == "read_floor":
+                    for f in fused:
+                        assert L.pmi_read_probe(f[2].w.data_ptr(), f[2].w.numel(), 4 * n_cu,
+                                                sink.data_ptr(), stream.cuda_stream) == 0
                 else:
-                    gate_loop(stream.cuda_stream, 64, 2 * n_layers)
+                    gate_loop(stream.cuda_stream, m_rows, 2 * n_layers)
         torch.cuda.synchronize()
-        log(f"{args.kernel_only}: 5 passes")
+        log(f"{args.kernel_only} (M={m_rows}): 5 passes, kernel "
+            f"{P.kernel_choice(m_rows, 14336, 4096, GS)}")
         return
 
     # --- eager vs graph: same outputs -------------------------------------
@@ -406,6 +572,26 @@ def main():
     log(f"  gate M=64: {m64_us:.2f} us {m64_tflops:.1f} TFLOP/s {m64_gbs:.1f} GB/s")
     del gm
 
+    # --- config 3: gate_proj at M = 1 .. 128, automatic dispatch -------------
+    sweep = {}
+    for M in (1, 2, 4, 8, 16, 32, 64, M_MAX):
+        gs_ = capture(lambda s, M=M: gate_loop(s, M, copies), stream)
+        gs_.replay()
+        us = time_graph(gs_, 5, stream) * 1e3 / copies
+        gbs = layer_bytes(14336, 4096, M) / (us * 1e-6) / 1e9
+        tfl = 2 * M * 14336 * 4096 / (us * 1e-6) / 1e12
+        sweep[M] = {"us": round(us, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
+                    "TFLOP/s": round(tfl, 2), "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4),
+                    "kernel": P.kernel_choice(M, 14336, 4096, GS)}
+        log(f"  sweep gate M={M:3d}: {sweep[M]}")
+        del gs_
+    detail["gate_sweep"] = sweep
+
+    # --- achievable peaks and the reference's own per-layer shapes ----------
+    detail["measured_peaks"] = measured_peaks(L, dev, stream, [f[2] for f in fused])
+    log(f"  measured peaks: {detail['measured_peaks']}")
+    detail["reference_shapes_4096x4096"] = reference_shapes(dev, stream)
+
     # --- Qwen2.5-7B act_order layers at M = 1 and 16 (config 4) ---------------
     qwen = {}
     for qi, (name, N, K) in enumerate(QWEN):
@@ -450,32 +636,33 @@ def main():
             e2e[f"bs{bs}"] = r
             log(f"  e2e BS={bs}: {r['tokens_per_sec']} tok/s, {r['decode_ms_per_step']} ms/step "
                 f"decode, prefill {r['prefill_ms']} ms")
+        # BASELINE.json configs[4] as stated: the linears on the HIP kernel, the
+        # rest of the model (attention via PyTorch SDPA, norms, RoPE, SiLU,
+        # argmax) in PyTorch-ROCm
+        model.fused_ops = False
+        e2e["torch_ops_note"] = ("fused_ops=False: every INT4 linear on the HIP kernel, attention "
+                                 "through torch scaled_dot_product_attention, norms/RoPE/SiLU/argmax "
+                                 "as PyTorch ops; still graph-captured decode")
+        for bs in (1, 4):
+            r = decoder_throughput(model, batch=bs, prompt_len=512, n_generate=128)
+            e2e[f"bs{bs}_torch_ops"] = r
+            log(f"  e2e BS={bs} (PyTorch SDPA attention): {r['tokens_per_sec']} tok/s, "
+                f"{r['decode_ms_per_step']} ms/step decode, prefill {r['prefill_ms']} ms")
+        model.fused_ops = True
         detail["e2e_decoder"] = e2e
         del model
         torch.cuda.empty_cache()
 
-    if args.sweep:
-        sweep = {}
-        for M in (1, 2, 4, 8, 16, 32, 64, M_MAX):
-            gs_ = capture(lambda s, M=M: gate_loop(s, M, copies), stream)
-            gs_.replay()
-            us = time_graph(gs_, 5, stream) * 1e3 / copies
-            sweep[M] = {"us": round(us, 2),
-                        "GB/s": round(layer_bytes(14336, 4096, M) / (us * 1e-6) / 1e9, 1),
-                        "TFLOP/s": round(2 * M * 14336 * 4096 / (us * 1e-6) / 1e12, 2),
-                        "kernel": P.kernel_choice(M, 14336, 4096, GS)}
-            log(f"  sweep gate M={M:3d}: {sweep[M]}")
-            del gs_
-        detail["gate_sweep"] = sweep
 
     traffic = None
     tfile = ROOT / "profiles" / "traffic_gemv_gate_up_m1.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
 
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_baseline(dev)
     if cpu:
-        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['cpu_model']}); "
+            f"kernel max-abs vs fp32 oracle {cpu['kernel_max_abs_vs_fp32_oracle']}")
 
     out = {
         "metric": METRIC,

@@ -358,6 +358,15 @@ PMI_API size_t pmi_argmax_workspace_bytes(int64_t rows, int64_t n);
  * out [rows, F] fp16; F % 8 == 0. */
 PMI_API int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64_t F, void* stream);
 
+/* ---- Measurement hook ------------------------------------------------------
+ * Reads `bytes` (a multiple of 16) of device memory at `buf` once, with at most
+ * `grid` workgroups each streaming one contiguous range in 16-byte loads, and
+ * computes nothing from it: the read floor that a kernel reading the same bytes
+ * on the same grid can reach. sink: device uint32 [grid] (never written in
+ * practice; it keeps the loads live). No reference counterpart. */
+PMI_API int pmi_read_probe(const void* buf, int64_t bytes, int64_t grid, uint32_t* sink,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

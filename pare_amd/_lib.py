@@ -72,6 +72,7 @@ SIGNATURES = {
     "pmi_decode_attention_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "pmi_argmax_f16": (_i, [_vp, _i64, _i64, _vp, _i64, _vp, ctypes.c_size_t, _vp]),
     "pmi_argmax_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "pmi_read_probe": (_i, [_vp, _i64, _i64, _vp, _vp]),
     "pmi_silu_mul_f16": (_i, [_vp, _vp, _i64, _i64, _vp]),
 }
 

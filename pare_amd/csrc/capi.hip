@@ -674,6 +674,16 @@ int pmi_argmax_f16(const void* x, int64_t rows, int64_t n, int64_t* out, int64_t
                   fn);
 }
 
+int pmi_read_probe(const void* buf, int64_t bytes, int64_t grid, uint32_t* sink, void* stream) {
+  const char* fn = "pmi_read_probe";
+  if (bytes < 0 || bytes % 16 != 0 || grid <= 0 || grid > (1 << 20))
+    return fail(PMI_ERR_INVALID, "%s: need bytes %% 16 == 0 and 0 < grid <= 2^20", fn);
+  if (bytes == 0) return ok();
+  if (!buf || !sink) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(buf, 16) || !aligned(sink, 4)) return fail(PMI_ERR_INVALID, "%s: misaligned", fn);
+  return from_hip(pmi::launch_read_probe(buf, bytes, grid, sink, (hipStream_t)stream), fn);
+}
+
 int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64_t F, void* stream) {
   const char* fn = "pmi_silu_mul_f16";
   if (rows < 0 || F <= 0 || F % 8 != 0)

@@ -182,6 +182,11 @@ hipError_t launch_gptq_block(const float* w, const float* c, const int32_t* colg
 hipError_t launch_gptq_pack(const uint8_t* qt, const int32_t* inv_perm, uint8_t* packed, int64_t N,
                             int64_t K, hipStream_t stream);
 
+// Streaming read of `bytes` (multiple of 16) over at most `grid` workgroups
+// (probes.hip); sink: `grid` uint32 (written only in a case that never occurs).
+hipError_t launch_read_probe(const void* buf, int64_t bytes, int64_t grid, uint32_t* sink,
+                             hipStream_t stream);
+
 hipError_t launch_rtn(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
                       int64_t N, int64_t K, int64_t gs, int sym, hipStream_t stream);
 
