@@ -466,11 +466,11 @@ def main():
         for i in range(copies):
             run(s, [single[i % n_layers][4 + (i // n_layers) % 2]], M)  # gate and up of all layers
 
-    # the M > 4 legs read group-major scale/zero copies: build them outside any
-    # graph capture, as a module does once per layer
-    for layer in single:
-        layer[4].gm()
-        layer[5].gm()
+    # group-major scale/zero copies (read by the one-row GEMV and the MFMA
+    # GEMM): built outside any graph capture, as a module does once per layer
+    for layer in fused + single:
+        for b in layer:
+            b.gm()
     torch.cuda.synchronize()
 
     if args.kernel_only:

@@ -19,7 +19,9 @@
 // range of rows. Each wave walks its rows in batches of U through a D-deep
 // register ring: buffer loads of batch i+D-1 (row offsets in SGPRs, so no
 // address VALU) are issued before batch i is unpacked and reduced. Every load
-// is unconditional, so the compiler waits for exactly the older batch.
+// is unconditional, so the compiler waits for exactly the older batch. The
+// weight loads are non-temporal: each 16-byte chunk is read once, and keeping
+// the stream out of the caches' normal replacement gave 3-5 % on every shape.
 //
 // Reduction. Partial sums of a batch are reduced across the 64 lanes with a
 // transpose butterfly (v_permlane32_swap / v_permlane16_swap for the two wide
@@ -218,7 +220,7 @@ PMI_DEV void load_batch(Batch<U, SPW, ZU8>& bt, const Rsrc& rs, int first_row, i
 #pragma unroll
     for (int sp = 0; sp < SPW; ++sp) {
       const u32x4 wv = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, boff[sp], n * row_bytes, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, boff[sp], n * row_bytes, 2));
       bt.w[sp][u] = wv;
       bt.s[sp][u] = __builtin_bit_cast(
           float, __builtin_amdgcn_raw_buffer_load_b32(rs.s, grp[sp] * 4, n * G * 4, 0));
@@ -725,15 +727,18 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
   c.slices_per_wave = c.n_slices > kMaxWaves ? 2 : 1;
   c.slice_waves = (c.n_slices + c.slices_per_wave - 1) / c.slices_per_wave;
   c.row_waves = kMaxWaves / c.slice_waves;
-  // Rows per batch (U) and workgroups per CU, from a sweep of every built
-  // variant on MI355X at M = 1 (graph-timed, 21-64 weight copies beyond the
-  // MALL). Long rows (three or more slice waves, e.g. K = 14336): four rows,
-  // one workgroup per CU (8.6 us against 9.0 us for pairs). Otherwise by rows
-  // per CU: >= 96 (N = 28672) pairs at three per CU (14.0 us), >= 48
-  // (N = 14336) pairs at one per CU (8.5 us), >= 20 (N = 6144) single rows
-  // at two per CU (5.4 us). Fewer rows (q/o, k/v): one batch per wave, of the
-  // most rows that still give every CU a workgroup (N = 4096: four rows,
-  // 4.4 us; N = 1024: one row, 3.2 us).
+  // Rows per batch (U) and workgroups per CU, from sweeps of every built
+  // variant on MI355X at M = 1 with non-temporal weight loads (graph-timed,
+  // 8-64 weight copies beyond the MALL, three sweeps). Rows longer than 16384
+  // columns (two slices per wave, e.g. K = 18944): single rows at two per CU
+  // (10.2 us against 11.4-11.7 for four rows at one). Long rows (three or more
+  // slice waves, e.g. K = 14336): four rows, one workgroup per CU (8.0 us).
+  // Otherwise by rows per CU: >= 48 (N = 14336 and 28672) pairs at one per CU
+  // (7.9 and 12.7-13.0 us; three per CU gave 13.8-14.3 us at N = 28672),
+  // >= 20 (N = 6144) pairs at three per CU (5.0 us against 5.3-5.5 for single
+  // rows at two). Fewer rows (q/o, k/v): one batch per wave, of the most rows
+  // that still give every CU a workgroup (N = 4096: four rows, 4.25 us;
+  // N = 1024: one row, 3.1 us).
   // Tuning overrides (benchmark sweeps only), restricted to what is built.
   static const int env_u = env_int("PMI_GEMV_U", 0);
   static const int env_wr = env_int("PMI_GEMV_ROW_WAVES", 0);
@@ -751,10 +756,10 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K) {
   const int64_t cus = device_cus();
   const int64_t rows_per_cu = N / cus;
   bool one_batch = false;
-  if (mt == 1 && c.slice_waves >= 3) { c.rows_per_wave = 4; wpc = 1; }
-  else if (mt == 1 && rows_per_cu >= 96) { c.rows_per_wave = 2; wpc = 3; }
+  if (mt == 1 && c.slices_per_wave == 2) { c.rows_per_wave = 1; wpc = 2; }
+  else if (mt == 1 && c.slice_waves >= 3) { c.rows_per_wave = 4; wpc = 1; }
   else if (mt == 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 1; }
-  else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 1; wpc = 2; }
+  else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 2; wpc = 3; }
   else if (mt > 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 2; }
   else one_batch = true;
   if (one_batch || c.rows_per_wave > max_u) {
