@@ -77,6 +77,17 @@ class Buf:
         self.name, self.w, self.s, self.z, self.perm = name, w, s, z, perm
         self.N, self.K = w.shape[0], w.shape[1] * 2
         self._gm = None
+        self._tiled = None
+
+    def tiled(self):
+        """The tiled weight copy a module builds for 3..32 activation rows
+        (pack.tile_w4a16), where the shape supports it."""
+        import pare_amd as P
+
+        if self._tiled is None and P.tiled_supported(self.N, self.K, GS):
+            self.gm()
+            self._tiled = P.tile_w4a16(self.w, GS)
+        return self._tiled
 
     def gm(self):
         if self._gm is None:
@@ -135,7 +146,8 @@ def launch(L, buf, x, y, M, stream):
                             buf.z.data_ptr(), _lib.PMI_U8,
                             buf.perm.data_ptr() if buf.perm is not None else None,
                             s_gm.data_ptr() if s_gm is not None else None,
-                            z_gm.data_ptr() if z_gm is not None else None, y.data_ptr(),
+                            z_gm.data_ptr() if z_gm is not None else None,
+                            buf._tiled.data_ptr() if buf._tiled is not None else None, y.data_ptr(),
                             _lib.PMI_F16, M, buf.N, buf.K, GS, ws.data_ptr(), ws.numel(), stream)
     if rc != 0:
         raise RuntimeError(_lib.last_error())
@@ -471,6 +483,11 @@ def main():
     for layer in fused + single:
         for b in layer:
             b.gm()
+    # tiled copies of gate_proj/up_proj, which a module builds on its first
+    # forward with 3..32 rows (the C3 sweep and the gate legs)
+    for layer in single:
+        layer[4].tiled()
+        layer[5].tiled()
     torch.cuda.synchronize()
 
     if args.kernel_only:
@@ -490,7 +507,7 @@ def main():
                     gate_loop(stream.cuda_stream, m_rows, 2 * n_layers)
         torch.cuda.synchronize()
         log(f"{args.kernel_only} (M={m_rows}): 5 passes, kernel "
-            f"{P.kernel_choice(m_rows, 14336, 4096, GS)}")
+            f"{P.kernel_choice(m_rows, 14336, 4096, GS, tiled=True)}")
         return
 
     # --- eager vs graph: same outputs -------------------------------------
@@ -568,7 +585,7 @@ def main():
     m64_gbs = layer_bytes(14336, 4096, 64) / (m64_us * 1e-6) / 1e9
     detail["gate_m64"] = {"us": round(m64_us, 2), "TFLOP/s": round(m64_tflops, 1),
                           "mfma_frac": round(m64_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                          "GB/s": round(m64_gbs, 1), "kernel": P.kernel_choice(64, 14336, 4096, GS)}
+                          "GB/s": round(m64_gbs, 1), "kernel": P.kernel_choice(64, 14336, 4096, GS, tiled=True)}
     log(f"  gate M=64: {m64_us:.2f} us {m64_tflops:.1f} TFLOP/s {m64_gbs:.1f} GB/s")
     del gm
 
@@ -582,7 +599,7 @@ def main():
         tfl = 2 * M * 14336 * 4096 / (us * 1e-6) / 1e12
         sweep[M] = {"us": round(us, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
                     "TFLOP/s": round(tfl, 2), "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4),
-                    "kernel": P.kernel_choice(M, 14336, 4096, GS)}
+                    "kernel": P.kernel_choice(M, 14336, 4096, GS, tiled=True)}
         log(f"  sweep gate M={M:3d}: {sweep[M]}")
         del gs_
     detail["gate_sweep"] = sweep
@@ -598,6 +615,9 @@ def main():
         wbytes = N * K // 2
         n_copies = int(min(48, max(8, -(-600_000_000 // wbytes))))  # > 512 MB: beyond the MALL
         bufs = [make_act_order_layer(N, K, 7000 + 100 * qi + c, dev) for c in range(n_copies)]
+        for b in bufs:
+            b.gm()
+            b.tiled()
         xq = torch.randn(16, K, generator=g, device=dev).to(torch.float16)
         yq = torch.empty(16, N, dtype=torch.float16, device=dev)
         torch.cuda.synchronize()
@@ -609,7 +629,7 @@ def main():
             byt = layer_bytes(N, K, M) + 4 * K
             row[f"M{M}"] = {"us": round(us, 2), "GB/s": round(byt / (us * 1e-6) / 1e9, 1),
                             "TFLOP/s": round(2 * M * N * K / (us * 1e-6) / 1e12, 2),
-                            "kernel": P.kernel_choice(M, N, K, GS)}
+                            "kernel": P.kernel_choice(M, N, K, GS, tiled=True)}
             log(f"  qwen act_order {name:8s} {N:6d}x{K:6d} M={M:2d}: {row[f'M{M}']}")
             del gq
         qwen[name] = row

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 9
+#define PMI_ABI_VERSION 10
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -125,6 +125,24 @@ PMI_API int pmi_sz_group_major(const float* scales, const void* zeros, int zero_
                                float* scales_gm, uint8_t* zeros_gm, int32_t* bad_count,
                                int64_t N, int64_t G, void* stream);
 
+/* Bytes of the tiled copy of an [N,K] INT4 weight (64-row panels, N padded to
+ * a multiple of 64): ceil(N/64) * 64 * K/2. Host-only. No reference counterpart. */
+PMI_API size_t pmi_tiled_bytes(int64_t N, int64_t K);
+
+/* Kernel-layout weight (group size group_size, act_order permutation already
+ * applied) -> tiled copy for the tiled-weight GEMM that pmi_matmul_w4a16 runs
+ * for 3..32 activation rows: for every 64-row panel p and 128-column unit u
+ * one 4 KiB block of 4 tiles x 64 lanes x 16 bytes; lane n + 16h of tile j
+ * holds row 64p + 4n + j, and its byte b carries columns 128u + (b < 8 ?
+ * 8h + b : 32 + 8h + b - 8) (low nibble) and that + 64 (high nibble); rows
+ * past N are zero. w_tiled: pmi_tiled_bytes(N, K) bytes, 16-byte aligned;
+ * K % 128 == 0; group_size 32, 64 or a multiple of 128. Built once per layer.
+ * No reference counterpart: a derived per-layer layout, like the kernel-layout
+ * weight the reference caches (pare/layers/linear.py:148-151), laid out so a
+ * wave reads contiguous 1 KiB runs straight into MFMA operands. */
+PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N, int64_t K,
+                           int64_t group_size, void* stream);
+
 /* Y[M,N] = X[M,K] . dequant(W)^T with the dequantisation fused into the
  * matmul. x: fp16 [M,K] row-major, 16-byte aligned; w: kernel layout;
  * zeros: PMI_F32 or PMI_U8 [N,G]; perm (nullable, int32 [K]): act_order
@@ -134,6 +152,10 @@ PMI_API int pmi_sz_group_major(const float* scales, const void* zeros, int zero_
  * copies of scales and zeros; the MFMA GEMM reads them (one contiguous run per
  * group) instead of gathering [N,G] rows when N % 4 == 0. The other kernels
  * read scales and zeros.
+ * w_tiled (nullable): the pmi_tile_w4a16 copy of w. With it (and scales_gm,
+ * zeros_gm) 3..32 activation rows run on the tiled-weight GEMM where that
+ * wins (pmi_matmul_kernel_choice 5); without it those rows take the other
+ * kernels.
  * workspace (nullable when workspace_bytes == 0): device scratch of
  * pmi_matmul_workspace_bytes() bytes, 256-byte aligned, zero-filled before
  * its first use; every call leaves it zero-filled again (it holds split-K
@@ -146,7 +168,7 @@ PMI_API int pmi_sz_group_major(const float* scales, const void* zeros, int zero_
  *           pare/kernels/matmul_int4.py:183-243 (kernel :66-176) */
 PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_dtype, const int32_t* perm,
-                     const float* scales_gm, const uint8_t* zeros_gm, void* y,
+                     const float* scales_gm, const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream);
 
@@ -167,7 +189,8 @@ PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const
 PMI_API int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w,
                                      const float* scales, const void* zeros, int zero_dtype,
                                      const int32_t* perm, const float* scales_gm,
-                                     const uint8_t* zeros_gm, void* y, int y_dtype, int64_t M,
+                                     const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
+                                     int y_dtype, int64_t M,
                                      int64_t N, int64_t K, int64_t group_size, void* stream);
 
 /* y = (silu(gate) * up) . dequant(W)^T for M <= 4, the down projection of a
@@ -273,11 +296,14 @@ PMI_API int pmi_gptq_pack(const uint8_t* codes, const int32_t* inv_perm, uint8_t
 /* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
  * 2 = MFMA GEMM (group_size % 128 == 0 and K % 256 == 0), 3 = skinny MFMA
  * kernel (M <= 16), 4 = register-streamed MFMA GEMM (group_size == 128,
- * K % 512 == 0). Host-only; no reference counterpart (the reference has one
- * Triton kernel). */
-PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size);
+ * K % 512 == 0), 5 = tiled-weight MFMA GEMM (M <= 32, K % 512 == 0,
+ * K >= 1536, N % 4 == 0, group_size 32, 64 or a multiple of 128; needs the
+ * w_tiled copy, so it is chosen only when has_tiled is non-zero). Host-only;
+ * no reference counterpart (the reference has one Triton kernel). */
+PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                     int has_tiled);
 
-/* Forces pmi_matmul_w4a16 onto one kernel (1 to 4 as above; 0 restores the
+/* Forces pmi_matmul_w4a16 onto one kernel (1 to 5 as above; 0 restores the
  * automatic choice) for every thread of the process; returns the previous
  * setting, or PMI_ERR_INVALID for an unknown value. A test and benchmarking
  * hook with no reference counterpart. A forced kernel that cannot run a shape

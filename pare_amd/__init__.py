@@ -17,7 +17,8 @@ from .gptq import HessianAccumulator, gptq_quantize, quantize_linear_gptq
 from .kernels import kernel_available, kernel_choice, matmul_w4a16, triton_available
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .model_io import load_quantized, save_quantized
-from .pack import dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major, zeros_to_u8
+from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
+                   tile_w4a16, tiled_supported, zeros_to_u8)
 from .quant import rtn_quantize
 
 __all__ = [
@@ -25,6 +26,6 @@ __all__ = [
     "export_awq", "gptq_quantize", "HessianAccumulator", "kernel_available", "load_awq",
     "quantize_linear_gptq",
     "kernel_choice", "matmul_w4a16", "perm_from_g_idx", "repack_int4_for_kernel",
-    "load_quantized", "rtn_quantize", "save_quantized", "sz_group_major", "triton_available",
-    "zeros_to_u8",
+    "load_quantized", "rtn_quantize", "save_quantized", "sz_group_major", "tile_w4a16",
+    "tiled_supported", "triton_available", "zeros_to_u8",
 ]

@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -52,14 +52,16 @@ SIGNATURES = {
     "pmi_awq_gemm_to_storage": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "pmi_storage_to_awq_gemm": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                      _vp]),
-    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i64,
-                             _i64, _vp, ctypes.c_size_t, _vp]),
-    "pmi_matmul_w4a16_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64,
-                                      _i64, _i64, _vp]),
+    "pmi_tiled_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "pmi_tile_w4a16": (_i, [_vp, _vp, _i64, _i64, _i64, _vp]),
+    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i64, _i64,
+                             _i64, _i64, _vp, ctypes.c_size_t, _vp]),
+    "pmi_matmul_w4a16_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i64,
+                                      _i64, _i64, _i64, _vp]),
     "pmi_matmul_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i]),
     "pmi_dequant_w4a16": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _vp]),
     "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),
-    "pmi_matmul_kernel_choice": (_i, [_i64, _i64, _i64, _i64]),
+    "pmi_matmul_kernel_choice": (_i, [_i64, _i64, _i64, _i64, _i]),
     "pmi_set_kernel_override": (_i, [_i]),
     "pmi_add_rmsnorm_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "pmi_rope_kv_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -20,7 +20,8 @@ LIB_NAME = "libpare_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
 SOURCES = ["capi.hip", "w4a16_gemv.hip", "w4a16_gemm.hip", "w4a16_gemm64.hip", "w4a16_skinny.hip",
-           "w4a16_layout.hip", "decode_ops.hip", "gptq.hip", "probes.hip"]
+           "w4a16_layout.hip", "decode_ops.hip", "gptq.hip", "probes.hip",
+           "w4a16_tgemm.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

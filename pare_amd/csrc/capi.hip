@@ -150,15 +150,24 @@ int pmi_storage_to_awq_gemm(const uint8_t* packed, const float* scale, const voi
 }
 
 int pmi_set_kernel_override(int kernel) {
-  if (kernel < 0 || kernel > 4)
+  if (kernel < 0 || kernel > 5)
     return fail(PMI_ERR_INVALID, "pmi_set_kernel_override: unknown kernel %d", kernel);
   ok();
   return g_kernel_override.exchange(kernel);
 }
 
-int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size) {
+int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_tiled) {
   const int forced = g_kernel_override.load();
   if (forced) return forced;
+  // The tiled-weight GEMM (a contiguous weight stream, no K split) wins from
+  // 3 activation rows on wherever its workgroups fill the CUs: about one per
+  // CU from N = 3072 (16-row tiles) and no more than one pass over them
+  // (N <= 20480, 64-row tiles), with K <= 8192 (past that its activation
+  // reloads per 16-row tile outweigh the weights). Below 8192 rows the GEMV
+  // keeps M <= 4.
+  if (has_tiled && M >= 3 && pmi::tgemm_supported(M, N, K, group_size) && N >= 3072 &&
+      N <= 20480 && K <= 8192 && !(M <= 4 && N < 8192))
+    return 5;
   // Measured on MI355X (gate/up/down and q/k/v/o shapes): the GEMV wins up to
   // M = 2, and up to M = 4 for N < 8192 with K <= 8192, where the GEMM's K
   // splits cost more than its matrix cores save. With long rows the GEMV's
@@ -239,10 +248,37 @@ int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const void* no
                   fn);
 }
 
+size_t pmi_tiled_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 0;
+  return pmi::tiled_bytes(N, K);
+}
+
+int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N, int64_t K,
+                   int64_t group_size, void* stream) {
+  const char* fn = "pmi_tile_w4a16";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (K % 128 != 0)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: K=%lld must be a multiple of 128", fn, (long long)K);
+  if (group_size != 32 && group_size != 64 && group_size % 128 != 0)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: group_size must be 32, 64 or a multiple of 128 (got %lld)",
+                fn, (long long)group_size);
+  if ((int64_t)pmi::tiled_bytes(N, K) >= (1ll << 31))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: shape too large (N=%lld K=%lld)", fn, (long long)N,
+                (long long)K);
+  if (N == 0) return ok();
+  if (!w_kernel || !w_tiled) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (w_kernel == w_tiled) return fail(PMI_ERR_INVALID, "%s: in-place tiling is not supported", fn);
+  if (!aligned(w_kernel, 16) || !aligned(w_tiled, 16))
+    return fail(PMI_ERR_INVALID, "%s: buffers must be 16-byte aligned", fn);
+  return from_hip(pmi::launch_tile(w_kernel, w_tiled, N, K, group_size, (hipStream_t)stream), fn);
+}
+
 size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
                                   int has_perm) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
-  const int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
+  // the tiled GEMM, when a caller has the tiled copy, needs only the act_order
+  // gather of X, which every kernel's figure below already covers
+  const int choice = pmi_matmul_kernel_choice(M, N, K, group_size, 0);
   if (choice == 2 && pmi::gemm_supported(K, group_size))
     return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
   if (choice == 4 && pmi::gemm64_supported(M, K, group_size)) {
@@ -254,6 +290,10 @@ size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
   // where its rows do not fit LDS (the size is reported either way, so that a
   // caller's workspace covers a forced or fallback launch)
   if ((choice == 1 || choice == 4) && has_perm)
+    return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
+  // choice 3 (skinny) gathers in LDS; a tiled-GEMM launch with perm needs the
+  // gather of X in the workspace
+  if (has_perm && pmi::tgemm_supported(M, N, K, group_size))
     return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
   return 0;
 }
@@ -274,7 +314,7 @@ int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype, f
 
 int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_dtype, const int32_t* perm,
-                     const float* scales_gm, const uint8_t* zeros_gm, void* y,
+                     const float* scales_gm, const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "pmi_matmul_w4a16";
@@ -300,11 +340,37 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     return fail(PMI_ERR_INVALID, "%s: scales_gm and zeros_gm must be 4-byte aligned", fn);
   if (workspace_bytes && (!workspace || !aligned(workspace, 256)))
     return fail(PMI_ERR_INVALID, "%s: workspace must be non-null and 256-byte aligned", fn);
+  if (w_tiled && !aligned(w_tiled, 16))
+    return fail(PMI_ERR_INVALID, "%s: w_tiled must be 16-byte aligned", fn);
 
   hipStream_t s = (hipStream_t)stream;
   const int zu8 = zero_dtype == PMI_U8;
   const int forced = g_kernel_override.load();
-  int choice = pmi_matmul_kernel_choice(M, N, K, group_size);
+  // the tiled GEMM reads the tiled weights and the group-major scale/zero copies
+  const bool has_tiled = w_tiled && scales_gm && zeros_gm && N % 4 == 0;
+  int choice = pmi_matmul_kernel_choice(M, N, K, group_size, has_tiled ? 1 : 0);
+  if (choice == 5) {
+    if (!has_tiled || !pmi::tgemm_supported(M, N, K, group_size))
+      return fail(PMI_ERR_UNSUPPORTED, "%s: the tiled GEMM needs w_tiled, scales_gm and zeros_gm, "
+                  "M <= 32, N %% 4 == 0, K %% 512 == 0, K >= 1536 and group_size 32, 64 or a "
+                  "multiple of 128", fn);
+    const bool gather_fits = workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
+    if (!perm || gather_fits) {
+      // act_order: X[:, perm] is gathered into the workspace first
+      const void* xs = x;
+      if (perm) {
+        void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
+        hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
+        if (e != hipSuccess) return from_hip(e, fn);
+        xs = xg;
+      }
+      return from_hip(pmi::launch_tgemm(xs, w_tiled, scales_gm, zeros_gm, y, M, N, K, group_size, s),
+                      fn);
+    }
+    if (forced) return fail(PMI_ERR_UNSUPPORTED, "%s: forced tiled GEMM with perm needs a "
+                            "workspace of pmi_matmul_workspace_bytes() bytes", fn);
+    choice = pmi_matmul_kernel_choice(M, N, K, group_size, 0);
+  }
   // act_order on the GEMM gathers X[:, perm] into the workspace; without one
   // the automatic choice falls back to the GEMV.
   const bool perm_fits = !perm || !pmi::gemm_supported(K, group_size) ||
@@ -434,7 +500,8 @@ extern "C" {
 
 int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                              const void* zeros, int zero_dtype, const int32_t* perm,
-                             const float* scales_gm, const uint8_t* zeros_gm, void* y,
+                             const float* scales_gm, const uint8_t* zeros_gm,
+                             const uint8_t* w_tiled, void* y,
                              int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                              void* stream) {
   const char* fn = "pmi_matmul_w4a16_noalloc";
@@ -452,7 +519,7 @@ int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w, const
     if (int rc = scratch_ptr(&ws, (hipStream_t)stream, fn)) return rc;
   }
   const int rc = pmi_matmul_w4a16(x, x_dtype, w, scales, zeros, zero_dtype, perm, scales_gm,
-                                  zeros_gm, y, y_dtype, M, N, K, group_size, ws,
+                                  zeros_gm, w_tiled, y, y_dtype, M, N, K, group_size, ws,
                                   need ? kScratchBytes : 0, stream);
   if (rc) {
     // keep the message, name this entry point

@@ -30,6 +30,12 @@ struct GemmConfig {
   size_t ws_perm;   // workspace bytes for X[:, perm] (act_order)
 };
 
+struct TgemmConfig {
+  int mt;    // 16-row activation tiles (1: activations in registers, 2: LDS ring)
+  int ntw;   // 16-row weight tiles per workgroup (4, 2 or 1)
+  int grid;  // workgroups
+};
+
 struct SkinnyConfig {
   int k_waves;         // waves of a workgroup splitting the K groups
   int n_waves;         // waves of a workgroup taking different weight tiles
@@ -189,5 +195,21 @@ hipError_t launch_read_probe(const void* buf, int64_t bytes, int64_t grid, uint3
 
 hipError_t launch_rtn(const void* w, int w_dtype, uint8_t* packed, float* scale, float* zero,
                       int64_t N, int64_t K, int64_t gs, int sym, hipStream_t stream);
+
+}  // namespace pmi
+
+namespace pmi {
+
+// ---- tiled weight layout and its GEMM (w4a16_tgemm.hip) ----------------------
+// Bytes of the tiled copy of an [N, K] INT4 weight: 64-row panels, N padded.
+inline size_t tiled_bytes(int64_t N, int64_t K) { return (size_t)((N + 63) / 64) * 64 * (size_t)(K / 2); }
+// kernel layout (group size gs) -> tiled layout
+hipError_t launch_tile(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N, int64_t K, int64_t gs,
+                       hipStream_t stream);
+bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
+TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K);
+hipError_t launch_tgemm(const void* x, const uint8_t* w_tiled, const float* scales_gm,
+                        const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        hipStream_t stream);
 
 }  // namespace pmi

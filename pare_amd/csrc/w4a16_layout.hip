@@ -320,6 +320,51 @@ __global__ void rtn_kernel(const void* __restrict__ w, uint8_t* __restrict__ pac
   }
 }
 
+// Kernel layout (group size gs) -> tiled layout of the tiled-weight GEMM.
+// Output chunk i (16 bytes) of block (panel p, unit u): tile j = (i / 64) % 4,
+// lane L = i % 64 = n + 16 h, row 64 p + 4 n + j (zero past N); its byte b
+// holds columns c = 128 u + (b < 8 ? 8 h + b : 32 + 8 h + b - 8) in the low
+// nibble and c + 64 in the high nibble. In the kernel layout column k of a row
+// lies in the gs-wide tile starting at k0 = k - k % gs, byte k0 / 2 + k % (gs/2),
+// low nibble for k % gs < gs / 2, high nibble otherwise. One thread per chunk.
+__device__ __forceinline__ uint32_t kernel_nibble(const uint8_t* __restrict__ row, int k, int gs) {
+  const int k0 = k - k % gs, j = k - k0, hg = gs >> 1;
+  const uint8_t b = row[(k0 >> 1) + (j < hg ? j : j - hg)];
+  return j < hg ? (b & 0xFu) : (b >> 4);
+}
+
+__global__ void tile_kernel(const uint8_t* __restrict__ wk, uint8_t* __restrict__ wt, int64_t N,
+                            int64_t K, int gs) {
+  const int64_t U = K >> 7;
+  const int64_t chunks = (N + 63) / 64 * U * 256;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < chunks;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int L = (int)(i & 63), j = (int)((i >> 6) & 3);
+    const int64_t pu = i >> 8;
+    const int64_t u = pu % U, p = pu / U;
+    const int n = L & 15, h = L >> 4;
+    const int64_t row = 64 * p + 4 * n + j;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (row < N) {
+      const uint8_t* src = wk + row * (K >> 1);
+      if (gs == 128) {
+        // the unit is one group: its bytes carry columns c and c + 64 already
+        const uint32_t* a = reinterpret_cast<const uint32_t*>(src + 64 * u + 8 * h);
+        const uint32_t* b = reinterpret_cast<const uint32_t*>(src + 64 * u + 32 + 8 * h);
+        w[0] = a[0], w[1] = a[1], w[2] = b[0], w[3] = b[1];
+      } else {
+#pragma unroll
+        for (int bb = 0; bb < 16; ++bb) {
+          const int c = (int)(128 * u) + (bb < 8 ? 8 * h + bb : 32 + 8 * h + bb - 8);
+          const uint32_t v = kernel_nibble(src, c, gs) | (kernel_nibble(src, c + 64, gs) << 4);
+          w[bb >> 2] |= v << (8 * (bb & 3));
+        }
+      }
+    }
+    reinterpret_cast<u32x4*>(wt)[i] = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
 int grid_for(int64_t work, int per_thread = 1) {
   int64_t blocks = (work / per_thread + kBlock - 1) / kBlock;
   if (blocks < 1) blocks = 1;
@@ -333,6 +378,13 @@ hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* per
                          int64_t K, int64_t gs, hipStream_t stream) {
   hipLaunchKernelGGL(repack_kernel, dim3(grid_for(N * (K / 8))), dim3(kBlock), 0, stream, packed,
                      out, perm, N, K, gs);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N, int64_t K, int64_t gs,
+                       hipStream_t stream) {
+  hipLaunchKernelGGL(tile_kernel, dim3(grid_for((N + 63) / 64 * (K / 128) * 256)), dim3(kBlock), 0,
+                     stream, w_kernel, w_tiled, N, K, (int)gs);
   return hipGetLastError();
 }
 

@@ -1,0 +1,372 @@
+// Tiled-weight MFMA INT4 W4A16 GEMM for 3..32 activation rows, gfx950
+// (v_mfma_f32_16x16x32_f16).
+//
+// Why a tiled copy of the weights. At these row counts the kernel is a weight
+// stream, and how the stream meets the DRAM decides its speed: on MI355X a
+// grid that reads the gate_proj weights (29 MB) as 64-byte pieces of many rows
+// per load (the MFMA operand layout of the row-major kernel layout) moves them
+// in 8.7 us; the same bytes read as contiguous 4 KiB blocks take 6.1 us. The
+// tiled copy (`pmi_tile_w4a16`, built once per layer like the kernel-layout
+// weight) stores, for every 64-row panel p and 128-column unit u, one 4 KiB
+// block that a wave loads with four contiguous 1 KiB loads straight into MFMA
+// operand registers:
+//   block (p, u) = tile j (4) x lane L = n + 16 h (64) x 16 bytes;
+//   lane (n, h) of tile j holds row 64 p + 4 n + j, unit bytes b < 8:
+//   columns 128 u + 8 h + b (low nibble) and + 64 (high nibble); b >= 8:
+//   columns 128 u + 32 + 8 h + (b - 8) and + 64.
+// MFMA k-step t < 4 of a unit then covers columns 128 u + 32 t + [0, 32):
+// steps 0 and 1 take the low nibbles of bytes 0-7 and 8-15, steps 2 and 3 the
+// high nibbles, so every step lies inside one group of 32, 64 or 128 columns
+// and the per-group scale applies after the steps of its group.
+//
+// Work layout. No K split: a workgroup owns NTW 16-row tiles of one panel
+// (16 NTW weight rows) for all activation rows and the whole K range, so no
+// partial tiles cross workgroups. Its four compute waves take the units
+// u = 4 s + w (w = wave) and are added through LDS at the end; the four waves
+// of a workgroup read four consecutive blocks at every step. NTW is the
+// largest of 4, 2, 1 that still gives about a workgroup per CU.
+//
+// Activations. Up to 16 rows (MT = 1) every compute wave loads the A operands
+// of its own units with the weights (16 rows x 256 bytes per unit, L2
+// resident), so the kernel has no LDS staging and no barrier in its loop.
+// 17-32 rows (MT = 2) would need twice the registers; there two producer
+// waves copy the activations of each step (the four units of the four waves)
+// into a four-deep LDS ring with buffer_load ... lds, and all waves cross one
+// s_barrier per step.
+//
+// Pipeline. Each compute wave keeps a three-deep register ring of units
+// (weights, scales, zero points and, for MT = 1, activations): the loads of
+// step s + 2 are issued before step s is computed. The loop runs whole rounds
+// of three steps with no exit inside a round and every load unconditional
+// (past the range it re-reads the last unit), so the compiler waits for
+// exactly the two younger steps; a deeper ring measured slower (more requests
+// in flight per CU spread the DRAM pages).
+//
+// Operands and numerics are those of the MFMA GEMM: B = 8 fp16 (q - z), exact,
+// from v_perm_b32 under a 0x64 exponent byte and one packed subtract; the
+// products x * (q - z) are exact in fp32; per group y += s * sum x*(q - z) in
+// fp32, the reference's w = (q - z) * s with fp32 accumulation
+// (pare/kernels/matmul_int4.py:105-176).
+#include "pmi_common.h"
+#include "pmi_launch.h"
+
+namespace pmi {
+namespace {
+
+constexpr int kKW = 4;     // compute waves (units u = 4 s + w)
+constexpr int kDW = 3;     // register ring depth (steps)
+constexpr int kDX = 4;     // LDS ring depth (steps), MT = 2
+constexpr int kProd = 2;   // activation producer waves, MT = 2
+
+struct TgemmArgs {
+  const f16* x;
+  const uint8_t* wt;    // tiled weights
+  const float* s_gm;    // fp32 [G, N]
+  const uint8_t* z_gm;  // u8 [G, N]
+  f16* y;
+  int M, N, K, gs;
+};
+
+// One unit of a compute wave: activations (MT = 1), weights, and for each of
+// the GPU groups of the unit the NTW scales and zero points of the lane's rows.
+template <int MT, int NTW, int GPU>
+struct Unit {
+  u32x4 xa[MT == 1 ? 4 : 1];
+  u32x4 w[NTW];
+  f32x4 s[GPU];
+  uint32_t z[GPU];
+};
+
+template <int MT, int NTW, int GPU>
+__global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
+  constexpr bool RING = MT > 1;
+  constexpr int BM = 16 * MT;
+  constexpr int XG = BM * 256;   // activation bytes of one unit (RING)
+  constexpr int CPU = BM / 4;    // 1 KiB copies per unit (RING)
+  constexpr int SUBS = 4 / NTW;  // workgroups per panel
+  constexpr int TPG = 4 / GPU;   // MFMA k-steps per group
+  // activation ring (MT = 2), reused after the loop for the partial tiles of
+  // three waves
+  constexpr int kRing = RING ? kKW * kDX * XG : 0;
+  constexpr int kRed = (kKW - 1) * MT * NTW * 64 * 16;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kRing > kRed ? kRing : kRed];
+
+  const int tid = threadIdx.x, l = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int panel = blockIdx.x / SUBS, jb = (blockIdx.x % SUBS) * NTW;
+  const int M = a.M, N = a.N, K = a.K;
+  if (64 * panel + jb >= N) return;  // a padding workgroup past the last rows (uniform)
+  const int U = K >> 7;              // units
+  const int steps = (U + kKW - 1) / kKW;
+  const int ln = l & 15, h = l >> 4;
+  const int row0 = 64 * panel + 4 * ln + jb;  // first of the lane's NTW rows
+
+  f32x4 acc[MT][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (RING && wv >= kKW) {
+    // ---- activation producer p: per step the units 4 s .. 4 s + 3, copy c of
+    // unit k covers rows 4 c + l / 16; LDS chunk l % 16 of a row holds
+    // activation chunk (l % 16) ^ (row % 16)
+    const int p = wv - kKW;
+    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (int64_t)M * K * 2);
+    int vx[CPU];
+#pragma unroll
+    for (int c = 0; c < CPU; ++c) {
+      const int r = 4 * c + (l >> 4);
+      const int mg = r < M ? r : M - 1;
+      vx[c] = mg * K * 2 + 16 * ((l & 15) ^ (r & 15));
+    }
+    constexpr int CPS = kKW * CPU / kProd;  // copies per producer per step
+    static_assert((kDX - 1) * CPS < 64, "copies in flight fit vmcnt");
+    auto issue = [&](int slot, int st) {
+#pragma unroll
+      for (int q = 0; q < CPS; ++q) {
+        const int cc = q * kProd + p;
+        const int k = cc / CPU, c = cc % CPU;
+        int u = kKW * st + k;
+        u = u < U ? u : U - 1;
+        copy_to_lds<16>(rx, lds + (k * kDX + slot) * XG + c * 1024, vx[c],
+                        __builtin_amdgcn_readfirstlane(u * 256));
+      }
+    };
+    for (int d = 0; d < kDX - 1; ++d) issue(d, d);
+    int slot = kDX - 1;
+    for (int s = 0; s < steps; ++s) {
+      wait_vmcnt<(kDX - 2) * CPS>();  // step s has landed
+      barrier_only();                 // ... and every wave is done with step s - 1
+      issue(slot, s + kDX - 1);
+      slot = slot + 1 == kDX ? 0 : slot + 1;
+    }
+    wait_vmcnt<0>();  // clamped copies past the last step
+  } else {
+    // ---- compute wave kw: units u = 4 s + kw
+    const int kw = wv;
+    const int G = K / a.gs;
+    const int rowc = row0 < N ? row0 : N - 4 + jb;  // clamped for the scale/zero loads
+    const __amdgpu_buffer_rsrc_t rw = rsrc(a.wt, (int64_t)((N + 63) / 64) * 64 * (K >> 1));
+    const __amdgpu_buffer_rsrc_t rs = rsrc(a.s_gm, (int64_t)G * N * 4);
+    const __amdgpu_buffer_rsrc_t rz = rsrc(a.z_gm, (int64_t)G * N);
+    const int vw = panel * U * 4096 + 1024 * jb + 16 * l;
+    const int vs = rowc * 4, vz = rowc;
+    // groups per unit (GPU > 1: gs 32 or 64) or units per group (gs >= 128)
+    const int upg = a.gs >= 128 ? a.gs >> 7 : 1;
+    __amdgpu_buffer_rsrc_t rxd;
+    int vxd = 0;
+    if constexpr (MT == 1) {
+      rxd = rsrc(a.x, (int64_t)M * K * 2);
+      const int mg = ln < M ? ln : M - 1;
+      vxd = mg * K * 2 + 16 * h;
+    }
+    auto issue = [&](Unit<MT, NTW, GPU>& un, int s) {
+      int u = kKW * s + kw;
+      u = u < U ? u : U - 1;
+      const int uu = __builtin_amdgcn_readfirstlane(u);
+      if constexpr (MT == 1) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          un.xa[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rxd, vxd, uu * 256 + 64 * t, 0));
+      }
+#pragma unroll
+      for (int j = 0; j < NTW; ++j)
+        un.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw + 1024 * j, uu * 4096, 2));
+#pragma unroll
+      for (int gp = 0; gp < GPU; ++gp) {
+        const int g = GPU > 1 ? uu * GPU + gp : uu / upg;
+        // the vector result is converted as a whole: hipcc 7.2 mis-reads the
+        // lanes of a u32x4 bit-cast element by element to float
+        if constexpr (NTW == 4) {
+          un.s[gp] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vs, g * 4 * N, 0));
+          un.z[gp] = __builtin_amdgcn_raw_buffer_load_b32(rz, vz, g * N, 0);
+        } else if constexpr (NTW == 2) {
+          typedef float f32x2 __attribute__((ext_vector_type(2)));
+          const f32x2 v = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs, g * 4 * N, 0));
+          un.s[gp] = f32x4{v[0], v[1], 0.f, 0.f};
+          un.z[gp] = __builtin_amdgcn_raw_buffer_load_b16(rz, vz, g * N, 0);
+        } else {
+          un.s[gp] = f32x4{__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vs, g * 4 * N, 0)),
+                           0.f, 0.f, 0.f};
+          un.z[gp] = __builtin_amdgcn_raw_buffer_load_b8(rz, vz, g * N, 0);
+        }
+      }
+    };
+    auto compute = [&](const Unit<MT, NTW, GPU>& un, const uint8_t* xb) {
+      const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+      f32x4 cg[MT][NTW];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int gp = t / TPG;
+        const int run = t >> 1, half = t & 1;
+        f16x8 A[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (MT == 1) A[mt] = __builtin_bit_cast(f16x8, un.xa[t]);
+          else A[mt] = *reinterpret_cast<const f16x8*>(xb + (16 * mt + ln) * 256 + (((4 * t + h) ^ ln) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          const f16x2 nz = as_f16x2(neg_magic_zero_x2((un.z[gp] >> (8 * j)) & 0xFFu));
+          const uint32_t w0 = un.w[j][2 * half], w1 = un.w[j][2 * half + 1];
+          const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
+          const uint32_t t1 = (run ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
+          const f16x8 B = b_operand(t0, t1, nz);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B, t % TPG == 0 ? zero4 : cg[mt][j],
+                                                               0, 0, 0);
+        }
+        if (t % TPG == TPG - 1) {
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            const float sc = un.s[gp][j];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(sc, cg[mt][j][i], acc[mt][j][i]);
+          }
+        }
+      }
+    };
+
+    Unit<MT, NTW, GPU> ring[kDW];
+#pragma unroll
+    for (int d = 0; d < kDW - 1; ++d) {
+      issue(ring[d], d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    int xslot = 0;
+    auto step = [&](const Unit<MT, NTW, GPU>& un) {
+      const uint8_t* xb = nullptr;
+      if constexpr (RING) {
+        barrier_only();  // the activations of this step are in LDS
+        xb = lds + (kw * kDX + xslot) * XG;
+        xslot = xslot + 1 == kDX ? 0 : xslot + 1;
+      }
+      compute(un, xb);
+    };
+    // Whole rounds of kDW steps, then a tail already in flight. The host
+    // guarantees steps >= kDW.
+    int s0 = 0;
+    do {
+#pragma unroll
+      for (int d = 0; d < kDW; ++d) {
+        issue(ring[(d + kDW - 1) % kDW], s0 + d + kDW - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        step(ring[d]);
+      }
+      s0 += kDW;
+    } while (s0 + kDW <= steps);
+#pragma unroll
+    for (int d = 0; d < kDW - 1; ++d) {
+      if (s0 + d >= steps) break;
+      step(ring[d]);
+    }
+  }
+
+  // ---- the four waves' partial tiles are added through LDS (a unit past K,
+  // re-read by a clamped load, is never computed: steps * 4 covers U exactly
+  // only when U % 4 == 0, which the host requires)
+  __syncthreads();
+  f32x4* red = reinterpret_cast<f32x4*>(lds);
+  if (wv > 0 && wv < kKW) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) red[(((wv - 1) * MT + mt) * NTW + j) * 64 + l] = acc[mt][j];
+  }
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int k = 1; k < kKW; ++k)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) acc[mt][j] += red[(((k - 1) * MT + mt) * NTW + j) * 64 + l];
+  if (row0 >= N) return;
+  // lane (n, h): rows 16 mt + 4 h + i of the activations, weight rows row0 + j
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * mt + 4 * h + i;
+      if (m >= M) continue;
+      uint16_t v[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(acc[mt][j][i]));
+      f16* dst = a.y + (size_t)m * N + row0;
+      if constexpr (NTW == 4) {
+        *reinterpret_cast<uint2*>(dst) = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16),
+                                               (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
+      } else if constexpr (NTW == 2) {
+        *reinterpret_cast<uint32_t*>(dst) = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+      } else {
+        *reinterpret_cast<uint16_t*>(dst) = v[0];
+      }
+    }
+}
+
+template <int MT, int NTW, int GPU>
+hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU>), dim3(c.grid),
+                     dim3((kKW + (MT == 1 ? 0 : kProd)) * 64), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int MT, int NTW>
+hipError_t launch_gpu(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
+  if (a.gs == 32) return launch_cfg<MT, NTW, 4>(c, a, stream);
+  if (a.gs == 64) return launch_cfg<MT, NTW, 2>(c, a, stream);
+  return launch_cfg<MT, NTW, 1>(c, a, stream);
+}
+
+template <int MT>
+hipError_t launch_mt(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
+  if (c.ntw == 4) return launch_gpu<MT, 4>(c, a, stream);
+  if (c.ntw == 2) return launch_gpu<MT, 2>(c, a, stream);
+  return launch_gpu<MT, 1>(c, a, stream);
+}
+
+}  // namespace
+
+bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
+  // K % 512 == 0: every compute wave gets the same number of units, at least
+  // the ring depth of them (K >= 1536)
+  return M >= 1 && M <= 32 && N % 4 == 0 && K % 512 == 0 && K >= 1536 &&
+         (gs == 32 || gs == 64 || gs % 128 == 0) &&
+         K % gs == 0 && (int64_t)M * K * 2 < (1ll << 31) && ((N + 63) / 64) * 64 * (K / 2) < (1ll << 31);
+}
+
+TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {
+  TgemmConfig c;
+  c.mt = M <= 16 ? 1 : 2;
+  // the most rows per workgroup that still give about one workgroup per CU
+  const int64_t cus = device_cu_count();
+  const int64_t panels = (N + 63) / 64;
+  c.ntw = panels >= (cus * 3) / 4 ? 4 : (2 * panels >= (cus * 3) / 4 ? 2 : 1);
+  c.grid = (int)(panels * (4 / c.ntw));
+  (void)K;
+  return c;
+}
+
+hipError_t launch_tgemm(const void* x, const uint8_t* w_tiled, const float* scales_gm,
+                        const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        hipStream_t stream) {
+  const TgemmConfig c = tgemm_config(M, N, K);
+  TgemmArgs a;
+  a.x = (const f16*)x;
+  a.wt = w_tiled;
+  a.s_gm = scales_gm;
+  a.z_gm = zeros_gm;
+  a.y = (f16*)y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.gs = (int)gs;
+  if (c.mt == 1) return launch_mt<1>(c, a, stream);
+  return launch_mt<2>(c, a, stream);
+}
+
+}  // namespace pmi

@@ -120,6 +120,7 @@ def matmul_w4a16(
     *,
     perm: torch.Tensor | None = None,
     sz_gm: tuple[torch.Tensor, torch.Tensor] | None = None,
+    w_tiled: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Y[M,N] = X[M,K] @ dequant(W)^T with the dequantisation fused (fp16 in, fp16 out).
@@ -133,8 +134,10 @@ def matmul_w4a16(
     Extensions: ``perm`` (int32 [K]) for act_order layers whose weights were
     repacked with the same permutation; ``sz_gm``, the group-major copies of
     scales and zeros from ``pack.sz_group_major`` (fp32 and uint8 [G, N]), which
-    the MFMA GEMM reads as contiguous runs; ``out`` to write into a
-    preallocated [M, N] fp16 tensor.
+    the MFMA GEMM reads as contiguous runs; ``w_tiled``, the ``pack.tile_w4a16``
+    copy of the weights, which (with ``sz_gm``) lets 3..32 activation rows run
+    on the tiled-weight GEMM; ``out`` to write into a preallocated [M, N] fp16
+    tensor.
     Raises RuntimeError when x is not on a HIP device or the library is
     missing; AssertionError on layout violations, like the reference.
     """
@@ -173,6 +176,12 @@ def matmul_w4a16(
         assert z_gm.dtype == torch.uint8 and tuple(z_gm.shape) == (G, N) and z_gm.is_contiguous(), \
             "sz_gm[1] must be a contiguous uint8 [G, N] tensor"
         assert s_gm.device == dev and z_gm.device == dev, "sz_gm must be on x's device"
+    if w_tiled is not None:
+        assert w_tiled.dtype == torch.uint8 and w_tiled.device == dev and w_tiled.is_contiguous(), \
+            "w_tiled must be a contiguous uint8 tensor on x's device"
+        assert w_tiled.numel() == L.pmi_tiled_bytes(N, K), \
+            f"w_tiled must hold pmi_tiled_bytes(N, K)={L.pmi_tiled_bytes(N, K)} bytes"
+        w_tiled = _aligned16(w_tiled)
     if out is None:
         out = torch.empty(M, N, device=dev, dtype=torch.float16)
     else:
@@ -186,7 +195,8 @@ def matmul_w4a16(
             xa.data_ptr(), _lib.PMI_F16, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
             perm.data_ptr() if perm is not None else None,
             s_gm.data_ptr() if s_gm is not None else None,
-            z_gm.data_ptr() if z_gm is not None else None, out.data_ptr(), _lib.PMI_F16,
+            z_gm.data_ptr() if z_gm is not None else None,
+            w_tiled.data_ptr() if w_tiled is not None else None, out.data_ptr(), _lib.PMI_F16,
             M, N, K, group_size, ws.data_ptr() if ws is not None else None,
             ws.numel() if ws is not None else 0, stream), "pmi_matmul_w4a16")
     return out
@@ -261,7 +271,7 @@ def matmul_w4a16_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, norm_we
     return out, h
 
 
-_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4}
+_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4, "tgemm": 5}
 
 
 class force_kernel:
@@ -281,7 +291,8 @@ class force_kernel:
         return False
 
 
-def kernel_choice(M: int, N: int, K: int, group_size: int) -> str:
-    """'gemv', 'gemm', 'skinny' or 'gemm64': the kernel matmul_w4a16 runs for this shape."""
-    c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size)
-    return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64"}[c]
+def kernel_choice(M: int, N: int, K: int, group_size: int, tiled: bool = False) -> str:
+    """'gemv', 'gemm', 'skinny', 'gemm64' or 'tgemm': the kernel matmul_w4a16 runs
+    for this shape (``tiled``: the caller passes the tiled weight copy)."""
+    c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size, int(tiled))
+    return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64", 5: "tgemm"}[c]

@@ -23,6 +23,7 @@ import torch.nn.functional as F
 from .config import QuantConfig, is_int4, kernel_group_size
 from .kernels import matmul_w4a16
 from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
+                   tile_w4a16, tiled_supported,
                    zeros_to_u8)
 
 
@@ -122,6 +123,7 @@ class QuantizedLinear(nn.Module):
         if w_kernel is None:
             w_kernel = repack_int4_for_kernel(self.packed_weight, gs, perm=perm)
         self._packed_weight_kernel = w_kernel
+        self._packed_weight_tiled = None
         zero_u8 = zeros_to_u8(self.zero)
         self._kernel_cache = (self._stamp(), zero_u8, perm, sz_group_major(self.scale, zero_u8))
 
@@ -134,6 +136,17 @@ class QuantizedLinear(nn.Module):
             self._build_kernel_cache(None)
             cache = self._kernel_cache
         return self._packed_weight_kernel, cache[1], cache[2], cache[3]
+
+    def _tiled_buffer(self, w_kernel: torch.Tensor, M: int):
+        """Tiled copy of the kernel-layout weight for the tiled-weight GEMM,
+        built on the first forward with 3..32 rows (decode-only use never
+        pays for it) and kept with the kernel-layout weight."""
+        if not 3 <= M <= 32 or not tiled_supported(self.out_features, self.in_features,
+                                                   self._group_size()):
+            return None
+        if getattr(self, "_packed_weight_tiled", None) is None:
+            self._packed_weight_tiled = tile_w4a16(w_kernel, self._group_size())
+        return self._packed_weight_tiled
 
     def adopt_kernel_layout(self, w_kernel: torch.Tensor) -> None:
         """Uses a stored kernel-layout weight of this layer (the output of
@@ -150,7 +163,9 @@ class QuantizedLinear(nn.Module):
         w_k, zero_u8, perm, sz_gm = self._kernel_buffers()
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
-        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm, sz_gm=sz_gm)
+        w_t = self._tiled_buffer(w_k, x_2d.shape[0])
+        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm, sz_gm=sz_gm,
+                         w_tiled=w_t)
         y = y.to(x.dtype)
         if self.bias is not None:
             y = y + self.bias

@@ -86,6 +86,33 @@ def sz_group_major(scales: torch.Tensor, zeros: torch.Tensor) -> tuple[torch.Ten
     return s_gm, z_gm
 
 
+def tile_w4a16(w_kernel: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Tiled copy (uint8, ``pmi_tiled_bytes(N, K)`` bytes) of a kernel-layout
+    INT4 weight [N, K//2] for the tiled-weight GEMM (``matmul_w4a16(...,
+    w_tiled=...)``): 64-row panels x 128-column units, each a 4 KiB block that
+    a wave reads as four contiguous 1 KiB runs. Built once per layer, like the
+    kernel-layout weight; with act_order, tile the permuted kernel layout."""
+    L = _lib.lib()
+    _require_cuda(w_kernel, "tile_w4a16")
+    assert w_kernel.dtype == torch.uint8 and w_kernel.dim() == 2, "w_kernel must be uint8 [N, K//2]"
+    N, K_half = w_kernel.shape
+    K = K_half * 2
+    w = w_kernel.contiguous()
+    if w.data_ptr() % 16:
+        w = w.clone()
+    out = torch.empty(L.pmi_tiled_bytes(N, K), dtype=torch.uint8, device=w.device)
+    with _DeviceGuard(w.device):
+        _lib.check(L.pmi_tile_w4a16(w.data_ptr(), out.data_ptr(), N, K, group_size,
+                                    _stream_handle(w.device)), "pmi_tile_w4a16")
+    return out
+
+
+def tiled_supported(N: int, K: int, group_size: int) -> bool:
+    """Whether the tiled-weight GEMM can run an [N, K] layer of this group size."""
+    return (N % 4 == 0 and K % 512 == 0 and K >= 1536 and K % group_size == 0
+            and (group_size in (32, 64) or group_size % 128 == 0))
+
+
 _OUT_DTYPES = {torch.float16: _lib.PMI_F16, torch.bfloat16: _lib.PMI_BF16,
                torch.float32: _lib.PMI_F32}
 

@@ -44,47 +44,57 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == _lib.ABI_VERSION == 9
+    assert L.pmi_abi_version() == _lib.ABI_VERSION == 10
 
 
 def test_kernel_choice(L):
+    # the tiled-weight GEMM, for callers that pass the tiled copy
+    assert L.pmi_matmul_kernel_choice(16, 14336, 4096, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(3, 14336, 4096, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128, 1) == 1     # GEMV for N < 8192
+    assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(32, 6144, 4096, 32, 1) == 5
+    assert L.pmi_matmul_kernel_choice(33, 14336, 4096, 128, 1) != 5   # beyond 32 rows
+    assert L.pmi_matmul_kernel_choice(16, 4096, 14336, 128, 1) != 5   # K > 8192
+    assert L.pmi_matmul_kernel_choice(16, 1024, 4096, 128, 1) != 5    # too few workgroups
+    assert L.pmi_matmul_kernel_choice(16, 28672, 4096, 128, 1) != 5   # more than one pass
     # GEMV for M <= 2 (M <= 4 for N < 8192); skinny MFMA kernel up to M = 16 for
     # N <= 8192 while the activations fit the LDS budget; MFMA GEMM otherwise
-    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
-    assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128) == 1
-    assert L.pmi_matmul_kernel_choice(8, 4096, 3072, 128) == 3
-    assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128) == 2   # 64.1 KiB of padded activations
-    assert L.pmi_matmul_kernel_choice(8, 4096, 18944, 128) == 2   # 296 KiB of activations
-    assert L.pmi_matmul_kernel_choice(16, 4096, 4096, 128) == 2   # 128 KiB of activations
-    assert L.pmi_matmul_kernel_choice(4, 4096, 14336, 128) == 2   # long rows: MFMA GEMM
-    assert L.pmi_matmul_kernel_choice(3, 3584, 18944, 128) == 2
-    assert L.pmi_matmul_kernel_choice(4, 6144, 4096, 128) == 1    # GEMV
-    assert L.pmi_matmul_kernel_choice(3, 4096, 8192, 128) == 1
-    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 64) == 1     # group size not % 128
-    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256) == 2
-    assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64) == 1
+    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128, 0) == 1
+    assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128, 0) == 1
+    assert L.pmi_matmul_kernel_choice(8, 4096, 3072, 128, 0) == 3
+    assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128, 0) == 2   # 64.1 KiB of padded activations
+    assert L.pmi_matmul_kernel_choice(8, 4096, 18944, 128, 0) == 2   # 296 KiB of activations
+    assert L.pmi_matmul_kernel_choice(16, 4096, 4096, 128, 0) == 2   # 128 KiB of activations
+    assert L.pmi_matmul_kernel_choice(4, 4096, 14336, 128, 0) == 2   # long rows: MFMA GEMM
+    assert L.pmi_matmul_kernel_choice(3, 3584, 18944, 128, 0) == 2
+    assert L.pmi_matmul_kernel_choice(4, 6144, 4096, 128, 0) == 1    # GEMV
+    assert L.pmi_matmul_kernel_choice(3, 4096, 8192, 128, 0) == 1
+    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 64, 0) == 1     # group size not % 128
+    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 256, 0) == 2
+    assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64, 0) == 1
     # register-streamed GEMM: from M = 128, and at M = 33..64 when its 128-row
     # blocks fill the CUs without a K split (fused gate/up, N = 28672)
-    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128) == 2
-    assert L.pmi_matmul_kernel_choice(64, 28672, 4096, 128) == 4
-    assert L.pmi_matmul_kernel_choice(32, 28672, 4096, 128) == 2
-    assert L.pmi_matmul_kernel_choice(128, 14336, 4096, 128) == 4
-    assert L.pmi_matmul_kernel_choice(512, 4096, 14336, 128) == 4
-    assert L.pmi_matmul_kernel_choice(128, 4096, 4096, 256) == 2   # group size 256: MFMA GEMM
-    assert L.pmi_matmul_kernel_choice(32, 4096, 384, 128) == 1     # odd group count: GEMV
-    assert L.pmi_matmul_kernel_choice(2, 14336, 4096, 128) == 1    # GEMV up to M = 2
-    assert L.pmi_matmul_kernel_choice(3, 14336, 4096, 128) == 2    # large N: GEMM from M = 3
-    assert L.pmi_matmul_kernel_choice(4, 28672, 4096, 128) == 2
-    assert L.pmi_matmul_kernel_choice(4, 28672, 4096, 64) == 1     # no GEMM for gs 64
-    assert L.pmi_matmul_kernel_choice(8, 14336, 2048, 128) == 2    # skinny only for N <= 8192
-    assert L.pmi_matmul_kernel_choice(5, 4096, 2048, 128) == 3
+    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128, 0) == 2
+    assert L.pmi_matmul_kernel_choice(64, 28672, 4096, 128, 0) == 4
+    assert L.pmi_matmul_kernel_choice(32, 28672, 4096, 128, 0) == 2
+    assert L.pmi_matmul_kernel_choice(128, 14336, 4096, 128, 0) == 4
+    assert L.pmi_matmul_kernel_choice(512, 4096, 14336, 128, 0) == 4
+    assert L.pmi_matmul_kernel_choice(128, 4096, 4096, 256, 0) == 2   # group size 256: MFMA GEMM
+    assert L.pmi_matmul_kernel_choice(32, 4096, 384, 128, 0) == 1     # odd group count: GEMV
+    assert L.pmi_matmul_kernel_choice(2, 14336, 4096, 128, 0) == 1    # GEMV up to M = 2
+    assert L.pmi_matmul_kernel_choice(3, 14336, 4096, 128, 0) == 2    # large N: GEMM from M = 3
+    assert L.pmi_matmul_kernel_choice(4, 28672, 4096, 128, 0) == 2
+    assert L.pmi_matmul_kernel_choice(4, 28672, 4096, 64, 0) == 1     # no GEMM for gs 64
+    assert L.pmi_matmul_kernel_choice(8, 14336, 2048, 128, 0) == 2    # skinny only for N <= 8192
+    assert L.pmi_matmul_kernel_choice(5, 4096, 2048, 128, 0) == 3
     assert L.pmi_matmul_workspace_bytes(32, 4096, 384, 128, 0) == 0
 
 
 def test_kernel_override(L):
     try:
         assert L.pmi_set_kernel_override(1) == 0
-        assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
+        assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128, 0) == 1
         assert L.pmi_set_kernel_override(7) == _lib.PMI_ERR_INVALID
         assert "unknown kernel" in _lib.last_error()
         assert L.pmi_set_kernel_override(3) == 1
@@ -93,7 +103,7 @@ def test_kernel_override(L):
         assert "skinny" in _lib.last_error()
     finally:
         L.pmi_set_kernel_override(0)
-    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128) == 1
+    assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128, 0) == 1
 
 
 FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid calls
@@ -101,8 +111,8 @@ FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid
 
 def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.PMI_F32,
         perm=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16, s_gm=None, z_gm=None):
-    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, s_gm, z_gm, y, ydt, M, N, K, gs, None, 0,
-                              None)
+    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, s_gm, z_gm, None, y, ydt, M, N, K, gs,
+                              None, 0, None)
 
 
 @pytest.mark.parametrize("kw,code,msg", [

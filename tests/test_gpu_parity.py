@@ -491,7 +491,7 @@ def test_gemv_act_order_gathered_equals_in_kernel_gather(M):
         for wsp, nb in ((ws.data_ptr(), need), (None, 0)):
             y = torch.empty(M, N, dtype=torch.float16, device=DEV)
             rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
-                                    zu8.data_ptr(), _lib.PMI_U8, pm.data_ptr(), None, None,
+                                    zu8.data_ptr(), _lib.PMI_U8, pm.data_ptr(), None, None, None,
                                     y.data_ptr(), _lib.PMI_F16, M, N, K, gs, wsp, nb, stream)
             assert rc == 0, _lib.last_error()
             outs.append(y)
@@ -553,7 +553,7 @@ def test_gemm_workspace_reused_across_shapes():
             with force_kernel("gemm"):
                 rc = L.pmi_matmul_w4a16(xd.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
                                         zd.data_ptr(), _lib.PMI_U8,
-                                        pm.data_ptr() if pm is not None else None, None, None,
+                                        pm.data_ptr() if pm is not None else None, None, None, None,
                                         y.data_ptr(), _lib.PMI_F16, M, N, K, gs, ws.data_ptr(),
                                         ws.numel(), stream)
             assert rc == 0, _lib.last_error()

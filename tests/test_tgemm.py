@@ -1,0 +1,227 @@
+"""The tiled weight layout and the tiled-weight GEMM (3..32 activation rows).
+
+Layout: pmi_tile_w4a16 is checked byte for byte against a numpy restatement of
+its documented mapping, written from the quantisation codes (not from the
+kernel layout it reads), for every group size it takes and for act_order
+(permuted) weights. GEMM: outputs against the fp32-accumulated oracle at
+rtol = atol = 1e-2 (the bar of the other kernels), across row counts,
+shapes (ragged N included), group sizes, act_order and the module path.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import pare_amd as P
+from oracle import pare_oracle as O
+from pare_amd import _lib
+from pare_amd.kernels import force_kernel
+
+DEV = "cuda"
+RTOL = ATOL = 1e-2
+
+
+def tiled_from_codes(q: np.ndarray) -> np.ndarray:
+    """Tiled bytes of INT4 codes q (uint8 [N, K], values 0..15): block (panel p,
+    unit u) is 4 tiles x 64 lanes x 16 bytes; lane n + 16 h of tile j holds row
+    64 p + 4 n + j, byte b < 8 columns 128 u + 8 h + b (low nibble) and + 64
+    (high nibble), byte b >= 8 columns 128 u + 32 + 8 h + (b - 8) and + 64;
+    rows past N are zero."""
+    N, K = q.shape
+    P_, U = (N + 63) // 64, K // 128
+    qp = np.zeros((P_ * 64, K), dtype=np.uint8)
+    qp[:N] = q
+    out = np.zeros((P_, U, 4, 4, 16, 16), dtype=np.uint8)  # p, u, j, h, n, b
+    b = np.arange(16)
+    for h in range(4):
+        cols = np.where(b < 8, 8 * h + b, 32 + 8 * h + (b - 8))  # [16] within a unit
+        for j in range(4):
+            rows = np.arange(P_)[:, None] * 64 + 4 * np.arange(16)[None, :] + j  # [P, 16]
+            for u in range(U):
+                lo = qp[rows][:, :, 128 * u + cols]        # [P, 16(n), 16(b)]
+                hi = qp[rows][:, :, 128 * u + cols + 64]
+                out[:, u, j, h] = lo | (hi << 4)
+    return out.reshape(-1)
+
+
+def codes_storage(packed: np.ndarray) -> np.ndarray:
+    """INT4 codes [N, K] of a storage-layout (pack_int4) weight."""
+    return O.unpack_int4(packed)
+
+
+def _cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _layer(N, K, gs, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy().astype(np.float32)
+    return O.rtn_quantize(w, gs)
+
+
+# ---- CPU: the restatement itself ------------------------------------------------
+
+def test_tiled_restatement_places_every_code_once():
+    """Brute force on a small layer: each code appears exactly once, in the
+    slot the documented formula names (found by searching the tiled bytes for a
+    marker)."""
+    N, K = 70, 256
+    q = np.zeros((N, K), dtype=np.uint8)
+    t = tiled_from_codes(q)
+    assert t.size == ((N + 63) // 64) * 64 * K // 2
+    for row, col in [(0, 0), (5, 9), (63, 127), (64, 128), (69, 255), (17, 70), (2, 200)]:
+        q[:] = 0
+        q[row, col] = 7
+        t = tiled_from_codes(q)
+        nz = np.flatnonzero(t)
+        assert nz.size == 1
+        byte = t[nz[0]]
+        hi = col % 128 >= 64
+        assert byte == (7 << 4 if hi else 7)
+        i = nz[0]
+        b, L = i % 16, (i // 16) % 64
+        j, pu = (i // 1024) % 4, i // 4096
+        u, p = pu % (K // 128), pu // (K // 128)
+        n, h = L % 16, L // 16
+        assert row == 64 * p + 4 * n + j
+        c = col % 128 - (64 if hi else 0)
+        assert c == (8 * h + b if b < 8 else 32 + 8 * h + b - 8)
+        assert col // 128 == u
+
+
+
+# ---- GPU: layout -----------------------------------------------------------------
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,gs", [(64, 512, 128), (200, 1024, 32), (130, 1536, 64),
+                                    (256, 2048, 256), (96, 512, 512), (4096, 4096, 128)])
+def test_tile_bitexact(N, K, gs):
+    packed, s, z = _layer(N, K, gs, seed=N + K)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs)
+    wt = P.tile_w4a16(wk, gs).cpu().numpy()
+    assert np.array_equal(wt, tiled_from_codes(codes_storage(packed)))
+
+
+@pytest.mark.gpu
+def test_tile_act_order_bitexact():
+    N, K, gs = 128, 1024, 128
+    packed, s, z = _layer(N, K, gs, seed=5)
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=perm.to(DEV))
+    wt = P.tile_w4a16(wk, gs).cpu().numpy()
+    q = codes_storage(packed)[:, perm.numpy()]
+    assert np.array_equal(wt, tiled_from_codes(q))
+
+
+@pytest.mark.gpu
+def test_tile_rejects():
+    L = _lib.lib()
+    assert L.pmi_tile_w4a16(0x10000, 0x20000, 64, 200, 100, None) != 0  # K % gs
+    assert L.pmi_tile_w4a16(0x10000, 0x20000, 64, 320, 160, None) != 0  # gs 160
+    assert L.pmi_tile_w4a16(0x10000, 0x20000, 64, 192, 64, None) != 0   # K % 128
+    assert L.pmi_tiled_bytes(70, 256) == 128 * 128
+
+
+# ---- GPU: GEMM ---------------------------------------------------------------------
+
+def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False):
+    if act_order:
+        g0 = torch.Generator().manual_seed(seed)
+        w = (torch.randn(N, K, generator=g0) * 0.02).numpy().astype(np.float32)
+        packed, s, z, g_idx = O.rtn_quantize_act_order(w, np.random.default_rng(seed).permutation(K), gs)
+        perm = P.perm_from_g_idx(_cuda(g_idx), gs)
+        wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=perm)
+        ref_w = O.dequantize_gidx(O.unpack_int4(packed), s, z, g_idx)
+    else:
+        packed, s, z = _layer(N, K, gs, seed)
+        perm = None
+        wk = P.repack_int4_for_kernel(_cuda(packed), gs)
+        ref_w = O.dequantize_packed(packed, s, z)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    sz = P.sz_group_major(_cuda(s), zu8)
+    wt = P.tile_w4a16(wk, gs)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(M, K, generator=g).to(torch.float16)
+    with force_kernel(kernel):
+        y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt, perm=perm)
+    torch.cuda.synchronize()
+    ref = O.linear_fp32(x.float().numpy(), ref_w)
+    yy = y.float().cpu().numpy()
+    err = np.abs(yy - ref)
+    print(f"[parity] tgemm M={M} N={N} K={K} gs={gs} act_order={act_order}: "
+          f"max_abs={err.max():.3e}", flush=True)
+    assert np.isfinite(yy).all()
+    assert (err <= ATOL + RTOL * np.abs(ref)).all(), f"max_abs={err.max():.4e}"
+    return y
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 16, 17, 24, 32])
+def test_tgemm_rows(M):
+    _tgemm_case(M, 1024, 2048, 128, seed=10 + M)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 4096), (6144, 4096), (3584, 3584),
+                                 (1028, 1536), (200, 2560), (4100, 2048)])
+@pytest.mark.parametrize("M", [4, 16, 32])
+def test_tgemm_shapes(M, N, K):
+    _tgemm_case(M, N, K, 128, seed=N % 97 + M)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gs", [32, 64, 256, "channel"])
+@pytest.mark.parametrize("M", [5, 20])
+def test_tgemm_group_sizes(gs, M):
+    K = 2048
+    _tgemm_case(M, 2048, K, K if gs == "channel" else gs, seed=7 + M)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [3, 16, 29])
+def test_tgemm_act_order(M):
+    _tgemm_case(M, 3584, 3584, 128, seed=40 + M, act_order=True)
+
+
+@pytest.mark.gpu
+def test_tgemm_automatic_dispatch_and_determinism():
+    """Gate_proj at 16 rows with the tiled copy runs on the tiled GEMM by
+    itself, gives the same bits on every call, and agrees with the MFMA GEMM
+    within the parity bar."""
+    assert P.kernel_choice(16, 14336, 4096, 128, tiled=True) == "tgemm"
+    assert P.kernel_choice(16, 14336, 4096, 128) != "tgemm"
+    y0 = _tgemm_case(16, 14336, 4096, 128, seed=3, kernel="auto")
+    y1 = _tgemm_case(16, 14336, 4096, 128, seed=3, kernel="auto")
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    y2 = _tgemm_case(16, 14336, 4096, 128, seed=3, kernel="gemm")
+    assert torch.allclose(y0.float(), y2.float(), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+def test_tgemm_needs_tiled_copy_when_forced():
+    N, K, gs = 1024, 2048, 128
+    packed, s, z = _layer(N, K, gs, 1)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs)
+    x = torch.randn(8, K, device=DEV, dtype=torch.float16)
+    with force_kernel("tgemm"), pytest.raises(RuntimeError, match="tiled GEMM"):
+        P.matmul_w4a16(x, wk, _cuda(s), P.zeros_to_u8(_cuda(z)), gs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [2, 16, 32])
+def test_module_builds_tiled_copy(rows):
+    """QuantizedLinear builds the tiled copy on its first 3..32-row forward
+    and matches its own dequant path."""
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(4096, 6144, bias=False).half()
+    q = P.QuantizedLinear.from_linear(lin.to(DEV), P.QuantConfig()).to(DEV)
+    q.use_kernel = True
+    x = torch.randn(rows, 4096, device=DEV, dtype=torch.float16)
+    y = q(x)
+    assert (getattr(q, "_packed_weight_tiled", None) is not None) == (rows >= 3)
+    q.use_kernel = False
+    ref = q(x)
+    torch.cuda.synchronize()
+    assert torch.allclose(y.float(), ref.float(), rtol=RTOL, atol=ATOL)
