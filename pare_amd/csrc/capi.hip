@@ -159,14 +159,18 @@ int pmi_set_kernel_override(int kernel) {
 int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_tiled) {
   const int forced = g_kernel_override.load();
   if (forced) return forced;
-  // The tiled-weight GEMM (a contiguous weight stream, no K split) wins from
-  // 3 activation rows on wherever its workgroups fill the CUs: about one per
-  // CU from N = 3072 (16-row tiles) and no more than one pass over them
-  // (N <= 20480, 64-row tiles), with K <= 8192 (past that its activation
-  // reloads per 16-row tile outweigh the weights). Below 8192 rows the GEMV
-  // keeps M <= 4.
-  if (has_tiled && M >= 3 && pmi::tgemm_supported(M, N, K, group_size) && N >= 3072 &&
-      N <= 20480 && K <= 8192 && !(M <= 4 && N < 8192))
+  // The tiled-weight GEMM (a contiguous weight stream, no K split), measured
+  // on MI355X against the GEMV, skinny kernel and MFMA GEMM: it wins from 3
+  // activation rows up to 32 wherever its workgroups fill the CUs, i.e. from
+  // N = 3072 (16-row tiles) with K <= 8192 (past that its activation reloads
+  // per 16-row tile outweigh the weights). Past one pass over the CUs
+  // (N > 20480) it still wins up to 12 rows (fused gate/up at M = 8: 15.5
+  // against 17.5 us), not at 16-32. At 33-64 rows (two activation blocks)
+  // it loses to the MFMA GEMM (gate at M = 64: 19.6 against 16.4 us). At 2
+  // rows it beats the GEMV for 8192 <= N <= 20480 (gate: 8.1 against 9.3 us),
+  // not for narrower or wider layers.
+  if (has_tiled && M >= 2 && M <= 32 && pmi::tgemm_supported(M, N, K, group_size) && N >= 3072 &&
+      K <= 8192 && (N <= 20480 || M <= 12) && (M >= 3 || (N >= 8192 && N <= 20480)))
     return 5;
   // Measured on MI355X (gate/up/down and q/k/v/o shapes): the GEMV wins up to
   // M = 2, and up to M = 4 for N < 8192 with K <= 8192, where the GEMM's K

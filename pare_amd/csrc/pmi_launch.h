@@ -31,9 +31,11 @@ struct GemmConfig {
 };
 
 struct TgemmConfig {
-  int mt;    // 16-row activation tiles (1: activations in registers, 2: LDS ring)
-  int ntw;   // 16-row weight tiles per workgroup (4, 2 or 1)
-  int grid;  // workgroups
+  int mt;      // 16-row activation tiles (1: activations in registers, 2: LDS ring)
+  int ntw;     // 16-row weight tiles per workgroup (4, 2 or 1)
+  int n_wg;    // weight workgroups
+  int grid_m;  // activation blocks
+  int grid;    // workgroups
 };
 
 struct SkinnyConfig {

@@ -47,6 +47,8 @@
 // products x * (q - z) are exact in fp32; per group y += s * sum x*(q - z) in
 // fp32, the reference's w = (q - z) * s with fp32 accumulation
 // (pare/kernels/matmul_int4.py:105-176).
+#include <stdlib.h>
+
 #include "pmi_common.h"
 #include "pmi_launch.h"
 
@@ -65,6 +67,8 @@ struct TgemmArgs {
   const uint8_t* z_gm;  // u8 [G, N]
   f16* y;
   int M, N, K, gs;
+  int n_wg;    // weight workgroups (16 NTW rows each)
+  int grid_m;  // activation blocks of 16 MT rows
 };
 
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
@@ -93,9 +97,22 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int panel = blockIdx.x / SUBS, jb = (blockIdx.x % SUBS) * NTW;
+  // (weight workgroup, activation block). Workgroups are dealt to the 8 XCDs
+  // round-robin by index, so the activation blocks of one weight workgroup
+  // are numbered 8 apart: they share an XCD, and the second read of its
+  // weights mostly hits that XCD's L2 (a placement preference only).
+  int wg = blockIdx.x, mb = 0;
+  if (a.grid_m > 1) {
+    const int span = 8 * a.grid_m;
+    const int q = blockIdx.x / span, r = blockIdx.x % span;
+    wg = 8 * q + (r & 7);
+    mb = r >> 3;
+  }
+  const int panel = wg / SUBS, jb = (wg % SUBS) * NTW;
   const int M = a.M, N = a.N, K = a.K;
-  if (64 * panel + jb >= N) return;  // a padding workgroup past the last rows (uniform)
+  // padding workgroups: past the weight workgroups, or past the last rows (uniform)
+  if (wg >= a.n_wg || 64 * panel + jb >= N) return;
+  const int m0 = mb * BM;  // first activation row of this block
   const int U = K >> 7;              // units
   const int steps = (U + kKW - 1) / kKW;
   const int ln = l & 15, h = l >> 4;
@@ -117,7 +134,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 #pragma unroll
     for (int c = 0; c < CPU; ++c) {
       const int r = 4 * c + (l >> 4);
-      const int mg = r < M ? r : M - 1;
+      const int mg = m0 + r < M ? m0 + r : M - 1;
       vx[c] = mg * K * 2 + 16 * ((l & 15) ^ (r & 15));
     }
     constexpr int CPS = kKW * CPU / kProd;  // copies per producer per step
@@ -158,7 +175,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     int vxd = 0;
     if constexpr (MT == 1) {
       rxd = rsrc(a.x, (int64_t)M * K * 2);
-      const int mg = ln < M ? ln : M - 1;
+      const int mg = m0 + ln < M ? m0 + ln : M - 1;
       vxd = mg * K * 2 + 16 * h;
     }
     auto issue = [&](Unit<MT, NTW, GPU>& un, int s) {
@@ -291,7 +308,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int m = 16 * mt + 4 * h + i;
+      const int m = m0 + 16 * mt + 4 * h + i;
       if (m >= M) continue;
       uint16_t v[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -334,7 +351,7 @@ hipError_t launch_mt(const TgemmConfig& c, const TgemmArgs& a, hipStream_t strea
 bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
   // K % 512 == 0: every compute wave gets the same number of units, at least
   // the ring depth of them (K >= 1536)
-  return M >= 1 && M <= 32 && N % 4 == 0 && K % 512 == 0 && K >= 1536 &&
+  return M >= 1 && M <= 64 && N % 4 == 0 && K % 512 == 0 && K >= 1536 &&
          (gs == 32 || gs == 64 || gs % 128 == 0) &&
          K % gs == 0 && (int64_t)M * K * 2 < (1ll << 31) && ((N + 63) / 64) * 64 * (K / 2) < (1ll << 31);
 }
@@ -346,7 +363,12 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {
   const int64_t cus = device_cu_count();
   const int64_t panels = (N + 63) / 64;
   c.ntw = panels >= (cus * 3) / 4 ? 4 : (2 * panels >= (cus * 3) / 4 ? 2 : 1);
-  c.grid = (int)(panels * (4 / c.ntw));
+  // tuning override (benchmark sweeps only)
+  static const int env_ntw = [] { const char* e = getenv("PMI_TGEMM_NTW"); return e ? atoi(e) : 0; }();
+  if (env_ntw == 1 || env_ntw == 2 || env_ntw == 4) c.ntw = env_ntw;
+  c.n_wg = (int)(panels * (4 / c.ntw));
+  c.grid_m = (int)((M + 16 * c.mt - 1) / (16 * c.mt));
+  c.grid = c.grid_m == 1 ? c.n_wg : (int)((c.n_wg + 7) / 8 * 8 * c.grid_m);
   (void)K;
   return c;
 }
@@ -365,6 +387,8 @@ hipError_t launch_tgemm(const void* x, const uint8_t* w_tiled, const float* scal
   a.N = (int)N;
   a.K = (int)K;
   a.gs = (int)gs;
+  a.n_wg = c.n_wg;
+  a.grid_m = c.grid_m;
   if (c.mt == 1) return launch_mt<1>(c, a, stream);
   return launch_mt<2>(c, a, stream);
 }

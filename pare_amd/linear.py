@@ -21,7 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .config import QuantConfig, is_int4, kernel_group_size
-from .kernels import matmul_w4a16
+from .kernels import kernel_choice, matmul_w4a16
 from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
                    tile_w4a16, tiled_supported,
                    zeros_to_u8)
@@ -139,12 +139,14 @@ class QuantizedLinear(nn.Module):
 
     def _tiled_buffer(self, w_kernel: torch.Tensor, M: int):
         """Tiled copy of the kernel-layout weight for the tiled-weight GEMM,
-        built on the first forward with 3..32 rows (decode-only use never
-        pays for it) and kept with the kernel-layout weight."""
-        if not 3 <= M <= 32 or not tiled_supported(self.out_features, self.in_features,
-                                                   self._group_size()):
-            return None
+        built on the first forward whose row count runs on it (decode-only use
+        at one row never pays for it) and kept with the kernel-layout weight."""
         if getattr(self, "_packed_weight_tiled", None) is None:
+            if not tiled_supported(self.out_features, self.in_features, self._group_size()):
+                return None
+            if kernel_choice(M, self.out_features, self.in_features, self._group_size(),
+                             tiled=True) != "tgemm":
+                return None
             self._packed_weight_tiled = tile_w4a16(w_kernel, self._group_size())
         return self._packed_weight_tiled
 

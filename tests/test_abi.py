@@ -51,13 +51,18 @@ def test_kernel_choice(L):
     # the tiled-weight GEMM, for callers that pass the tiled copy
     assert L.pmi_matmul_kernel_choice(16, 14336, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(3, 14336, 4096, 128, 1) == 5
-    assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128, 1) == 1     # GEMV for N < 8192
+    assert L.pmi_matmul_kernel_choice(4, 4096, 4096, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(2, 14336, 4096, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(2, 6144, 4096, 128, 1) == 1     # GEMV at 2 rows below N = 8192
+    assert L.pmi_matmul_kernel_choice(1, 14336, 4096, 128, 1) == 1    # GEMV at 1 row
+    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128, 1) == 2   # MFMA GEMM past 32 rows
+    assert L.pmi_matmul_kernel_choice(8, 28672, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(32, 6144, 4096, 32, 1) == 5
     assert L.pmi_matmul_kernel_choice(33, 14336, 4096, 128, 1) != 5   # beyond 32 rows
     assert L.pmi_matmul_kernel_choice(16, 4096, 14336, 128, 1) != 5   # K > 8192
     assert L.pmi_matmul_kernel_choice(16, 1024, 4096, 128, 1) != 5    # too few workgroups
-    assert L.pmi_matmul_kernel_choice(16, 28672, 4096, 128, 1) != 5   # more than one pass
+    assert L.pmi_matmul_kernel_choice(16, 28672, 4096, 128, 1) != 5   # more than one pass at 16 rows
     # GEMV for M <= 2 (M <= 4 for N < 8192); skinny MFMA kernel up to M = 16 for
     # N <= 8192 while the activations fit the LDS budget; MFMA GEMM otherwise
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128, 0) == 1

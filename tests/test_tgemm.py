@@ -212,8 +212,9 @@ def test_tgemm_needs_tiled_copy_when_forced():
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows", [2, 16, 32])
 def test_module_builds_tiled_copy(rows):
-    """QuantizedLinear builds the tiled copy on its first 3..32-row forward
-    and matches its own dequant path."""
+    """QuantizedLinear builds the tiled copy on its first forward whose row
+    count runs on the tiled GEMM (not at 2 rows for N = 6144) and matches its
+    own dequant path."""
     torch.manual_seed(0)
     lin = torch.nn.Linear(4096, 6144, bias=False).half()
     q = P.QuantizedLinear.from_linear(lin.to(DEV), P.QuantConfig()).to(DEV)
