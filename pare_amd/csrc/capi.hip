@@ -172,6 +172,12 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   if (has_tiled && M >= 2 && M <= 32 && pmi::tgemm_supported(M, N, K, group_size) && N >= 3072 &&
       K <= 8192 && (N <= 20480 || M <= 12) && (M >= 3 || (N >= 8192 && N <= 20480)))
     return 5;
+  // Group sizes 32 and 64 have no other matrix-core kernel: past 4 rows the
+  // tiled GEMM (one activation block of 32 rows after another) replaces the
+  // GEMV, which would stream the weights once per 4 rows.
+  if (has_tiled && M > 4 && !pmi::gemm_supported(K, group_size) &&
+      pmi::tgemm_supported(M, N, K, group_size))
+    return 5;
   // Measured on MI355X (gate/up/down and q/k/v/o shapes): the GEMV wins up to
   // M = 2, and up to M = 4 for N < 8192 with K <= 8192, where the GEMM's K
   // splits cost more than its matrix cores save. With long rows the GEMV's

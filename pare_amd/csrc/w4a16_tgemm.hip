@@ -351,9 +351,10 @@ hipError_t launch_mt(const TgemmConfig& c, const TgemmArgs& a, hipStream_t strea
 bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
   // K % 512 == 0: every compute wave gets the same number of units, at least
   // the ring depth of them (K >= 1536)
-  return M >= 1 && M <= 64 && N % 4 == 0 && K % 512 == 0 && K >= 1536 &&
+  return M >= 1 && N % 4 == 0 && K % 512 == 0 && K >= 1536 &&
          (gs == 32 || gs == 64 || gs % 128 == 0) &&
-         K % gs == 0 && (int64_t)M * K * 2 < (1ll << 31) && ((N + 63) / 64) * 64 * (K / 2) < (1ll << 31);
+         K % gs == 0 && (int64_t)M * K * 2 < (1ll << 31) && ((N + 63) / 64) * 64 * (K / 2) < (1ll << 31) &&
+         ((N + 63) / 64 * 4 + 8) * ((M + 15) / 16) < (1ll << 31);  // workgroups
 }
 
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {

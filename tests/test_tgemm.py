@@ -180,6 +180,16 @@ def test_tgemm_group_sizes(gs, M):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("gs", [32, 64])
+@pytest.mark.parametrize("M", [33, 64, 100])
+def test_tgemm_small_groups_many_rows(gs, M):
+    """Group sizes 32 and 64 past 32 rows: activation blocks of 32 rows, chosen
+    automatically when the tiled copy is there."""
+    assert P.kernel_choice(M, 4096, 4096, gs, tiled=True) == "tgemm"
+    _tgemm_case(M, 4096, 4096, gs, seed=M + gs, kernel="auto")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("M", [3, 16, 29])
 def test_tgemm_act_order(M):
     _tgemm_case(M, 3584, 3584, 128, seed=40 + M, act_order=True)
