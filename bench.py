@@ -131,6 +131,7 @@ WORKSPACE = []  # one zero-filled scratch buffer shared by every (stream-ordered
 
 
 M_MAX = 128  # largest activation row count any leg launches
+SWEEP_M = (1, 2, 4, 8, 16, 32, 64, 128)  # configs[2]: gate_proj at these row counts
 
 
 def launch(L, buf, x, y, M, stream):
@@ -387,7 +388,7 @@ def main():
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only",
-                    choices=["gate_up_m1", "gate_m64", "gate", "read_floor", "copy", "e2e_bs1",
+                    choices=["gate_up_m1", "gate_m64", "gate", "sweep", "read_floor", "copy", "e2e_bs1",
                              "e2e_bs4"],
                     default=None,
                     help="run only one kernel loop (for rocprofv3 counter passes): gate_up_m1 "
@@ -490,8 +491,19 @@ def main():
         layer[5].tiled()
     torch.cuda.synchronize()
 
+    if args.kernel_only == "sweep":
+        # the C3 sweep for counter passes: 5 x 64 gate/up launches per row count,
+        # in the order of SWEEP_M (each block of 320 matmul dispatches is one M)
+        with torch.cuda.stream(stream):
+            for M in SWEEP_M:
+                for _ in range(5):
+                    gate_loop(stream.cuda_stream, M, 2 * n_layers)
+                torch.cuda.synchronize()
+                log(f"sweep M={M}: 320 launches, kernel {P.kernel_choice(M, 14336, 4096, GS, tiled=True)}")
+        return
+
     if args.kernel_only:
-        m_rows = 64 if args.kernel_only == "gate_m64" else args.m
+        m_rows = {"gate_m64": 64, "gate_up_m1": 1}.get(args.kernel_only, args.m)
         assert 1 <= m_rows <= M_MAX, f"--m must be in 1..{M_MAX}"
         sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
         n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -591,7 +603,7 @@ def main():
 
     # --- config 3: gate_proj at M = 1 .. 128, automatic dispatch -------------
     sweep = {}
-    for M in (1, 2, 4, 8, 16, 32, 64, M_MAX):
+    for M in SWEEP_M:
         gs_ = capture(lambda s, M=M: gate_loop(s, M, copies), stream)
         gs_.replay()
         us = time_graph(gs_, 5, stream) * 1e3 / copies
