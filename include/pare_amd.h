@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 10
+#define PMI_ABI_VERSION 11
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -293,15 +293,23 @@ PMI_API int pmi_gptq_block(const float* w, const float* c, const int32_t* colg,
 PMI_API int pmi_gptq_pack(const uint8_t* codes, const int32_t* inv_perm, uint8_t* packed,
                           int64_t N, int64_t K, void* stream);
 
+/* Flags of pmi_matmul_kernel_choice: the call passes the tiled copy (with
+ * scales_gm and zeros_gm), and an act_order perm. */
+#define PMI_CHOICE_TILED 1
+#define PMI_CHOICE_PERM  2
+
 /* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
  * 2 = MFMA GEMM (group_size % 128 == 0 and K % 256 == 0), 3 = skinny MFMA
  * kernel (M <= 16), 4 = register-streamed MFMA GEMM (group_size == 128,
  * K % 512 == 0), 5 = tiled-weight MFMA GEMM (M <= 32, K % 512 == 0,
  * K >= 1536, N % 4 == 0, group_size 32, 64 or a multiple of 128; needs the
- * w_tiled copy, so it is chosen only when has_tiled is non-zero). Host-only;
- * no reference counterpart (the reference has one Triton kernel). */
+ * w_tiled copy, so it is chosen only with PMI_CHOICE_TILED in flags; with
+ * PMI_CHOICE_PERM as well, up to 16 rows it gathers X[:, perm] itself when
+ * M (2K + 16) + 4K bytes fit its LDS, which widens where it wins). flags 0
+ * and 1 keep the meaning of the former has_tiled argument. Host-only; no
+ * reference counterpart (the reference has one Triton kernel). */
 PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size,
-                                     int has_tiled);
+                                     int flags);
 
 /* Forces pmi_matmul_w4a16 onto one kernel (1 to 5 as above; 0 restores the
  * automatic choice) for every thread of the process; returns the previous

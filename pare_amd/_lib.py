@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -23,6 +23,7 @@ PMI_ERR_HIP = -3
 PMI_ERR_NO_DEVICE = -4
 
 PMI_F16, PMI_BF16, PMI_F32, PMI_U8 = 0, 1, 2, 3
+PMI_CHOICE_TILED, PMI_CHOICE_PERM = 1, 2
 PMI_LAYOUT_STORAGE, PMI_LAYOUT_KERNEL = 0, 1
 
 _ERR_NAMES = {

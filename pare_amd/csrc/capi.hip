@@ -156,22 +156,32 @@ int pmi_set_kernel_override(int kernel) {
   return g_kernel_override.exchange(kernel);
 }
 
-int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_tiled) {
+int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size, int flags) {
   const int forced = g_kernel_override.load();
   if (forced) return forced;
+  const bool has_tiled = flags & PMI_CHOICE_TILED, has_perm = flags & PMI_CHOICE_PERM;
   // The tiled-weight GEMM (a contiguous weight stream, no K split), measured
-  // on MI355X against the GEMV, skinny kernel and MFMA GEMM: it wins from 3
-  // activation rows up to 32 wherever its workgroups fill the CUs, i.e. from
-  // N = 3072 (16-row tiles) with K <= 8192 (past that its activation reloads
-  // per 16-row tile outweigh the weights). Past one pass over the CUs
-  // (N > 20480) it still wins up to 12 rows (fused gate/up at M = 8: 15.5
-  // against 17.5 us), not at 16-32. At 33-64 rows (two activation blocks)
-  // it loses to the MFMA GEMM (gate at M = 64: 19.6 against 16.4 us). At 2
-  // rows it beats the GEMV for 8192 <= N <= 20480 (gate: 8.1 against 9.3 us),
-  // not for narrower or wider layers.
-  if (has_tiled && M >= 2 && M <= 32 && pmi::tgemm_supported(M, N, K, group_size) && N >= 3072 &&
-      K <= 8192 && (N <= 20480 || M <= 12) && (M >= 3 || (N >= 8192 && N <= 20480)))
-    return 5;
+  // on MI355X against the GEMV, skinny kernel and MFMA GEMM over 8-48 weight
+  // copies beyond the MALL:
+  // - 5..32 rows: it wins at every N while its workgroups take one pass over
+  //   the CUs (N <= 16384; 1024 x 4096 at M = 16: 6.9 against 10.7 us for the
+  //   MFMA GEMM; 512 x 3584 at M = 8: 5.3 against 7.3 us for the skinny
+  //   kernel), and past that up to 12 rows (fused gate/up 28672 x 4096 at
+  //   M = 8: 15.5 against 17.5 us; 18944 x 3584 at M = 16: 15.1 against
+  //   13.9 us for the MFMA GEMM). K <= 8192: with longer rows its activation
+  //   reloads per 16-row tile outweigh the weights.
+  // - 3..4 rows: from N = 3072 (narrower layers: the GEMV, 4.3 against 5.1
+  //   us at 1024 x 4096).
+  // - 2 rows: for 8192 <= N <= 20480 (gate: 8.1 against 9.3 us for the GEMV).
+  // - act_order up to 16 rows (X[:, perm] gathered inside the kernel when it
+  //   fits LDS): from 3 rows at any N (512 x 3584 at M = 4: 6.0 against 7.5
+  //   us for the GEMV, which gathers too), and at 2 rows from N = 3072.
+  if (has_tiled && M >= 2 && M <= 32 && pmi::tgemm_supported(M, N, K, group_size) && K <= 8192 &&
+      (N <= 16384 || M <= 12)) {
+    const bool gathers = has_perm && M <= 16 && pmi::tgemm_gather_supported(M, K);
+    if (gathers ? (M >= 3 || N >= 3072) : (M >= 5 || (M >= 3 && N >= 3072) || (N >= 8192 && N <= 20480)))
+      return 5;
+  }
   // Group sizes 32 and 64 have no other matrix-core kernel: past 4 rows the
   // tiled GEMM (one activation block of 32 rows after another) replaces the
   // GEMV, which would stream the weights once per 4 rows.
@@ -358,24 +368,24 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   const int forced = g_kernel_override.load();
   // the tiled GEMM reads the tiled weights and the group-major scale/zero copies
   const bool has_tiled = w_tiled && scales_gm && zeros_gm && N % 4 == 0;
-  int choice = pmi_matmul_kernel_choice(M, N, K, group_size, has_tiled ? 1 : 0);
+  int choice = pmi_matmul_kernel_choice(
+      M, N, K, group_size, (has_tiled ? PMI_CHOICE_TILED : 0) | (perm ? PMI_CHOICE_PERM : 0));
   if (choice == 5) {
     if (!has_tiled || !pmi::tgemm_supported(M, N, K, group_size))
       return fail(PMI_ERR_UNSUPPORTED, "%s: the tiled GEMM needs w_tiled, scales_gm and zeros_gm, "
                   "M <= 32, N %% 4 == 0, K %% 512 == 0, K >= 1536 and group_size 32, 64 or a "
                   "multiple of 128", fn);
-    const bool gather_fits = workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
-    if (!perm || gather_fits) {
-      // act_order: X[:, perm] is gathered into the workspace first
-      const void* xs = x;
-      if (perm) {
-        void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
-        hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
-        if (e != hipSuccess) return from_hip(e, fn);
-        xs = xg;
-      }
-      return from_hip(pmi::launch_tgemm(xs, w_tiled, scales_gm, zeros_gm, y, M, N, K, group_size, s),
-                      fn);
+    // act_order: up to 16 rows the kernel gathers X[:, perm] itself (from
+    // LDS); past that X[:, perm] is gathered into the workspace first
+    if (!perm || pmi::tgemm_gather_supported(M, K))
+      return from_hip(pmi::launch_tgemm(x, perm, w_tiled, scales_gm, zeros_gm, y, M, N, K,
+                                        group_size, s), fn);
+    if (workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
+      void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
+      hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
+      if (e != hipSuccess) return from_hip(e, fn);
+      return from_hip(pmi::launch_tgemm(xg, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N, K,
+                                        group_size, s), fn);
     }
     if (forced) return fail(PMI_ERR_UNSUPPORTED, "%s: forced tiled GEMM with perm needs a "
                             "workspace of pmi_matmul_workspace_bytes() bytes", fn);

@@ -98,6 +98,14 @@ PMI_DEV void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
 }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0): all but the N youngest vector-memory
+// operations and every LDS operation of this wave are complete
+template <int N>
+PMI_DEV void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | ((N >> 4) << 14));
+}
+
 // BYTES (4 or 16) per lane from a buffer straight into LDS (buffer_load_dword /
 // _dwordx4 ... lds): lane i writes lds + BYTES*i; `lds` must be wave-uniform
 // (it is M0). The builtin only exists for the device; the host pass, which

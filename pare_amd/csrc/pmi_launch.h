@@ -209,9 +209,13 @@ inline size_t tiled_bytes(int64_t N, int64_t K) { return (size_t)((N + 63) / 64)
 hipError_t launch_tile(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N, int64_t K, int64_t gs,
                        hipStream_t stream);
 bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
+// act_order inside the tiled GEMM: X rows and the perm table fit its LDS
+constexpr int kTgemmXGLds = 160 * 1024 - 1024;
+bool tgemm_gather_supported(int64_t M, int64_t K);
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K);
-hipError_t launch_tgemm(const void* x, const uint8_t* w_tiled, const float* scales_gm,
-                        const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        hipStream_t stream);
+// perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null
+hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
+                        const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
+                        int64_t N, int64_t K, int64_t gs, hipStream_t stream);
 
 }  // namespace pmi

@@ -34,6 +34,15 @@
 // into a four-deep LDS ring with buffer_load ... lds, and all waves cross one
 // s_barrier per step.
 //
+// act_order (GATHER, up to 16 rows). The tiled weights hold their columns in perm
+// order, so the A operand of column c is x[:, perm[c]]. Every workgroup copies
+// the M activation rows (row stride 2K + 16 bytes, which puts the 16 rows of
+// one column in 16 different LDS banks) and the perm table (as byte offsets
+// 2 perm[c], out-of-range entries read column 0) into LDS once, before its
+// loop; each lane then gathers its 8 columns per k-step with 2-byte LDS reads,
+// one step ahead of the MFMAs. A workgroup reads X once either way, so the
+// gather adds the 4K-byte table to its L2 traffic and no launch.
+//
 // Pipeline. Each compute wave keeps a three-deep register ring of units
 // (weights, scales, zero points and, for MT = 1, activations): the loads of
 // step s + 2 are issued before step s is computed. The loop runs whole rounds
@@ -49,6 +58,8 @@
 // (pare/kernels/matmul_int4.py:105-176).
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "pmi_common.h"
 #include "pmi_launch.h"
 
@@ -59,9 +70,12 @@ constexpr int kKW = 4;     // compute waves (units u = 4 s + w)
 constexpr int kDW = 3;     // register ring depth (steps)
 constexpr int kDX = 4;     // LDS ring depth (steps), MT = 2
 constexpr int kProd = 2;   // activation producer waves, MT = 2
+constexpr int kXGLds = kTgemmXGLds;  // LDS of the act_order variant (X rows + perm table)
+constexpr int kXGPermIt = 8;         // perm-table entries per thread / 4 (K <= 8192)
 
 struct TgemmArgs {
   const f16* x;
+  const int32_t* perm;  // act_order columns (GATHER), else null
   const uint8_t* wt;    // tiled weights
   const float* s_gm;    // fp32 [G, N]
   const uint8_t* z_gm;  // u8 [G, N]
@@ -81,19 +95,26 @@ struct Unit {
   uint32_t z[GPU];
 };
 
-template <int MT, int NTW, int GPU>
+template <int MT, int NTW, int GPU, bool GATHER>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
+  static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
   constexpr bool RING = MT > 1;
   constexpr int BM = 16 * MT;
-  constexpr int XG = BM * 256;   // activation bytes of one unit (RING)
+  constexpr int XBYTES = BM * 256;   // activation bytes of one unit (RING)
   constexpr int CPU = BM / 4;    // 1 KiB copies per unit (RING)
   constexpr int SUBS = 4 / NTW;  // workgroups per panel
   constexpr int TPG = 4 / GPU;   // MFMA k-steps per group
   // activation ring (MT = 2), reused after the loop for the partial tiles of
   // three waves
-  constexpr int kRing = RING ? kKW * kDX * XG : 0;
+  constexpr int kRing = RING ? kKW * kDX * XBYTES : 0;
   constexpr int kRed = (kKW - 1) * MT * NTW * 64 * 16;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kRing > kRed ? kRing : kRed];
+  constexpr int kLds0 = kRing > kRed ? kRing : kRed;
+  // GATHER: the activation rows and the perm table in dynamic LDS sized by the
+  // host (max(M (2K + 16) + 4K, the partial tiles)), so that small row counts
+  // leave room for other workgroups; reused after the loop for the partial tiles
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s[GATHER ? 16 : kLds0];
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_d[];
+  uint8_t* const lds = GATHER ? lds_d : lds_s;
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -146,7 +167,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         const int k = cc / CPU, c = cc % CPU;
         int u = kKW * st + k;
         u = u < U ? u : U - 1;
-        copy_to_lds<16>(rx, lds + (k * kDX + slot) * XG + c * 1024, vx[c],
+        copy_to_lds<16>(rx, lds + (k * kDX + slot) * XBYTES + c * 1024, vx[c],
                         __builtin_amdgcn_readfirstlane(u * 256));
       }
     };
@@ -173,16 +194,80 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     const int upg = a.gs >= 128 ? a.gs >> 7 : 1;
     __amdgpu_buffer_rsrc_t rxd;
     int vxd = 0;
+    const int xstride = 2 * K + 16;   // GATHER: LDS bytes per activation row
+    const int xtab = M * xstride;     // GATHER: LDS offset of the perm table
+    int xrow = 0;                     // GATHER: LDS offset of the lane's row
     if constexpr (MT == 1) {
-      rxd = rsrc(a.x, (int64_t)M * K * 2);
       const int mg = m0 + ln < M ? m0 + ln : M - 1;
-      vxd = mg * K * 2 + 16 * h;
+      if constexpr (GATHER) {
+        xrow = mg * xstride;
+      } else {
+        rxd = rsrc(a.x, (int64_t)M * K * 2);
+        vxd = mg * K * 2 + 16 * h;
+      }
     }
+    // GATHER: X rows in 1 KiB copies (K % 512 == 0), dealt to the waves, and
+    // the perm table through registers (clamped, scaled to byte offsets; the
+    // table is written after the ring's first weight loads are issued, so
+    // that the latencies overlap)
+    u32x4 pv[GATHER ? kXGPermIt : 1];
+    auto stage_issue = [&]() {
+      if constexpr (GATHER) {
+        const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (int64_t)M * K * 2);
+        const int cpr = K >> 9;
+        for (int c = kw; c < M * cpr; c += kKW) {
+          const int m = c / cpr, q = c - m * cpr;
+          copy_to_lds<16>(rx, lds + m * xstride + q * 1024, 16 * l,
+                          __builtin_amdgcn_readfirstlane(m * K * 2 + q * 1024));
+        }
+        const __amdgpu_buffer_rsrc_t rp = rsrc(a.perm, (int64_t)K * 4);
+#pragma unroll
+        for (int i = 0; i < kXGPermIt; ++i) {
+          const int e = tid + i * kKW * 64;  // entries 4 e .. 4 e + 3
+          pv[i] = 4 * e < K ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 16 * e, 0, 0))
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    };
+    // GATHER: the A operands of a step come from LDS in three stages, each one
+    // step ahead of the next so that no LDS read waits inside a step: the
+    // perm-table offsets of step s + 2 (8 per k-step: lane (n, h), k-step t
+    // takes columns perm[128 u + 32 t + 8 h + i], i < 8, of row n), the
+    // 2-byte gathers of step s + 1, and the packing of step s.
+    uint32_t poff[GATHER ? 32 : 1], graw[GATHER ? 32 : 1];
+    auto table_read = [&](int s) {
+      if constexpr (GATHER) {
+        int u = kKW * s + kw;
+        u = u < U ? u : U - 1;
+        const uint8_t* pt = lds + xtab + (u * 128 + 8 * h) * 4;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(pt + 128 * (q >> 1) + 16 * (q & 1));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) poff[4 * q + c] = v[c];
+        }
+      }
+    };
+    auto gather_issue = [&]() {
+      if constexpr (GATHER) {
+        const uint8_t* xr = lds + xrow;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) graw[k] = *reinterpret_cast<const uint16_t*>(xr + poff[k]);
+      }
+    };
+    auto pack = [&](Unit<MT, NTW, GPU>& un) {
+      if constexpr (GATHER) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          un.xa[t] = u32x4{graw[8 * t] | (graw[8 * t + 1] << 16), graw[8 * t + 2] | (graw[8 * t + 3] << 16),
+                           graw[8 * t + 4] | (graw[8 * t + 5] << 16), graw[8 * t + 6] | (graw[8 * t + 7] << 16)};
+      }
+    };
     auto issue = [&](Unit<MT, NTW, GPU>& un, int s) {
       int u = kKW * s + kw;
       u = u < U ? u : U - 1;
       const int uu = __builtin_amdgcn_readfirstlane(u);
-      if constexpr (MT == 1) {
+      if constexpr (MT == 1 && !GATHER) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           un.xa[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rxd, vxd, uu * 256 + 64 * t, 0));
@@ -249,17 +334,41 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     };
 
     Unit<MT, NTW, GPU> ring[kDW];
+    if constexpr (GATHER) {
+      stage_issue();
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int d = 0; d < kDW - 1; ++d) {
       issue(ring[d], d);
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (GATHER) {
+#pragma unroll
+      for (int i = 0; i < kXGPermIt; ++i) {
+        const int e = tid + i * kKW * 64;  // entries 4 e .. 4 e + 3
+        if (4 * e < K) {
+          u32x4 o;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) o[c] = pv[i][c] < (uint32_t)K ? 2u * pv[i][c] : 0u;
+          *reinterpret_cast<u32x4*>(lds + xtab + 16 * e) = o;
+        }
+      }
+      // this wave's X copies have landed (only the ring's loads may still be
+      // in flight) and its table writes are done; after the barrier so are
+      // every wave's
+      wait_vmcnt_lgkm0<(kDW - 1) * (NTW + 2 * GPU)>();
+      barrier_only();
+      table_read(0);
+      gather_issue();
+      table_read(1);
     }
     int xslot = 0;
     auto step = [&](const Unit<MT, NTW, GPU>& un) {
       const uint8_t* xb = nullptr;
       if constexpr (RING) {
         barrier_only();  // the activations of this step are in LDS
-        xb = lds + (kw * kDX + xslot) * XG;
+        xb = lds + (kw * kDX + xslot) * XBYTES;
         xslot = xslot + 1 == kDX ? 0 : xslot + 1;
       }
       compute(un, xb);
@@ -272,6 +381,12 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       for (int d = 0; d < kDW; ++d) {
         issue(ring[(d + kDW - 1) % kDW], s0 + d + kDW - 1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (GATHER) {
+          pack(ring[d]);
+          gather_issue();
+          table_read(s0 + d + 2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         step(ring[d]);
       }
       s0 += kDW;
@@ -279,6 +394,11 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 #pragma unroll
     for (int d = 0; d < kDW - 1; ++d) {
       if (s0 + d >= steps) break;
+      if constexpr (GATHER) {
+        pack(ring[d]);
+        gather_issue();
+        table_read(s0 + d + 2);
+      }
       step(ring[d]);
     }
   }
@@ -327,8 +447,30 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 
 template <int MT, int NTW, int GPU>
 hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU>), dim3(c.grid),
-                     dim3((kKW + (MT == 1 ? 0 : kProd)) * 64), 0, stream, a);
+  const dim3 block((kKW + (MT == 1 ? 0 : kProd)) * 64);
+  if constexpr (MT == 1) {
+    if (a.perm) {
+      // dynamic LDS beyond the 64 KiB default: allowed once per variant and device
+      static std::atomic<uint64_t> allowed{0};
+      int dev = 0;
+      if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+      const uint64_t bit = 1ull << (dev & 63);
+      if (!(allowed.load() & bit)) {
+        if (hipError_t e = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&w4a16_tgemm_kernel<1, NTW, GPU, true>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, kXGLds);
+            e != hipSuccess)
+          return e;
+        allowed.fetch_or(bit);
+      }
+      const size_t need = (size_t)a.M * (2 * a.K + 16) + 4 * (size_t)a.K;
+      const size_t red = (size_t)(kKW - 1) * NTW * 64 * 16;
+      hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW, GPU, true>), dim3(c.grid), block,
+                         need > red ? need : red, stream, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU, false>), dim3(c.grid), block, 0, stream, a);
   return hipGetLastError();
 }
 
@@ -374,12 +516,18 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {
   return c;
 }
 
-hipError_t launch_tgemm(const void* x, const uint8_t* w_tiled, const float* scales_gm,
-                        const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
-                        hipStream_t stream) {
+bool tgemm_gather_supported(int64_t M, int64_t K) {
+  return M >= 1 && M <= 16 && K <= 4 * 64 * kXGPermIt * 4 && M * (2 * K + 16) + 4 * K <= kXGLds;
+}
+
+hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
+                        const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
+                        int64_t N, int64_t K, int64_t gs, hipStream_t stream) {
+  if (perm && !tgemm_gather_supported(M, K)) return hipErrorInvalidValue;
   const TgemmConfig c = tgemm_config(M, N, K);
   TgemmArgs a;
   a.x = (const f16*)x;
+  a.perm = perm;
   a.wt = w_tiled;
   a.s_gm = scales_gm;
   a.z_gm = zeros_gm;

@@ -291,8 +291,11 @@ class force_kernel:
         return False
 
 
-def kernel_choice(M: int, N: int, K: int, group_size: int, tiled: bool = False) -> str:
+def kernel_choice(M: int, N: int, K: int, group_size: int, tiled: bool = False,
+                  perm: bool = False) -> str:
     """'gemv', 'gemm', 'skinny', 'gemm64' or 'tgemm': the kernel matmul_w4a16 runs
-    for this shape (``tiled``: the caller passes the tiled weight copy)."""
-    c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size, int(tiled))
+    for this shape (``tiled``: the caller passes the tiled weight copy;
+    ``perm``: an act_order permutation)."""
+    flags = (_lib.PMI_CHOICE_TILED if tiled else 0) | (_lib.PMI_CHOICE_PERM if perm else 0)
+    c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size, flags)
     return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64", 5: "tgemm"}[c]

@@ -137,7 +137,7 @@ class QuantizedLinear(nn.Module):
             cache = self._kernel_cache
         return self._packed_weight_kernel, cache[1], cache[2], cache[3]
 
-    def _tiled_buffer(self, w_kernel: torch.Tensor, M: int):
+    def _tiled_buffer(self, w_kernel: torch.Tensor, M: int, perm: torch.Tensor | None = None):
         """Tiled copy of the kernel-layout weight for the tiled-weight GEMM,
         built on the first forward whose row count runs on it (decode-only use
         at one row never pays for it) and kept with the kernel-layout weight."""
@@ -145,7 +145,7 @@ class QuantizedLinear(nn.Module):
             if not tiled_supported(self.out_features, self.in_features, self._group_size()):
                 return None
             if kernel_choice(M, self.out_features, self.in_features, self._group_size(),
-                             tiled=True) != "tgemm":
+                             tiled=True, perm=perm is not None) != "tgemm":
                 return None
             self._packed_weight_tiled = tile_w4a16(w_kernel, self._group_size())
         return self._packed_weight_tiled
@@ -165,7 +165,7 @@ class QuantizedLinear(nn.Module):
         w_k, zero_u8, perm, sz_gm = self._kernel_buffers()
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
-        w_t = self._tiled_buffer(w_k, x_2d.shape[0])
+        w_t = self._tiled_buffer(w_k, x_2d.shape[0], perm)
         y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm, sz_gm=sz_gm,
                          w_tiled=w_t)
         y = y.to(x.dtype)

@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == _lib.ABI_VERSION == 10
+    assert L.pmi_abi_version() == _lib.ABI_VERSION == 11
 
 
 def test_kernel_choice(L):
@@ -65,8 +65,21 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(32, 6144, 4096, 32, 1) == 5
     assert L.pmi_matmul_kernel_choice(33, 14336, 4096, 128, 1) != 5   # beyond 32 rows
     assert L.pmi_matmul_kernel_choice(16, 4096, 14336, 128, 1) != 5   # K > 8192
-    assert L.pmi_matmul_kernel_choice(16, 1024, 4096, 128, 1) != 5    # too few workgroups
+    assert L.pmi_matmul_kernel_choice(16, 1024, 4096, 128, 1) == 5    # narrow layers too
+    assert L.pmi_matmul_kernel_choice(8, 512, 3584, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(4, 1024, 4096, 128, 1) == 1     # narrow at 4 rows: GEMV
     assert L.pmi_matmul_kernel_choice(16, 28672, 4096, 128, 1) != 5   # more than one pass at 16 rows
+    assert L.pmi_matmul_kernel_choice(16, 18944, 3584, 128, 1) != 5
+    # act_order (PMI_CHOICE_PERM): the in-kernel gather up to 16 rows where X
+    # and the perm table fit LDS
+    TP = _lib.PMI_CHOICE_TILED | _lib.PMI_CHOICE_PERM
+    assert L.pmi_matmul_kernel_choice(4, 512, 3584, 128, TP) == 5
+    assert L.pmi_matmul_kernel_choice(2, 512, 3584, 128, TP) == 1     # GEMV at 2 narrow rows
+    assert L.pmi_matmul_kernel_choice(2, 3584, 3584, 128, TP) == 5
+    assert L.pmi_matmul_kernel_choice(16, 3584, 3584, 128, TP) == 5
+    assert L.pmi_matmul_kernel_choice(1, 3584, 3584, 128, TP) == 1
+    assert L.pmi_matmul_kernel_choice(4, 512, 3584, 128, _lib.PMI_CHOICE_PERM) == 1  # no copy
+    assert L.pmi_matmul_kernel_choice(16, 3584, 18944, 128, TP) != 5  # K past the tiled GEMM
     # GEMV for M <= 2 (M <= 4 for N < 8192); skinny MFMA kernel up to M = 16 for
     # N <= 8192 while the activations fit the LDS budget; MFMA GEMM otherwise
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128, 0) == 1

@@ -126,7 +126,22 @@ def test_tile_rejects():
 
 # ---- GPU: GEMM ---------------------------------------------------------------------
 
-def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False):
+def _abi_no_workspace(x, wk, s, zu8, sz, wt, perm, gs):
+    """pmi_matmul_w4a16 with no workspace at all (null, 0 bytes)."""
+    M, K = x.shape
+    N = wk.shape[0]
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+    L = _lib.lib()
+    rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, wk.data_ptr(), s.data_ptr(), zu8.data_ptr(),
+                            _lib.PMI_U8, perm.data_ptr() if perm is not None else None,
+                            sz[0].data_ptr(), sz[1].data_ptr(), wt.data_ptr(), y.data_ptr(),
+                            _lib.PMI_F16, M, N, K, gs, None, 0,
+                            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.last_error()
+    return y
+
+
+def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False, no_workspace=False):
     if act_order:
         g0 = torch.Generator().manual_seed(seed)
         w = (torch.randn(N, K, generator=g0) * 0.02).numpy().astype(np.float32)
@@ -145,7 +160,11 @@ def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False):
     g = torch.Generator().manual_seed(seed + 1)
     x = torch.randn(M, K, generator=g).to(torch.float16)
     with force_kernel(kernel):
-        y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt, perm=perm)
+        if no_workspace:
+            y = _abi_no_workspace(x.to(DEV), wk, _cuda(s).contiguous(), zu8.contiguous(), sz, wt,
+                                  perm, gs)
+        else:
+            y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt, perm=perm)
     torch.cuda.synchronize()
     ref = O.linear_fp32(x.float().numpy(), ref_w)
     yy = y.float().cpu().numpy()
@@ -193,6 +212,18 @@ def test_tgemm_small_groups_many_rows(gs, M):
 @pytest.mark.parametrize("M", [3, 16, 29])
 def test_tgemm_act_order(M):
     _tgemm_case(M, 3584, 3584, 128, seed=40 + M, act_order=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,gs", [
+    (1, 512, 3584, 128), (2, 1024, 1536, 128), (7, 4096, 4096, 128), (16, 4096, 4096, 128),
+    (16, 512, 3584, 128), (8, 2048, 7680, 128), (16, 200, 2048, 32), (11, 1028, 3072, 64),
+    (16, 18944, 3584, 128)])
+def test_tgemm_act_order_in_kernel_gather(M, N, K, gs):
+    """Up to 16 rows the tiled GEMM gathers X[:, perm] itself from LDS (no
+    workspace, no gather launch): every row count, group size and the largest
+    K its LDS takes at 8 and 16 rows."""
+    _tgemm_case(M, N, K, gs, seed=M * 31 + N % 89, act_order=True, no_workspace=True)
 
 
 @pytest.mark.gpu
