@@ -49,7 +49,10 @@ struct SkinnyConfig {
 // Compute units of the current device (cached; 256 when the query fails).
 int device_cu_count();
 
-GemvConfig gemv_config(int64_t M, int64_t N, int64_t K);
+// gather: act_order with X staged in LDS per workgroup (mode 4), where every
+// workgroup also reads X and the permutation once, so long rows take fewer,
+// larger workgroups
+GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, bool gather = false);
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
 
