@@ -176,7 +176,11 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   // - act_order up to 16 rows (X[:, perm] gathered inside the kernel when it
   //   fits LDS): from 3 rows at any N (512 x 3584 at M = 4: 6.0 against 7.5
   //   us for the GEMV, which gathers too), and at 2 rows from N = 3072.
-  if (has_tiled && M >= 2 && M <= 32 && pmi::tgemm_supported(M, N, K, group_size) && K <= 8192 &&
+  // - 33..64 rows (64-row activation blocks, every B operand feeding four
+  //   activation tiles) while the workgroups take one pass (gate 14336 x 4096
+  //   at M = 64: 15.9 against 17.6 us for the MFMA GEMM; 4096 x 4096: 10.5
+  //   against 11.8 us).
+  if (has_tiled && M >= 2 && M <= 64 && pmi::tgemm_supported(M, N, K, group_size) && K <= 8192 &&
       (N <= 16384 || M <= 12)) {
     const bool gathers = has_perm && M <= 16 && pmi::tgemm_gather_supported(M, K);
     if (gathers ? (M >= 3 || N >= 3072) : (M >= 5 || (M >= 3 && N >= 3072) || (N >= 8192 && N <= 20480)))

@@ -1,4 +1,4 @@
-// Tiled-weight MFMA INT4 W4A16 GEMM for 3..32 activation rows, gfx950
+// Tiled-weight MFMA INT4 W4A16 GEMM for 2..64 activation rows, gfx950
 // (v_mfma_f32_16x16x32_f16).
 //
 // Why a tiled copy of the weights. At these row counts the kernel is a weight
@@ -32,7 +32,11 @@
 // 17-32 rows (MT = 2) would need twice the registers; there two producer
 // waves copy the activations of each step (the four units of the four waves)
 // into a four-deep LDS ring with buffer_load ... lds, and all waves cross one
-// s_barrier per step.
+// s_barrier per step. 33-64 rows (MT = 4) use the same ring with half units
+// per slot (64 columns; 32 KiB a slot, 128 KiB for four), two barriers per
+// step: every B operand then feeds four activation tiles, and the ring stays
+// four slots deep (gate_proj at M = 64: 15.9 against 17.6 us for the MFMA
+// GEMM of w4a16_gemm.hip; with full-unit slots, two fit: 16.4 us).
 //
 // act_order (GATHER, up to 16 rows). The tiled weights hold their columns in perm
 // order, so the A operand of column c is x[:, perm[c]]. Every workgroup copies
@@ -68,8 +72,8 @@ namespace {
 
 constexpr int kKW = 4;     // compute waves (units u = 4 s + w)
 constexpr int kDW = 3;     // register ring depth (steps)
-constexpr int kDX = 4;     // LDS ring depth (steps), MT = 2
-constexpr int kProd = 2;   // activation producer waves, MT = 2
+constexpr int kDX = 4;     // LDS ring depth (slots), MT = 2 and 4
+constexpr int kProd = 2;   // activation producer waves, MT = 2 and 4
 constexpr int kXGLds = kTgemmXGLds;  // LDS of the act_order variant (X rows + perm table)
 constexpr int kXGPermIt = 8;         // perm-table entries per thread / 4 (K <= 8192)
 
@@ -99,12 +103,18 @@ template <int MT, int NTW, int GPU, bool GATHER>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
   constexpr bool RING = MT > 1;
+  // MT = 4: the ring holds half units (64 columns, k-steps 0-1 or 2-3), two
+  // slots per unit, so that the same 128 KiB hold four slots
+  constexpr bool HALF = MT == 4;
   constexpr int BM = 16 * MT;
-  constexpr int XBYTES = BM * 256;   // activation bytes of one unit (RING)
-  constexpr int CPU = BM / 4;    // 1 KiB copies per unit (RING)
+  constexpr int RB = HALF ? 128 : 256;  // bytes of an activation row in a slot
+  constexpr int XBYTES = BM * RB;       // activation bytes of a slot (RING)
+  constexpr int CPU = XBYTES / 1024;    // 1 KiB copies per slot (RING)
+  constexpr int RPC = 1024 / RB;        // activation rows per copy
+  constexpr int CH = RB / 16;           // 16-byte chunks per row in a slot
   constexpr int SUBS = 4 / NTW;  // workgroups per panel
   constexpr int TPG = 4 / GPU;   // MFMA k-steps per group
-  // activation ring (MT = 2), reused after the loop for the partial tiles of
+  // activation ring (MT = 2, 4), reused after the loop for the partial tiles of
   // three waves
   constexpr int kRing = RING ? kKW * kDX * XBYTES : 0;
   constexpr int kRed = (kKW - 1) * MT * NTW * 64 * 16;
@@ -146,17 +156,19 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (RING && wv >= kKW) {
-    // ---- activation producer p: per step the units 4 s .. 4 s + 3, copy c of
-    // unit k covers rows 4 c + l / 16; LDS chunk l % 16 of a row holds
-    // activation chunk (l % 16) ^ (row % 16)
+    // ---- activation producer p: per slot the units 4 s .. 4 s + 3 (MT = 4:
+    // their halves), copy c of unit k covers rows RPC c + l / CH; LDS chunk
+    // l % CH of a row holds activation chunk (l % CH) ^ (row % 16) (MT = 4:
+    // ^ ((row / 2) % 8), so that each 16 lanes of an A read, rows n = 0..15,
+    // hit 16 different bank groups)
     const int p = wv - kKW;
     const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, (int64_t)M * K * 2);
     int vx[CPU];
 #pragma unroll
     for (int c = 0; c < CPU; ++c) {
-      const int r = 4 * c + (l >> 4);
+      const int r = RPC * c + l / CH;
       const int mg = m0 + r < M ? m0 + r : M - 1;
-      vx[c] = mg * K * 2 + 16 * ((l & 15) ^ (r & 15));
+      vx[c] = mg * K * 2 + 16 * ((l % CH) ^ ((HALF ? r >> 1 : r) % CH));
     }
     constexpr int CPS = kKW * CPU / kProd;  // copies per producer per step
     static_assert((kDX - 1) * CPS < 64, "copies in flight fit vmcnt");
@@ -165,16 +177,16 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       for (int q = 0; q < CPS; ++q) {
         const int cc = q * kProd + p;
         const int k = cc / CPU, c = cc % CPU;
-        int u = kKW * st + k;
+        int u = kKW * (HALF ? st >> 1 : st) + k;
         u = u < U ? u : U - 1;
         copy_to_lds<16>(rx, lds + (k * kDX + slot) * XBYTES + c * 1024, vx[c],
-                        __builtin_amdgcn_readfirstlane(u * 256));
+                        __builtin_amdgcn_readfirstlane(u * 256 + (HALF ? (st & 1) * 128 : 0)));
       }
     };
     for (int d = 0; d < kDX - 1; ++d) issue(d, d);
     int slot = kDX - 1;
-    for (int s = 0; s < steps; ++s) {
-      wait_vmcnt<(kDX - 2) * CPS>();  // step s has landed
+    for (int s = 0; s < (HALF ? 2 * steps : steps); ++s) {
+      wait_vmcnt<(kDX - 2) * CPS>();  // slot s has landed
       barrier_only();                 // ... and every wave is done with step s - 1
       issue(slot, s + kDX - 1);
       slot = slot + 1 == kDX ? 0 : slot + 1;
@@ -295,17 +307,21 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         }
       }
     };
-    auto compute = [&](const Unit<MT, NTW, GPU>& un, const uint8_t* xb) {
+    f32x4 cg[MT][NTW];  // the current group's products (kept across the halves of MT = 4)
+    auto compute = [&](const Unit<MT, NTW, GPU>& un, const uint8_t* xb, int half) {
       const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-      f32x4 cg[MT][NTW];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        if (HALF && (t >> 1) != half) continue;
         const int gp = t / TPG;
         const int run = t >> 1, half = t & 1;
         f16x8 A[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           if constexpr (MT == 1) A[mt] = __builtin_bit_cast(f16x8, un.xa[t]);
+          else if constexpr (HALF)
+            A[mt] = *reinterpret_cast<const f16x8*>(xb + (16 * mt + ln) * RB +
+                                                     (((4 * (t & 1) + h) ^ ((ln >> 1) % CH)) << 4));
           else A[mt] = *reinterpret_cast<const f16x8*>(xb + (16 * mt + ln) * 256 + (((4 * t + h) ^ ln) << 4));
         }
 #pragma unroll
@@ -371,7 +387,13 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         xb = lds + (kw * kDX + xslot) * XBYTES;
         xslot = xslot + 1 == kDX ? 0 : xslot + 1;
       }
-      compute(un, xb);
+      compute(un, xb, 0);
+      if constexpr (HALF) {
+        barrier_only();  // ... and of its second half
+        xb = lds + (kw * kDX + xslot) * XBYTES;
+        xslot = xslot + 1 == kDX ? 0 : xslot + 1;
+        compute(un, xb, 1);
+      }
     };
     // Whole rounds of kDW steps, then a tail already in flight. The host
     // guarantees steps >= kDW.
@@ -501,7 +523,7 @@ bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
 
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {
   TgemmConfig c;
-  c.mt = M <= 16 ? 1 : 2;
+  c.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   // the most rows per workgroup that still give about one workgroup per CU
   const int64_t cus = device_cu_count();
   const int64_t panels = (N + 63) / 64;
@@ -539,7 +561,8 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   a.n_wg = c.n_wg;
   a.grid_m = c.grid_m;
   if (c.mt == 1) return launch_mt<1>(c, a, stream);
-  return launch_mt<2>(c, a, stream);
+  if (c.mt == 2) return launch_mt<2>(c, a, stream);
+  return launch_mt<4>(c, a, stream);
 }
 
 }  // namespace pmi

@@ -55,7 +55,9 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(2, 14336, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(2, 6144, 4096, 128, 1) == 1     # GEMV at 2 rows below N = 8192
     assert L.pmi_matmul_kernel_choice(1, 14336, 4096, 128, 1) == 1    # GEMV at 1 row
-    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128, 1) == 2   # MFMA GEMM past 32 rows
+    assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128, 1) == 5   # 64-row blocks
+    assert L.pmi_matmul_kernel_choice(65, 14336, 4096, 128, 1) != 5   # past 64 rows
+    assert L.pmi_matmul_kernel_choice(64, 28672, 4096, 128, 1) != 5   # more than one pass
     assert L.pmi_matmul_kernel_choice(8, 28672, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64, 1) == 5    # gs 64: tiled GEMM past 4 rows
     assert L.pmi_matmul_kernel_choice(512, 4096, 4096, 32, 1) == 5
@@ -63,7 +65,6 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64, 0) == 1    # without the copy: GEMV
     assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(32, 6144, 4096, 32, 1) == 5
-    assert L.pmi_matmul_kernel_choice(33, 14336, 4096, 128, 1) != 5   # beyond 32 rows
     assert L.pmi_matmul_kernel_choice(16, 4096, 14336, 128, 1) != 5   # K > 8192
     assert L.pmi_matmul_kernel_choice(16, 1024, 4096, 128, 1) == 5    # narrow layers too
     assert L.pmi_matmul_kernel_choice(8, 512, 3584, 128, 1) == 5

@@ -177,7 +177,7 @@ def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False, no_workspace
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 3, 5, 8, 16, 17, 24, 32])
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 16, 17, 24, 32, 33, 47, 64, 65, 100])
 def test_tgemm_rows(M):
     _tgemm_case(M, 1024, 2048, 128, seed=10 + M)
 
@@ -185,7 +185,7 @@ def test_tgemm_rows(M):
 @pytest.mark.gpu
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 4096), (6144, 4096), (3584, 3584),
                                  (1028, 1536), (200, 2560), (4100, 2048)])
-@pytest.mark.parametrize("M", [4, 16, 32])
+@pytest.mark.parametrize("M", [4, 16, 32, 64])
 def test_tgemm_shapes(M, N, K):
     _tgemm_case(M, N, K, 128, seed=N % 97 + M)
 
