@@ -49,10 +49,10 @@ struct SkinnyConfig {
 // Compute units of the current device (cached; 256 when the query fails).
 int device_cu_count();
 
-// gather: act_order with X staged in LDS per workgroup (mode 4), where every
-// workgroup also reads X and the permutation once, so long rows take fewer,
-// larger workgroups
-GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, bool gather = false);
+// xmode: the activation transform (GemvXform::mode). Modes whose per-workgroup
+// prologue reads all of X once (4: act_order staged in LDS, 3: RMSNorm over
+// the row) take fewer, larger workgroups on some shapes.
+GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode = 0);
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);
 

@@ -718,7 +718,7 @@ constexpr int kMaxPartBytes = 32 * 1024;  // LDS for the per-row partials
 
 }  // namespace
 
-GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, bool gather) {
+GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   GemvConfig c;
   const int mt = (int)(M < 4 ? M : 4);
   const int64_t row_chunks = K / 32;
@@ -759,9 +759,13 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, bool gather) {
   // act_order gather (mode 4) on such rows: one per CU, since every workgroup
   // reads the activations (2K bytes) and the permutation (4K) from L2 once
   // (Qwen down 3584 x 18944: 13.8 against 18.1 us at two per CU)
-  if (mt == 1 && c.slices_per_wave == 2) { c.rows_per_wave = 1; wpc = gather ? 1 : 2; }
+  if (mt == 1 && c.slices_per_wave == 2) { c.rows_per_wave = 1; wpc = xmode == 4 ? 1 : 2; }
   else if (mt == 1 && c.slice_waves >= 3) { c.rows_per_wave = 4; wpc = 1; }
   else if (mt == 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 1; }
+  // with the RMSNorm prologue (mode 3) every workgroup first reduces the whole
+  // row: single rows at two per CU (fused q/k/v in the decoder: 8.0 against
+  // 9.1 us for pairs at three)
+  else if (mt == 1 && rows_per_cu >= 20 && xmode == 3) { c.rows_per_wave = 1; wpc = 2; }
   else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 2; wpc = 3; }
   else if (mt > 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 2; }
   else one_batch = true;
@@ -804,7 +808,7 @@ hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, con
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream, const GemvXform* xform) {
   const GemvXform xf = xform ? *xform : GemvXform{};
-  const GemvConfig c = gemv_config(M, N, K, perm && xf.mode == 4);
+  const GemvConfig c = gemv_config(M, N, K, perm || xf.mode != 4 ? xf.mode : 0);
   const int n = (int)N, k = (int)K, g = (int)gs;
   switch (M) {
     case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, xf, stream);
