@@ -117,7 +117,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // activation ring (MT = 2, 4), reused after the loop for the partial tiles of
   // three waves
   constexpr int kRing = RING ? kKW * kDX * XBYTES : 0;
-  constexpr int kRed = (kKW - 1) * MT * NTW * 64 * 16;
+  constexpr int kRed = kKW * MT * NTW * 64 * 16;  // partial tiles, indexed by source wave
   constexpr int kLds0 = kRing > kRed ? kRing : kRed;
   // GATHER: the activation rows and the perm table in dynamic LDS sized by the
   // host (max(M (2K + 16) + 4K, the partial tiles)), so that small row counts
@@ -428,33 +428,38 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // ---- the four waves' partial tiles are added through LDS (a unit past K,
   // re-read by a clamped load, is never computed: steps * 4 covers U exactly
   // only when U % 4 == 0, which the host requires)
+  // Activation tile mt is finished by compute wave mt % 4 (all by wave 0 at
+  // MT = 1): every compute wave stores its partial tiles, and the finishing
+  // wave adds the four in wave order 0..3 (no register array is indexed by
+  // the wave number, which would put it in scratch memory).
   __syncthreads();
   f32x4* red = reinterpret_cast<f32x4*>(lds);
-  if (wv > 0 && wv < kKW) {
+  if (wv < kKW) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) red[(((wv - 1) * MT + mt) * NTW + j) * 64 + l] = acc[mt][j];
+      for (int j = 0; j < NTW; ++j) red[((wv * MT + mt) * NTW + j) * 64 + l] = acc[mt][j];
   }
   __syncthreads();
-  if (wv != 0) return;
+  if (wv >= kKW || row0 >= N) return;
 #pragma unroll
-  for (int k = 1; k < kKW; ++k)
+  for (int mt = 0; mt < MT; ++mt) {
+    if ((MT == 1 ? 0 : mt % kKW) != wv) continue;
+    f32x4 sum[NTW];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int j = 0; j < NTW; ++j) {
+      sum[j] = red[(mt * NTW + j) * 64 + l];
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) acc[mt][j] += red[(((k - 1) * MT + mt) * NTW + j) * 64 + l];
-  if (row0 >= N) return;
-  // lane (n, h): rows 16 mt + 4 h + i of the activations, weight rows row0 + j
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+      for (int k = 1; k < kKW; ++k) sum[j] += red[((k * MT + mt) * NTW + j) * 64 + l];
+    }
+    // lane (n, h): rows 16 mt + 4 h + i of the activations, weight rows row0 + j
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = m0 + 16 * mt + 4 * h + i;
       if (m >= M) continue;
       uint16_t v[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(acc[mt][j][i]));
+      for (int j = 0; j < NTW; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(sum[j][i]));
       f16* dst = a.y + (size_t)m * N + row0;
       if constexpr (NTW == 4) {
         *reinterpret_cast<uint2*>(dst) = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16),
@@ -465,6 +470,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         *reinterpret_cast<uint16_t*>(dst) = v[0];
       }
     }
+  }
 }
 
 template <int MT, int NTW, int GPU>
@@ -486,7 +492,7 @@ hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stre
         allowed.fetch_or(bit);
       }
       const size_t need = (size_t)a.M * (2 * a.K + 16) + 4 * (size_t)a.K;
-      const size_t red = (size_t)(kKW - 1) * NTW * 64 * 16;
+      const size_t red = (size_t)kKW * NTW * 64 * 16;
       hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW, GPU, true>), dim3(c.grid), block,
                          need > red ? need : red, stream, a);
       return hipGetLastError();
