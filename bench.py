@@ -518,8 +518,9 @@ def main():
                 else:
                     gate_loop(stream.cuda_stream, m_rows, 2 * n_layers)
         torch.cuda.synchronize()
-        log(f"{args.kernel_only} (M={m_rows}): 5 passes, kernel "
-            f"{P.kernel_choice(m_rows, 14336, 4096, GS, tiled=True)}")
+        what = ("read probe" if args.kernel_only == "read_floor" else
+                f"kernel {P.kernel_choice(m_rows, 14336, 4096, GS, tiled=True)}")
+        log(f"{args.kernel_only} (M={m_rows}): 5 passes, {what}")
         return
 
     # --- eager vs graph: same outputs -------------------------------------

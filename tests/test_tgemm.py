@@ -267,3 +267,26 @@ def test_module_builds_tiled_copy(rows):
     ref = q(x)
     torch.cuda.synchronize()
     assert torch.allclose(y.float(), ref.float(), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(16, 512, 3584), (5, 3584, 3584), (16, 4096, 4096), (2, 1024, 1536)])
+def test_tgemm_in_kernel_gather_equals_pregathered(M, N, K):
+    """The in-kernel gather of X[:, perm] gives the same bits as the tiled GEMM
+    on X[:, perm] gathered beforehand (same A operands, same order of sums)."""
+    gs = 128
+    g0 = torch.Generator().manual_seed(M + N)
+    w = (torch.randn(N, K, generator=g0) * 0.02).numpy().astype(np.float32)
+    packed, s, z, g_idx = O.rtn_quantize_act_order(w, np.random.default_rng(K).permutation(K), gs)
+    perm = P.perm_from_g_idx(_cuda(g_idx), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=perm)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    sz = P.sz_group_major(_cuda(s), zu8)
+    wt = P.tile_w4a16(wk, gs)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(3)).to(torch.float16).to(DEV)
+    with force_kernel("tgemm"):
+        y_in = _abi_no_workspace(x, wk, _cuda(s).contiguous(), zu8.contiguous(), sz, wt, perm, gs)
+        y_pre = _abi_no_workspace(x[:, perm.long()].contiguous(), wk, _cuda(s).contiguous(),
+                                  zu8.contiguous(), sz, wt, None, gs)
+    torch.cuda.synchronize()
+    assert torch.equal(y_in.view(torch.int16), y_pre.view(torch.int16))
