@@ -766,7 +766,9 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   // row: single rows at two per CU (fused q/k/v in the decoder: 8.0 against
   // 9.1 us for pairs at three)
   else if (mt == 1 && rows_per_cu >= 20 && xmode == 3) { c.rows_per_wave = 1; wpc = 2; }
-  else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 2; wpc = 3; }
+  // act_order staged in LDS (mode 4) reads X and the int32 permutation once per
+  // workgroup: one per CU (6144 x 4096: 6.7 against 9.4 us at three)
+  else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 2; wpc = xmode == 4 ? 1 : 3; }
   else if (mt > 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 2; }
   else one_batch = true;
   if (one_batch || c.rows_per_wave > max_u) {
