@@ -294,6 +294,17 @@ def measured_peaks(L, dev, stream, gate_up_bufs):
         del gr
     best = min(floor.values(), key=lambda r: r["us"])
     out["read_floor_gate_up_weights"] = {"bytes_per_launch": wbytes, "best": best, **floor}
+
+    # the per-launch floor of a graph of dependent launches: the same probe
+    # reading 16 KiB on one workgroup, 128 launches back to back (a decode step
+    # of the 4-launch set is 128 launches)
+    def tiny(s):
+        for _ in range(128):
+            assert L.pmi_read_probe(gate_up_bufs[0].w.data_ptr(), 16 << 10, 1, sink.data_ptr(), s) == 0
+    gt = capture(tiny, stream)
+    gt.replay()
+    out["graph_launch_floor_us"] = round(time_graph(gt, 5, stream) * 1e3 / 128, 2)
+    del gt
     big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     big2 = torch.empty_like(big)
 
