@@ -180,8 +180,14 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
   //   activation tiles) while the workgroups take one pass (gate 14336 x 4096
   //   at M = 64: 15.9 against 17.6 us for the MFMA GEMM; 4096 x 4096: 10.5
   //   against 11.8 us).
+  // - past one pass over the CUs (N > 16384), up to 12 rows, and up to 16 where
+  //   ranges of 5-6 tiles per workgroup cover the tiles in one pass (Qwen gate/up
+  //   18944 x 3584 at M = 16: 13.6 against 13.9 us; with act_order 13.3 against
+  //   17.4 for the MFMA GEMM with its gather launch).
+  const int64_t panels = (N + 63) / 64, cus = pmi::device_cu_count();
+  const bool ranged = panels > cus && 4 * panels <= 6 * cus && group_size % 128 == 0;
   if (has_tiled && M >= 2 && M <= 64 && pmi::tgemm_supported(M, N, K, group_size) && K <= 8192 &&
-      (N <= 16384 || M <= 12)) {
+      (N <= 16384 || M <= 12 || (ranged && M <= 16))) {
     const bool gathers = has_perm && M <= 16 && pmi::tgemm_gather_supported(M, K);
     if (gathers ? (M >= 3 || N >= 3072) : (M >= 5 || (M >= 3 && N >= 3072) || (N >= 8192 && N <= 20480)))
       return 5;

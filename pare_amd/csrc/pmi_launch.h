@@ -32,7 +32,8 @@ struct GemmConfig {
 
 struct TgemmConfig {
   int mt;      // 16-row activation tiles (1: activations in registers, 2: LDS ring)
-  int ntw;     // 16-row weight tiles per workgroup (4, 2 or 1)
+  int ntw;     // 16-row weight tiles per workgroup (4, 2 or 1; 5 or 6 for ranges)
+  bool rng;    // ntw consecutive tiles per workgroup across panels (up to 16 rows)
   int n_wg;    // weight workgroups
   int grid_m;  // activation blocks
   int grid;    // workgroups
@@ -215,7 +216,7 @@ bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 // act_order inside the tiled GEMM: X rows and the perm table fit its LDS
 constexpr int kTgemmXGLds = 160 * 1024 - 1024;
 bool tgemm_gather_supported(int64_t M, int64_t K);
-TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K);
+TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gather);
 // perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null
 hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
                         const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,

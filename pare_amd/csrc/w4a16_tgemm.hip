@@ -87,21 +87,30 @@ struct TgemmArgs {
   int M, N, K, gs;
   int n_wg;    // weight workgroups (16 NTW rows each)
   int grid_m;  // activation blocks of 16 MT rows
+  int n_tiles; // RNG: 16-row tiles (4 per 64-row panel)
 };
 
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
-// the GPU groups of the unit the NTW scales and zero points of the lane's rows.
-template <int MT, int NTW, int GPU>
+// the GPU groups of the unit the NTW scales and zero points of the lane's rows
+// (RNG: one scale and zero point per tile, the tiles' rows are not adjacent).
+template <int MT, int NTW, int GPU, bool RNG = false>
 struct Unit {
   u32x4 xa[MT == 1 ? 4 : 1];
   u32x4 w[NTW];
-  f32x4 s[GPU];
-  uint32_t z[GPU];
+  f32x4 s[RNG ? 1 : GPU];
+  uint32_t z[RNG ? 1 : GPU];
+  float sr[RNG ? NTW : 1];
+  uint32_t zr[RNG ? NTW : 1];
 };
 
-template <int MT, int NTW, int GPU, bool GATHER>
+// RNG: the workgroup takes NTW consecutive 16-row tiles t0 = wg NTW .. of the
+// 4 n_panels tiles (5 or 6 of them, so that one pass over the CUs covers more
+// than one 64-row panel per CU), the last ones clamped and not stored.
+template <int MT, int NTW, int GPU, bool GATHER, bool RNG>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
+  static_assert(!RNG || (MT == 1 && GPU == 1), "tile ranges are built for up to 16 rows, gs >= 128");
+  using UnitT = Unit<MT, NTW, GPU, RNG>;
   constexpr bool RING = MT > 1;
   // MT = 4: the ring holds half units (64 columns, k-steps 0-1 or 2-3), two
   // slots per unit, so that the same 128 KiB hold four slots
@@ -139,15 +148,27 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     wg = 8 * q + (r & 7);
     mb = r >> 3;
   }
-  const int panel = wg / SUBS, jb = (wg % SUBS) * NTW;
+  const int panel = RNG ? 0 : wg / SUBS, jb = RNG ? 0 : (wg % SUBS) * NTW;
   const int M = a.M, N = a.N, K = a.K;
   // padding workgroups: past the weight workgroups, or past the last rows (uniform)
-  if (wg >= a.n_wg || 64 * panel + jb >= N) return;
+  if (wg >= a.n_wg || (!RNG && 64 * panel + jb >= N)) return;
   const int m0 = mb * BM;  // first activation row of this block
   const int U = K >> 7;              // units
   const int steps = (U + kKW - 1) / kKW;
   const int ln = l & 15, h = l >> 4;
   const int row0 = 64 * panel + 4 * ln + jb;  // first of the lane's NTW rows
+  // RNG: tile j of the range (clamped to the last tile), its lane row and the
+  // wave-uniform byte offset of its 1 KiB in every 4 KiB block
+  int trow[RNG ? NTW : 1], tbase[RNG ? NTW : 1];
+  if constexpr (RNG) {
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      int t = wg * NTW + j;
+      t = t < a.n_tiles ? t : a.n_tiles - 1;
+      trow[j] = 64 * (t >> 2) + 4 * ln + (t & 3);
+      tbase[j] = (t >> 2) * (K >> 7) * 4096 + 1024 * (t & 3);
+    }
+  }
 
   f32x4 acc[MT][NTW];
 #pragma unroll
@@ -267,7 +288,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         for (int k = 0; k < 32; ++k) graw[k] = *reinterpret_cast<const uint16_t*>(xr + poff[k]);
       }
     };
-    auto pack = [&](Unit<MT, NTW, GPU>& un) {
+    auto pack = [&](UnitT& un) {
       if constexpr (GATHER) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -275,7 +296,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
                            graw[8 * t + 4] | (graw[8 * t + 5] << 16), graw[8 * t + 6] | (graw[8 * t + 7] << 16)};
       }
     };
-    auto issue = [&](Unit<MT, NTW, GPU>& un, int s) {
+    auto issue = [&](UnitT& un, int s) {
       int u = kKW * s + kw;
       u = u < U ? u : U - 1;
       const int uu = __builtin_amdgcn_readfirstlane(u);
@@ -283,6 +304,18 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           un.xa[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rxd, vxd, uu * 256 + 64 * t, 0));
+      }
+      if constexpr (RNG) {
+        const int g = uu / upg;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          un.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+              rw, 16 * l, __builtin_amdgcn_readfirstlane(tbase[j] + uu * 4096), 2));
+          const int rc = trow[j] < N ? trow[j] : N - 1;
+          un.sr[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, rc * 4, g * 4 * N, 0));
+          un.zr[j] = __builtin_amdgcn_raw_buffer_load_b8(rz, rc, g * N, 0);
+        }
+        return;
       }
 #pragma unroll
       for (int j = 0; j < NTW; ++j)
@@ -308,7 +341,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       }
     };
     f32x4 cg[MT][NTW];  // the current group's products (kept across the halves of MT = 4)
-    auto compute = [&](const Unit<MT, NTW, GPU>& un, const uint8_t* xb, int half) {
+    auto compute = [&](const UnitT& un, const uint8_t* xb, int half) {
       const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -326,7 +359,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         }
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
-          const f16x2 nz = as_f16x2(neg_magic_zero_x2((un.z[gp] >> (8 * j)) & 0xFFu));
+          const uint32_t zq = RNG ? un.zr[j] & 0xFFu : (un.z[gp] >> (8 * j)) & 0xFFu;
+          const f16x2 nz = as_f16x2(neg_magic_zero_x2(zq));
           const uint32_t w0 = un.w[j][2 * half], w1 = un.w[j][2 * half + 1];
           const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
           const uint32_t t1 = (run ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
@@ -339,7 +373,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         if (t % TPG == TPG - 1) {
 #pragma unroll
           for (int j = 0; j < NTW; ++j) {
-            const float sc = un.s[gp][j];
+            const float sc = RNG ? un.sr[j] : un.s[gp][j];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -349,7 +383,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       }
     };
 
-    Unit<MT, NTW, GPU> ring[kDW];
+    UnitT ring[kDW];
     if constexpr (GATHER) {
       stage_issue();
       __builtin_amdgcn_sched_barrier(0);
@@ -373,14 +407,14 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       // this wave's X copies have landed (only the ring's loads may still be
       // in flight) and its table writes are done; after the barrier so are
       // every wave's
-      wait_vmcnt_lgkm0<(kDW - 1) * (NTW + 2 * GPU)>();
+      wait_vmcnt_lgkm0<(kDW - 1) * (RNG ? 3 * NTW : NTW + 2 * GPU)>();
       barrier_only();
       table_read(0);
       gather_issue();
       table_read(1);
     }
     int xslot = 0;
-    auto step = [&](const Unit<MT, NTW, GPU>& un) {
+    auto step = [&](const UnitT& un) {
       const uint8_t* xb = nullptr;
       if constexpr (RING) {
         barrier_only();  // the activations of this step are in LDS
@@ -441,7 +475,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       for (int j = 0; j < NTW; ++j) red[((wv * MT + mt) * NTW + j) * 64 + l] = acc[mt][j];
   }
   __syncthreads();
-  if (wv >= kKW || row0 >= N) return;
+  if (wv >= kKW || (!RNG && row0 >= N)) return;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     if ((MT == 1 ? 0 : mt % kKW) != wv) continue;
@@ -457,9 +491,16 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     for (int i = 0; i < 4; ++i) {
       const int m = m0 + 16 * mt + 4 * h + i;
       if (m >= M) continue;
+      if constexpr (RNG) {
+        // one 2-byte store per tile: the range's rows are 4 apart per tile
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+          if (wg * NTW + j < a.n_tiles && trow[j] < N) a.y[(size_t)m * N + trow[j]] = f32_to_f16_rne(sum[j][i]);
+        continue;
+      }
       uint16_t v[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(sum[j][i]));
+      for (int j = 0; j < NTW && j < 4; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(sum[j][i]));
       f16* dst = a.y + (size_t)m * N + row0;
       if constexpr (NTW == 4) {
         *reinterpret_cast<uint2*>(dst) = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16),
@@ -473,7 +514,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   }
 }
 
-template <int MT, int NTW, int GPU>
+template <int MT, int NTW, int GPU, bool RNG = false>
 hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
   const dim3 block((kKW + (MT == 1 ? 0 : kProd)) * 64);
   if constexpr (MT == 1) {
@@ -485,7 +526,7 @@ hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stre
       const uint64_t bit = 1ull << (dev & 63);
       if (!(allowed.load() & bit)) {
         if (hipError_t e = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&w4a16_tgemm_kernel<1, NTW, GPU, true>),
+                reinterpret_cast<const void*>(&w4a16_tgemm_kernel<1, NTW, GPU, true, RNG>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, kXGLds);
             e != hipSuccess)
           return e;
@@ -493,12 +534,12 @@ hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stre
       }
       const size_t need = (size_t)a.M * (2 * a.K + 16) + 4 * (size_t)a.K;
       const size_t red = (size_t)kKW * NTW * 64 * 16;
-      hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW, GPU, true>), dim3(c.grid), block,
+      hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW, GPU, true, RNG>), dim3(c.grid), block,
                          need > red ? need : red, stream, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU, false>), dim3(c.grid), block, 0, stream, a);
+  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU, false, RNG>), dim3(c.grid), block, 0, stream, a);
   return hipGetLastError();
 }
 
@@ -511,6 +552,15 @@ hipError_t launch_gpu(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stre
 
 template <int MT>
 hipError_t launch_mt(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
+  if constexpr (MT == 1) {
+    if (c.rng) {
+      switch (c.ntw) {
+        case 5: return launch_cfg<1, 5, 1, true>(c, a, stream);
+        case 6: return launch_cfg<1, 6, 1, true>(c, a, stream);
+        default: return hipErrorInvalidValue;
+      }
+    }
+  }
   if (c.ntw == 4) return launch_gpu<MT, 4>(c, a, stream);
   if (c.ntw == 2) return launch_gpu<MT, 2>(c, a, stream);
   return launch_gpu<MT, 1>(c, a, stream);
@@ -527,9 +577,10 @@ bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
          ((N + 63) / 64 * 4 + 8) * ((M + 15) / 16) < (1ll << 31);  // workgroups
 }
 
-TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {
+TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gather) {
   TgemmConfig c;
   c.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  c.rng = false;
   // the most rows per workgroup that still give about one workgroup per CU
   const int64_t cus = device_cu_count();
   const int64_t panels = (N + 63) / 64;
@@ -538,6 +589,24 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K) {
   static const int env_ntw = [] { const char* e = getenv("PMI_TGEMM_NTW"); return e ? atoi(e) : 0; }();
   if (env_ntw == 1 || env_ntw == 2 || env_ntw == 4) c.ntw = env_ntw;
   c.n_wg = (int)(panels * (4 / c.ntw));
+  // Up to 16 rows with more panels than CUs: ranges of 5 or 6 consecutive
+  // 16-row tiles per workgroup, so that one pass over the CUs covers every
+  // tile. Measured on Qwen gate/up 18944 x 3584: with the act_order gather
+  // (whose LDS keeps one workgroup per CU) 13.3 against 19.2 us at M = 16 and
+  // 12.4 against 14.0 at M = 4; without it 13.6 against 15.0 at M = 16 and
+  // 12.7 against 13.0 at M = 8, but 13.9 against 12.6 at M = 4, where two
+  // workgroups per CU already share the passes. Ranges of 7 (fused gate/up
+  // 28672 rows) measured slower than two passes (18.6 against 15.5 at M = 8).
+  static const int env_rng = [] { const char* e = getenv("PMI_TGEMM_RANGE"); return e ? atoi(e) : -1; }();
+  if (c.mt == 1 && gs % 128 == 0 && panels > cus && env_rng != 0 && (gather || M >= 8)) {
+    const int64_t tiles = 4 * panels;
+    const int64_t per = (tiles + cus - 1) / cus;
+    if (per <= 6) {
+      c.rng = true;
+      c.ntw = (int)(per < 5 ? 5 : per);
+      c.n_wg = (int)((tiles + c.ntw - 1) / c.ntw);
+    }
+  }
   c.grid_m = (int)((M + 16 * c.mt - 1) / (16 * c.mt));
   c.grid = c.grid_m == 1 ? c.n_wg : (int)((c.n_wg + 7) / 8 * 8 * c.grid_m);
   (void)K;
@@ -552,7 +621,7 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
                         const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
                         int64_t N, int64_t K, int64_t gs, hipStream_t stream) {
   if (perm && !tgemm_gather_supported(M, K)) return hipErrorInvalidValue;
-  const TgemmConfig c = tgemm_config(M, N, K);
+  const TgemmConfig c = tgemm_config(M, N, K, gs, perm != nullptr);
   TgemmArgs a;
   a.x = (const f16*)x;
   a.perm = perm;
@@ -566,6 +635,7 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   a.gs = (int)gs;
   a.n_wg = c.n_wg;
   a.grid_m = c.grid_m;
+  a.n_tiles = (int)(4 * ((N + 63) / 64));
   if (c.mt == 1) return launch_mt<1>(c, a, stream);
   if (c.mt == 2) return launch_mt<2>(c, a, stream);
   return launch_mt<4>(c, a, stream);

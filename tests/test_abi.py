@@ -70,7 +70,8 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(8, 512, 3584, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(4, 1024, 4096, 128, 1) == 1     # narrow at 4 rows: GEMV
     assert L.pmi_matmul_kernel_choice(16, 28672, 4096, 128, 1) != 5   # more than one pass at 16 rows
-    assert L.pmi_matmul_kernel_choice(16, 18944, 3584, 128, 1) != 5
+    assert L.pmi_matmul_kernel_choice(16, 18944, 3584, 128, 1) == 5   # tile ranges: one pass
+    assert L.pmi_matmul_kernel_choice(16, 18944, 3584, 128, 3) == 5
     # act_order (PMI_CHOICE_PERM): the in-kernel gather up to 16 rows where X
     # and the perm table fit LDS
     TP = _lib.PMI_CHOICE_TILED | _lib.PMI_CHOICE_PERM

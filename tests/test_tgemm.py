@@ -290,3 +290,14 @@ def test_tgemm_in_kernel_gather_equals_pregathered(M, N, K):
                                   zu8.contiguous(), sz, wt, None, gs)
     torch.cuda.synchronize()
     assert torch.equal(y_in.view(torch.int16), y_pre.view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,act_order", [
+    (16, 18944, 3584, False), (5, 18944, 3584, False), (16, 18944, 3584, True), (3, 18944, 3584, True),
+    (8, 28672, 4096, False), (12, 20004, 1536, False), (16, 16448, 2048, False), (7, 16448, 2048, True)])
+def test_tgemm_tile_ranges(M, N, K, act_order):
+    """Up to 16 rows with more 64-row panels than CUs, each workgroup takes a
+    range of 5-8 consecutive 16-row tiles (ragged N, and the in-kernel act_order
+    gather, included)."""
+    _tgemm_case(M, N, K, 128, seed=N % 101 + M, act_order=act_order, no_workspace=True)
