@@ -192,6 +192,14 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
     if (gathers ? (M >= 3 || N >= 3072) : (M >= 5 || (M >= 3 && N >= 3072) || (N >= 8192 && N <= 20480)))
       return 5;
   }
+  // Past 64 rows on narrow layers, while the tiled GEMM's 64-row blocks still
+  // take one pass over the CUs: against the register-streamed GEMM, whose K
+  // splits these layers need, k/v 1024 x 4096 at M = 256 takes 10.3 against
+  // 17.0 us and 512 x 3584 at M = 512 takes 9.5 against 15.9 us; with a second
+  // pass it loses (1024 x 4096 at M = 512: 19.4 against 16.3 us).
+  if (has_tiled && M > 64 && K <= 8192 && pmi::tgemm_supported(M, N, K, group_size) &&
+      pmi::tgemm_config(M, N, K, group_size, false).grid <= cus)
+    return 5;
   // Group sizes 32 and 64 have no other matrix-core kernel: past 4 rows the
   // tiled GEMM (one activation block of 32 rows after another) replaces the
   // GEMV, which would stream the weights once per 4 rows.

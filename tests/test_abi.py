@@ -58,6 +58,11 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128, 1) == 5   # 64-row blocks
     assert L.pmi_matmul_kernel_choice(65, 14336, 4096, 128, 1) != 5   # past 64 rows
     assert L.pmi_matmul_kernel_choice(64, 28672, 4096, 128, 1) != 5   # more than one pass
+    assert L.pmi_matmul_kernel_choice(256, 1024, 4096, 128, 1) == 5   # narrow: 64-row blocks, one pass
+    assert L.pmi_matmul_kernel_choice(512, 512, 3584, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(512, 1024, 4096, 128, 1) != 5   # two passes
+    assert L.pmi_matmul_kernel_choice(96, 3584, 3584, 128, 1) != 5
+    assert L.pmi_matmul_kernel_choice(128, 1024, 14336, 128, 1) != 5  # K > 8192
     assert L.pmi_matmul_kernel_choice(8, 28672, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64, 1) == 5    # gs 64: tiled GEMM past 4 rows
     assert L.pmi_matmul_kernel_choice(512, 4096, 4096, 32, 1) == 5

@@ -183,6 +183,17 @@ def test_tgemm_rows(M):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,act_order", [(256, 1024, 4096, False), (512, 512, 3584, False),
+                                             (129, 1024, 4096, True), (200, 520, 3584, False)])
+def test_tgemm_narrow_many_rows(M, N, K, act_order):
+    """Narrow layers past 64 rows, where dispatch picks the tiled GEMM while its
+    64-row blocks take one pass over the CUs (act_order: X[:, perm] gathered
+    into the workspace first)."""
+    assert P.kernel_choice(M, N, K, 128, tiled=True, perm=act_order) == "tgemm"
+    _tgemm_case(M, N, K, 128, seed=M + N, kernel="auto", act_order=act_order)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 4096), (6144, 4096), (3584, 3584),
                                  (1028, 1536), (200, 2560), (4100, 2048)])
 @pytest.mark.parametrize("M", [4, 16, 32, 64])
