@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 11
+#define PMI_ABI_VERSION 12
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -131,7 +131,7 @@ PMI_API size_t pmi_tiled_bytes(int64_t N, int64_t K);
 
 /* Kernel-layout weight (group size group_size, act_order permutation already
  * applied) -> tiled copy for the tiled-weight GEMM that pmi_matmul_w4a16 runs
- * for 3..32 activation rows: for every 64-row panel p and 128-column unit u
+ * for 2..64 activation rows: for every 64-row panel p and 128-column unit u
  * one 4 KiB block of 4 tiles x 64 lanes x 16 bytes; lane n + 16h of tile j
  * holds row 64p + 4n + j, and its byte b carries columns 128u + (b < 8 ?
  * 8h + b : 32 + 8h + b - 8) (low nibble) and that + 64 (high nibble); rows
@@ -153,9 +153,9 @@ PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N,
  * group) instead of gathering [N,G] rows when N % 4 == 0. The other kernels
  * read scales and zeros.
  * w_tiled (nullable): the pmi_tile_w4a16 copy of w. With it (and scales_gm,
- * zeros_gm) 3..32 activation rows run on the tiled-weight GEMM where that
- * wins (pmi_matmul_kernel_choice 5); without it those rows take the other
- * kernels.
+ * zeros_gm) 2..64 activation rows (more on narrow layers) run on the
+ * tiled-weight GEMM where that wins (pmi_matmul_kernel_choice 5); without it
+ * those rows take the other kernels.
  * workspace (nullable when workspace_bytes == 0): device scratch of
  * pmi_matmul_workspace_bytes() bytes, 256-byte aligned, zero-filled before
  * its first use; every call leaves it zero-filled again (it holds split-K
@@ -301,15 +301,23 @@ PMI_API int pmi_gptq_pack(const uint8_t* codes, const int32_t* inv_perm, uint8_t
 /* Which kernel pmi_matmul_w4a16 would run for this shape: 1 = split-K GEMV,
  * 2 = MFMA GEMM (group_size % 128 == 0 and K % 256 == 0), 3 = skinny MFMA
  * kernel (M <= 16), 4 = register-streamed MFMA GEMM (group_size == 128,
- * K % 512 == 0), 5 = tiled-weight MFMA GEMM (M <= 32, K % 512 == 0,
- * K >= 1536, N % 4 == 0, group_size 32, 64 or a multiple of 128; needs the
- * w_tiled copy, so it is chosen only with PMI_CHOICE_TILED in flags; with
- * PMI_CHOICE_PERM as well, up to 16 rows it gathers X[:, perm] itself when
- * M (2K + 16) + 4K bytes fit its LDS, which widens where it wins). flags 0
- * and 1 keep the meaning of the former has_tiled argument. Host-only; no
- * reference counterpart (the reference has one Triton kernel). */
+ * K % 512 == 0), 5 = tiled-weight MFMA GEMM (K % 512 == 0, K >= 1536,
+ * N % 4 == 0, group_size 32, 64 or a multiple of 128; needs the w_tiled copy,
+ * so it is chosen only with PMI_CHOICE_TILED in flags; with PMI_CHOICE_PERM
+ * as well, up to 16 rows it gathers X[:, perm] itself when M (2K + 16) + 4K
+ * bytes fit its LDS, which widens where it wins). flags 0 and 1 keep the
+ * meaning of the former has_tiled argument. Host-only; no reference
+ * counterpart (the reference has one Triton kernel). */
 PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size,
                                      int flags);
+
+/* The K ranges the tiled-weight GEMM (kernel 5) splits this shape into when
+ * the call has a workspace of pmi_matmul_workspace_bytes() bytes: up to 16
+ * rows on layers whose weight workgroups fill at most half of the CUs, each
+ * range on its own workgroup, the last to finish adding the fp32 partial
+ * tiles in range order; 1 = unsplit (always without a workspace). has_perm:
+ * an act_order perm. Host-only diagnostic; no reference counterpart. */
+PMI_API int pmi_tgemm_splits(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm);
 
 /* Forces pmi_matmul_w4a16 onto one kernel (1 to 5 as above; 0 restores the
  * automatic choice) for every thread of the process; returns the previous

@@ -311,11 +311,20 @@ int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N, int64_t
   return from_hip(pmi::launch_tile(w_kernel, w_tiled, N, K, group_size, (hipStream_t)stream), fn);
 }
 
-size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
-                                  int has_perm) {
-  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
-  // the tiled GEMM, when a caller has the tiled copy, needs only the act_order
-  // gather of X, which every kernel's figure below already covers
+namespace {
+
+// Workspace of the tiled GEMM (when a caller has the tiled copy): the act_order
+// gather of X where the kernel does not gather itself, and the split-K
+// partial tiles after it.
+size_t tgemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size, bool has_perm) {
+  if (!pmi::tgemm_supported(M, N, K, group_size)) return 0;
+  const bool gathers = has_perm && pmi::tgemm_gather_supported(M, K);
+  const size_t xg = has_perm && !gathers ? pmi::ws_perm_bytes(M, K) : 0;
+  const size_t split = pmi::tgemm_config(M, N, K, group_size, gathers).ws_split;
+  return xg + split ? pmi::kWsCounterBytes + xg + split : 0;
+}
+
+size_t other_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm) {
   const int choice = pmi_matmul_kernel_choice(M, N, K, group_size, 0);
   if (choice == 2 && pmi::gemm_supported(K, group_size))
     return pmi::gemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
@@ -334,6 +343,24 @@ size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
   if (has_perm && pmi::tgemm_supported(M, N, K, group_size))
     return pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
   return 0;
+}
+
+}  // namespace
+
+int pmi_tgemm_splits(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0 ||
+      !pmi::tgemm_supported(M, N, K, group_size))
+    return 1;
+  return pmi::tgemm_config(M, N, K, group_size, has_perm && pmi::tgemm_gather_supported(M, K)).splits;
+}
+
+size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                  int has_perm) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
+  // enough for whichever kernel runs, with or without the tiled copy
+  const size_t other = other_workspace_bytes(M, N, K, group_size, has_perm);
+  const size_t tiled = tgemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
+  return other > tiled ? other : tiled;
 }
 
 int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype, float* scales_gm,
@@ -391,19 +418,24 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   if (choice == 5) {
     if (!has_tiled || !pmi::tgemm_supported(M, N, K, group_size))
       return fail(PMI_ERR_UNSUPPORTED, "%s: the tiled GEMM needs w_tiled, scales_gm and zeros_gm, "
-                  "M <= 32, N %% 4 == 0, K %% 512 == 0, K >= 1536 and group_size 32, 64 or a "
+                  "N %% 4 == 0, K %% 512 == 0, K >= 1536 and group_size 32, 64 or a "
                   "multiple of 128", fn);
     // act_order: up to 16 rows the kernel gathers X[:, perm] itself (from
     // LDS); past that X[:, perm] is gathered into the workspace first
+    // (the split-K partial tiles follow the counters, or the gathered X)
+    void* ws = workspace_bytes >= pmi::kWsCounterBytes ? workspace : nullptr;
     if (!perm || pmi::tgemm_gather_supported(M, K))
       return from_hip(pmi::launch_tgemm(x, perm, w_tiled, scales_gm, zeros_gm, y, M, N, K,
-                                        group_size, s), fn);
+                                        group_size, ws, workspace_bytes, pmi::kWsCounterBytes, s),
+                      fn);
     if (workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
       void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
       hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
       if (e != hipSuccess) return from_hip(e, fn);
       return from_hip(pmi::launch_tgemm(xg, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N, K,
-                                        group_size, s), fn);
+                                        group_size, ws, workspace_bytes,
+                                        pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K), s),
+                      fn);
     }
     if (forced) return fail(PMI_ERR_UNSUPPORTED, "%s: forced tiled GEMM with perm needs a "
                             "workspace of pmi_matmul_workspace_bytes() bytes", fn);

@@ -36,7 +36,9 @@ struct TgemmConfig {
   bool rng;    // ntw consecutive tiles per workgroup across panels (up to 16 rows)
   int n_wg;    // weight workgroups
   int grid_m;  // activation blocks
+  int splits;  // K ranges per weight workgroup (up to 16 rows on narrow layers), else 1
   int grid;    // workgroups
+  size_t ws_split;  // workspace bytes of the split-K partial tiles (0 unsplit)
 };
 
 struct SkinnyConfig {
@@ -217,9 +219,12 @@ bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 constexpr int kTgemmXGLds = 160 * 1024 - 1024;
 bool tgemm_gather_supported(int64_t M, int64_t K);
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gather);
-// perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null
+// perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null.
+// workspace: counters (zero between calls) at its start and the split-K partial
+// tiles at part_offset; null or too small for them, the kernel runs unsplit.
 hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
                         const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
-                        int64_t N, int64_t K, int64_t gs, hipStream_t stream);
+                        int64_t N, int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
+                        size_t part_offset, hipStream_t stream);
 
 }  // namespace pmi

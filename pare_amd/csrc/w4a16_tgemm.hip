@@ -19,12 +19,14 @@
 // high nibbles, so every step lies inside one group of 32, 64 or 128 columns
 // and the per-group scale applies after the steps of its group.
 //
-// Work layout. No K split: a workgroup owns NTW 16-row tiles of one panel
-// (16 NTW weight rows) for all activation rows and the whole K range, so no
-// partial tiles cross workgroups. Its four compute waves take the units
-// u = 4 s + w (w = wave) and are added through LDS at the end; the four waves
-// of a workgroup read four consecutive blocks at every step. NTW is the
-// largest of 4, 2, 1 that still gives about a workgroup per CU.
+// Work layout. A workgroup owns NTW 16-row tiles of one panel (16 NTW weight
+// rows) for all activation rows and the whole K range. Its four compute waves
+// take the units u = 4 s + w (w = wave) and are added through LDS at the end;
+// the four waves of a workgroup read four consecutive blocks at every step.
+// NTW is the largest of 4, 2, 1 that still gives about a workgroup per CU.
+// Only narrow layers at 9-16 rows, whose tiles leave half of the CUs idle,
+// split K: 2-4 workgroups per tile take ranges of unit quads, and the last to
+// finish adds the fp32 partial tiles in range order (combine_splits).
 //
 // Activations. Up to 16 rows (MT = 1) every compute wave loads the A operands
 // of its own units with the weights (16 rows x 256 bytes per unit, L2
@@ -88,6 +90,9 @@ struct TgemmArgs {
   int n_wg;    // weight workgroups (16 NTW rows each)
   int grid_m;  // activation blocks of 16 MT rows
   int n_tiles; // RNG: 16-row tiles (4 per 64-row panel)
+  int splits;  // K ranges per weight workgroup (MT = 1, one activation block), else 1
+  int* counters;  // splits > 1: one per weight workgroup, zero between calls
+  float* part;    // splits > 1: [n_wg][splits][NTW] partial 16 x 16 fp32 tiles
 };
 
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
@@ -102,6 +107,44 @@ struct Unit {
   float sr[RNG ? NTW : 1];
   uint32_t zr[RNG ? NTW : 1];
 };
+
+// K split (one 16-row weight tile per workgroup): the partial tile of split sp
+// goes to the workspace; the last split of weight workgroup wg to arrive adds
+// all of them in split order (so the result does not depend on the arrival
+// order) and returns true with the sum in `sum`. Stores and loads carry the
+// device-scope cache policy (sc1), as agent-scope atomics do, so they are
+// coherent across the XCDs' L2 caches without a release fence: the stores
+// complete (s_waitcnt) before the counter increment, and the last split loads
+// only after its increment has returned the count. All kMaxSplits loads are
+// issued together (one round trip; past the last split they re-read it).
+constexpr int kMaxSplits = 4;
+__device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int sp, int l, f32x4& sum) {
+  constexpr int kTile = 1024;  // bytes of a 16 x 16 fp32 tile
+  constexpr int kSc1 = 16;
+  const __amdgpu_buffer_rsrc_t rp =
+      rsrc(a.part + (size_t)wg * a.splits * (kTile / 4), (int64_t)a.splits * kTile);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), rp, 16 * l,
+                                         __builtin_amdgcn_readfirstlane(sp * kTile), kSc1);
+  __builtin_amdgcn_s_waitcnt(0);
+  int old = 0;
+  if (l == 0)
+    old = __hip_atomic_fetch_add(&a.counters[wg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old != a.splits - 1) return false;
+  f32x4 v[kMaxSplits];
+#pragma unroll
+  for (int q = 0; q < kMaxSplits; ++q) {
+    const int qq = q < a.splits ? q : a.splits - 1;
+    v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rp, 16 * l, __builtin_amdgcn_readfirstlane(qq * kTile), kSc1));
+  }
+  sum = v[0];
+#pragma unroll
+  for (int q = 1; q < kMaxSplits; ++q)
+    if (q < a.splits) sum += v[q];
+  if (l == 0) __hip_atomic_store(&a.counters[wg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
 
 // RNG: the workgroup takes NTW consecutive 16-row tiles t0 = wg NTW .. of the
 // 4 n_panels tiles (5 or 6 of them, so that one pass over the CUs covers more
@@ -141,8 +184,13 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // round-robin by index, so the activation blocks of one weight workgroup
   // are numbered 8 apart: they share an XCD, and the second read of its
   // weights mostly hits that XCD's L2 (a placement preference only).
-  int wg = blockIdx.x, mb = 0;
-  if (a.grid_m > 1) {
+  int wg = blockIdx.x, mb = 0, sp = 0;
+  if (MT == 1 && NTW == 1 && !RNG && a.splits > 1) {
+    // K split (one activation block): the splits of a weight workgroup are
+    // consecutive blocks
+    wg = blockIdx.x / a.splits;
+    sp = blockIdx.x - wg * a.splits;
+  } else if (a.grid_m > 1) {
     const int span = 8 * a.grid_m;
     const int q = blockIdx.x / span, r = blockIdx.x % span;
     wg = 8 * q + (r & 7);
@@ -153,8 +201,13 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // padding workgroups: past the weight workgroups, or past the last rows (uniform)
   if (wg >= a.n_wg || (!RNG && 64 * panel + jb >= N)) return;
   const int m0 = mb * BM;  // first activation row of this block
-  const int U = K >> 7;              // units
-  const int steps = (U + kKW - 1) / kKW;
+  const int U = K >> 7;              // units (U % 4 == 0)
+  // steps of this workgroup: the unit quads q_lo .. q_lo + steps - 1 (all of
+  // them unsplit; split sp takes quads Q sp / splits .. Q (sp + 1) / splits - 1)
+  const int Q = U / kKW;
+  const bool split = MT == 1 && NTW == 1 && !RNG && a.splits > 1;
+  const int q_lo = split ? sp * Q / a.splits : 0;
+  const int steps = split ? (sp + 1) * Q / a.splits - q_lo : Q;
   const int ln = l & 15, h = l >> 4;
   const int row0 = 64 * panel + 4 * ln + jb;  // first of the lane's NTW rows
   // RNG: tile j of the range (clamped to the last tile), its lane row and the
@@ -270,8 +323,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     uint32_t poff[GATHER ? 32 : 1], graw[GATHER ? 32 : 1];
     auto table_read = [&](int s) {
       if constexpr (GATHER) {
-        int u = kKW * s + kw;
-        u = u < U ? u : U - 1;
+        const int u = kKW * (q_lo + (s < steps ? s : steps - 1)) + kw;
         const uint8_t* pt = lds + xtab + (u * 128 + 8 * h) * 4;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -297,8 +349,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       }
     };
     auto issue = [&](UnitT& un, int s) {
-      int u = kKW * s + kw;
-      u = u < U ? u : U - 1;
+      // past the range: re-read the wave's last unit (loaded, never computed)
+      const int u = kKW * (q_lo + (s < steps ? s : steps - 1)) + kw;
       const int uu = __builtin_amdgcn_readfirstlane(u);
       if constexpr (MT == 1 && !GATHER) {
 #pragma unroll
@@ -429,10 +481,10 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         compute(un, xb, 1);
       }
     };
-    // Whole rounds of kDW steps, then a tail already in flight. The host
-    // guarantees steps >= kDW.
+    // Whole rounds of kDW steps, then a tail already in flight (a K split may
+    // leave fewer than kDW steps: then only the tail).
     int s0 = 0;
-    do {
+    if (steps >= kDW) do {
 #pragma unroll
       for (int d = 0; d < kDW; ++d) {
         issue(ring[(d + kDW - 1) % kDW], s0 + d + kDW - 1);
@@ -475,7 +527,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       for (int j = 0; j < NTW; ++j) red[((wv * MT + mt) * NTW + j) * 64 + l] = acc[mt][j];
   }
   __syncthreads();
-  if (wv >= kKW || (!RNG && row0 >= N)) return;
+  if (wv >= kKW) return;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     if ((MT == 1 ? 0 : mt % kKW) != wv) continue;
@@ -486,6 +538,10 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 #pragma unroll
       for (int k = 1; k < kKW; ++k) sum[j] += red[((k * MT + mt) * NTW + j) * 64 + l];
     }
+    if constexpr (MT == 1 && !RNG && NTW == 1) {
+      if (split && !combine_splits(a, wg, sp, l, sum[0])) return;
+    }
+    if (!RNG && row0 >= N) return;
     // lane (n, h): rows 16 mt + 4 h + i of the activations, weight rows row0 + j
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -609,7 +665,28 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   }
   c.grid_m = (int)((M + 16 * c.mt - 1) / (16 * c.mt));
   c.grid = c.grid_m == 1 ? c.n_wg : (int)((c.n_wg + 7) / 8 * 8 * c.grid_m);
-  (void)K;
+  // 9-16 rows with the weight workgroups on at most half of the CUs (narrow
+  // layers): split K into ranges of whole unit quads, as many as fit one pass
+  // over the CUs, at most kMaxSplits; the last split of each workgroup adds the
+  // partial tiles. Measured on MI355X at M = 16 (us, unsplit -> split): 512 x
+  // 3584 6.6 -> 5.6 (4 splits; act_order 8.1 -> 7.5), 1024 x 4096 7.0 -> 6.3
+  // (4), 2048 x 4096 7.0 -> 6.5 (2), 512 x 8192 11.4 -> 6.9 (4). The combine
+  // costs about three device-scope round trips: 7 or 8 one-quad splits were
+  // slower than 4 (512 x 3584: 6.8), and at 8 rows no split gained.
+  c.splits = 1;
+  c.ws_split = 0;
+  static const int env_split = [] { const char* e = getenv("PMI_TGEMM_SPLIT"); return e ? atoi(e) : -1; }();
+  if (c.mt == 1 && !c.rng && c.ntw == 1 && env_split != 0 && (M > 8 || env_split > 0) &&
+      c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
+    int64_t s = env_split > 0 ? env_split : cus / c.n_wg;
+    if (s > (K >> 9)) s = K >> 9;
+    if (s > kMaxSplits) s = kMaxSplits;
+    if (s >= 2) {
+      c.splits = (int)s;
+      c.grid = c.n_wg * c.splits;
+      c.ws_split = ws_align((size_t)c.n_wg * c.splits * 1024);
+    }
+  }
   return c;
 }
 
@@ -619,9 +696,14 @@ bool tgemm_gather_supported(int64_t M, int64_t K) {
 
 hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
                         const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
-                        int64_t N, int64_t K, int64_t gs, hipStream_t stream) {
+                        int64_t N, int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
+                        size_t part_offset, hipStream_t stream) {
   if (perm && !tgemm_gather_supported(M, K)) return hipErrorInvalidValue;
-  const TgemmConfig c = tgemm_config(M, N, K, gs, perm != nullptr);
+  TgemmConfig c = tgemm_config(M, N, K, gs, perm != nullptr);
+  if (c.splits > 1 && (!workspace || ws_bytes < part_offset + c.ws_split)) {
+    c.splits = 1;
+    c.grid = c.n_wg;
+  }
   TgemmArgs a;
   a.x = (const f16*)x;
   a.perm = perm;
@@ -636,6 +718,9 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   a.n_wg = c.n_wg;
   a.grid_m = c.grid_m;
   a.n_tiles = (int)(4 * ((N + 63) / 64));
+  a.splits = c.splits;
+  a.counters = (int*)workspace;
+  a.part = c.splits > 1 ? (float*)((uint8_t*)workspace + part_offset) : nullptr;
   if (c.mt == 1) return launch_mt<1>(c, a, stream);
   if (c.mt == 2) return launch_mt<2>(c, a, stream);
   return launch_mt<4>(c, a, stream);

@@ -299,3 +299,9 @@ def kernel_choice(M: int, N: int, K: int, group_size: int, tiled: bool = False,
     flags = (_lib.PMI_CHOICE_TILED if tiled else 0) | (_lib.PMI_CHOICE_PERM if perm else 0)
     c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size, flags)
     return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64", 5: "tgemm"}[c]
+
+
+def tgemm_splits(M: int, N: int, K: int, group_size: int, perm: bool = False) -> int:
+    """K ranges the tiled GEMM splits this shape into when matmul_w4a16 runs it
+    (1: unsplit)."""
+    return _lib.lib().pmi_tgemm_splits(M, N, K, group_size, int(perm))

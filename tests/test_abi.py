@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == _lib.ABI_VERSION == 11
+    assert L.pmi_abi_version() == _lib.ABI_VERSION == 12
 
 
 def test_kernel_choice(L):
@@ -118,6 +118,25 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(8, 14336, 2048, 128, 0) == 2    # skinny only for N <= 8192
     assert L.pmi_matmul_kernel_choice(5, 4096, 2048, 128, 0) == 3
     assert L.pmi_matmul_workspace_bytes(32, 4096, 384, 128, 0) == 0
+
+
+def test_tgemm_splits(L):
+    # K ranges of the tiled GEMM at 9..16 rows where its workgroups fill at most
+    # half of the 256 CUs: as many as fit one pass, at most 4, one unit quad each
+    assert L.pmi_tgemm_splits(16, 512, 3584, 128, 0) == 4    # 32 workgroups
+    assert L.pmi_tgemm_splits(16, 512, 3584, 128, 1) == 4    # act_order (in-kernel gather)
+    assert L.pmi_tgemm_splits(16, 1024, 4096, 128, 0) == 4   # 64 workgroups
+    assert L.pmi_tgemm_splits(12, 2048, 4096, 128, 0) == 2   # 128 workgroups
+    assert L.pmi_tgemm_splits(16, 512, 1536, 128, 0) == 3    # 3 quads
+    assert L.pmi_tgemm_splits(9, 200, 8192, 32, 0) == 4
+    assert L.pmi_tgemm_splits(8, 512, 3584, 128, 0) == 1     # up to 8 rows: unsplit
+    assert L.pmi_tgemm_splits(16, 3584, 3584, 128, 0) == 1   # 224 workgroups: unsplit
+    assert L.pmi_tgemm_splits(17, 512, 3584, 128, 0) == 1    # past 16 rows: unsplit
+    assert L.pmi_tgemm_splits(16, 512, 1000, 128, 0) == 1    # not a tiled GEMM shape
+    # the workspace covers the partial tiles (1 KiB per workgroup and split)
+    # after the counter block
+    assert L.pmi_matmul_workspace_bytes(16, 512, 3584, 128, 0) >= 64 * 1024 + 32 * 4 * 1024
+    assert L.pmi_matmul_workspace_bytes(16, 1024, 4096, 128, 1) >= 64 * 1024 + 64 * 4 * 1024
 
 
 def test_kernel_override(L):

@@ -1,4 +1,4 @@
-"""The tiled weight layout and the tiled-weight GEMM (3..32 activation rows).
+"""The tiled weight layout and the tiled-weight GEMM (2..64 activation rows, more on narrow layers).
 
 Layout: pmi_tile_w4a16 is checked byte for byte against a numpy restatement of
 its documented mapping, written from the quantisation codes (not from the
@@ -17,7 +17,7 @@ import torch
 import pare_amd as P
 from oracle import pare_oracle as O
 from pare_amd import _lib
-from pare_amd.kernels import force_kernel
+from pare_amd.kernels import force_kernel, tgemm_splits
 
 DEV = "cuda"
 RTOL = ATOL = 1e-2
@@ -180,6 +180,38 @@ def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False, no_workspace
 @pytest.mark.parametrize("M", [1, 3, 5, 8, 16, 17, 24, 32, 33, 47, 64, 65, 100])
 def test_tgemm_rows(M):
     _tgemm_case(M, 1024, 2048, 128, seed=10 + M)
+
+
+SPLIT_CASES = [
+    # (M, N, K, gs, act_order): narrow layers at 9..16 rows, K split over
+    # workgroups (even and uneven quads per split, one quad per split, ragged
+    # N, gs 32 / 64 / 256 and act_order with the in-kernel gather)
+    (16, 512, 3584, 128, False), (16, 512, 3584, 128, True), (16, 1024, 4096, 128, False),
+    (16, 1024, 3584, 128, True), (12, 2048, 4096, 128, False), (9, 512, 1536, 128, False),
+    (12, 200, 2048, 32, False), (16, 1028, 3072, 64, False), (10, 512, 3584, 256, False),
+    (16, 520, 8192, 128, False), (9, 512, 3584, 128, True), (13, 1024, 4096, 128, True)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,gs,act_order", SPLIT_CASES)
+def test_tgemm_split_k(M, N, K, gs, act_order):
+    """The K split of narrow layers against the oracle; the same call twice
+    gives the same bits (partials added in split order, whatever the arrival
+    order), and the unsplit run (no workspace) agrees to the tolerance."""
+    assert tgemm_splits(M, N, K, gs, perm=act_order) > 1
+    y = _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order)
+    y2 = _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order)
+    assert torch.equal(y, y2)
+    _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order, no_workspace=True)
+
+
+@pytest.mark.gpu
+def test_tgemm_split_k_counters_reset():
+    """Calls of different split counts and workgroup counts alternate on one
+    stream and one workspace: every call leaves the counters at zero."""
+    shapes = [(16, 512, 3584), (16, 1024, 4096), (12, 2048, 4096), (16, 512, 1536)]
+    for M, N, K in shapes + shapes[::-1]:
+        _tgemm_case(M, N, K, 128, seed=M + N + K)
 
 
 @pytest.mark.gpu
