@@ -1,10 +1,10 @@
 """Bounded determinism soak of the cross-workgroup combines.
 
-Four kernels finish with a last-workgroup combine: the split-K MFMA GEMM and
-the register-streamed GEMM (partial tiles + a per-tile counter), the split
-decode attention (per-split max/sum/P.V partials) and the argmax (per-chunk
+Five kernels finish with a last-workgroup combine: the split-K MFMA GEMM, the
+register-streamed GEMM and the tiled GEMM's K split of narrow layers (partial
+tiles + a per-tile counter), the split decode attention (per-split max/sum/P.V partials) and the argmax (per-chunk
 maxima). Each combine adds its partials in a fixed order, so every call must
-give the same bits. Here 240 calls over mixed shapes, interleaved so that one
+give the same bits. Here 320 calls over mixed shapes, interleaved so that one
 workspace serves them all in turn, are each compared bit for bit with the
 first result of their case; the test stops at the first mismatch. Every call
 is bounded (no kernel waits on another workgroup), so a failure is a wrong
@@ -19,7 +19,7 @@ import torch
 import pare_amd as P
 from pare_amd import _lib
 from pare_amd.decoder import argmax_into, decode_attention
-from pare_amd.kernels import force_kernel
+from pare_amd.kernels import force_kernel, tgemm_splits
 
 pytestmark = pytest.mark.gpu
 
@@ -51,6 +51,20 @@ def _matmul_case(kernel, M, N, K, seed):
     return f"{kernel} M={M} N={N} K={K}", run
 
 
+def _tgemm_split_case(M, N, K, seed):
+    wk, s, z = _layer(N, K, seed)
+    x = torch.randn(M, K, generator=torch.Generator(device=DEV).manual_seed(seed + 1),
+                    device=DEV).half()
+    sz = P.sz_group_major(s, z)
+    wt = P.tile_w4a16(wk, GS)
+    assert tgemm_splits(M, N, K, GS) > 1, f"tgemm M={M} N={N} K={K} must split K"
+
+    def run():
+        with force_kernel("tgemm"):
+            return P.matmul_w4a16(x, wk, s, z, GS, sz_gm=sz, w_tiled=wt)
+    return f"tgemm split M={M} N={N} K={K}", run
+
+
 def _attention_case(B, H, KV, L, p, seed):
     D = 128
     g = torch.Generator(device=DEV).manual_seed(seed)
@@ -78,6 +92,8 @@ def test_combines_are_deterministic_under_repetition():
         _matmul_case("gemm", 16, 4096, 4096, 1),
         _matmul_case("gemm", 64, 1024, 4096, 2),
         _matmul_case("gemm64", 64, 4096, 4096, 3),
+        _tgemm_split_case(16, 512, 3584, 7),
+        _tgemm_split_case(12, 2048, 4096, 8),
         _attention_case(4, 32, 8, 640, 639, 4),
         _attention_case(1, 32, 8, 2048, 1500, 5),
         _argmax_case(4, 128256, 6),
