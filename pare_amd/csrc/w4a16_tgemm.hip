@@ -636,6 +636,9 @@ bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gather) {
   TgemmConfig c;
   c.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  // tuning override (benchmark sweeps only)
+  static const int env_mt = [] { const char* e = getenv("PMI_TGEMM_MT"); return e ? atoi(e) : 0; }();
+  if ((env_mt == 1 || env_mt == 2 || env_mt == 4) && !gather) c.mt = env_mt;
   c.rng = false;
   // the most rows per workgroup that still give about one workgroup per CU
   const int64_t cus = device_cu_count();
@@ -643,6 +646,28 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   c.ntw = panels >= (cus * 3) / 4 ? 4 : (2 * panels >= (cus * 3) / 4 ? 2 : 1);
   // tuning override (benchmark sweeps only)
   static const int env_ntw = [] { const char* e = getenv("PMI_TGEMM_NTW"); return e ? atoi(e) : 0; }();
+  // Past 24 rows, 16-row activation blocks (MT = 1: activations straight from
+  // L2 into registers, no LDS ring or barriers; the blocks of one weight
+  // workgroup share an XCD, so its weights come from HBM once) wherever the
+  // blocks and the weight workgroups fit one pass over the CUs, with the
+  // narrowest weight tiles that do. Against the 32- and 64-row LDS-ring
+  // kernels (us): 4096 x 4096 at M = 32 / 48 / 64 7.3 / 8.6 / 8.6 against 8.5 /
+  // 10.0 / 10.5; 2048 x 4096 at M = 64 7.4 against 9.7; 1024 x 4096 at M = 64 /
+  // 256 7.2 / 8.4 against 9.5 / 10.1. Where they do not fit (gate 14336 x 4096
+  // at M = 32 / 64: 15.8 / 26.3 against 11.8 / 14.7) the ring kernels stay,
+  // and at 17-24 rows, where the second block is mostly empty (4096 x 4096 at
+  // M = 17: 7.5 against 7.2; 3584 x 3584 at M = 24: 7.0 against 6.8).
+  if (M > 24 && !gather && env_mt == 0 && env_ntw == 0) {
+    const int64_t gm = (M + 15) / 16;
+    for (int ntw = 1; ntw <= 4; ntw *= 2) {
+      const int64_t n_wg = panels * (4 / ntw);
+      if ((n_wg + 7) / 8 * 8 * gm <= cus) {
+        c.mt = 1;
+        c.ntw = ntw;
+        break;
+      }
+    }
+  }
   if (env_ntw == 1 || env_ntw == 2 || env_ntw == 4) c.ntw = env_ntw;
   c.n_wg = (int)(panels * (4 / c.ntw));
   // Up to 16 rows with more panels than CUs: ranges of 5 or 6 consecutive
@@ -676,8 +701,8 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   c.splits = 1;
   c.ws_split = 0;
   static const int env_split = [] { const char* e = getenv("PMI_TGEMM_SPLIT"); return e ? atoi(e) : -1; }();
-  if (c.mt == 1 && !c.rng && c.ntw == 1 && env_split != 0 && (M > 8 || env_split > 0) &&
-      c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
+  if (c.mt == 1 && c.grid_m == 1 && !c.rng && c.ntw == 1 && env_split != 0 &&
+      (M > 8 || env_split > 0) && c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
     int64_t s = env_split > 0 ? env_split : cus / c.n_wg;
     if (s > (K >> 9)) s = K >> 9;
     if (s > kMaxSplits) s = kMaxSplits;
