@@ -80,8 +80,8 @@ class Buf:
         self._tiled = None
 
     def tiled(self):
-        """The tiled weight copy a module builds for 3..32 activation rows
-        (pack.tile_w4a16), where the shape supports it."""
+        """The tiled weight copy a module builds for the row counts the tiled GEMM
+        runs (pack.tile_w4a16), where the shape supports it."""
         import pare_amd as P
 
         if self._tiled is None and P.tiled_supported(self.N, self.K, GS):
@@ -399,12 +399,14 @@ def main():
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only",
-                    choices=["gate_up_m1", "gate_m64", "gate", "sweep", "read_floor", "copy", "e2e_bs1",
-                             "e2e_bs4"],
+                    choices=["gate_up_m1", "gate_m64", "gate", "sweep", "narrow", "read_floor", "copy",
+                             "e2e_bs1", "e2e_bs4"],
                     default=None,
                     help="run only one kernel loop (for rocprofv3 counter passes): gate_up_m1 "
                          "the fused gate/up GEMV; gate the gate_proj launches at --m rows "
-                         "(gate_m64: --m 64); read_floor the plain read of the gate/up weights; "
+                         "(gate_m64: --m 64); narrow the tiled GEMM on k/v at 16 rows (K split), "
+                         "q/o at 64 and k/v at 128 rows (16-row activation blocks); read_floor "
+                         "the plain read of the gate/up weights; "
                          "e2e_bs1 / e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens")
     ap.add_argument("--m", type=int, default=64, help="activation rows of --kernel-only gate")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoder leg")
@@ -511,6 +513,26 @@ def main():
                     gate_loop(stream.cuda_stream, M, 2 * n_layers)
                 torch.cuda.synchronize()
                 log(f"sweep M={M}: 320 launches, kernel {P.kernel_choice(M, 14336, 4096, GS, tiled=True)}")
+        return
+
+    if args.kernel_only == "narrow":
+        # the tiled GEMM's narrow-layer configurations, 5 x 64 launches each, in
+        # this order: k/v at 16 rows, q/o at 64 rows, k/v at 128 rows
+        for layer in single:
+            for i in range(4):
+                layer[i].tiled()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for M, idx in ((16, (1, 2)), (64, (0, 3)), (128, (1, 2))):
+                for _ in range(5):
+                    for layer in single:
+                        run(stream.cuda_stream, [layer[i] for i in idx], M)
+                torch.cuda.synchronize()
+                names = "/".join(LLAMA[i][0] for i in idx)
+                N = LLAMA[idx[0]][1]
+                log(f"narrow {names} M={M}: 320 launches, kernel "
+                    f"{P.kernel_choice(M, N, 4096, GS, tiled=True)}, "
+                    f"{P.kernels.tgemm_splits(M, N, 4096, GS)} K range(s)")
         return
 
     if args.kernel_only:
