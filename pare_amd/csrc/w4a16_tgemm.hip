@@ -65,6 +65,7 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "pmi_common.h"
 #include "pmi_launch.h"
@@ -98,14 +99,21 @@ struct TgemmArgs {
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
 // the GPU groups of the unit the NTW scales and zero points of the lane's rows
 // (RNG: one scale and zero point per tile, the tiles' rows are not adjacent).
+// The zero points stay as wide as their load (8 bits for one row, 16 for two)
+// and are widened where they are used: loaded into 32-bit ring registers,
+// the compiler narrowed the loop-carried copies and masked them before the
+// loop, a wait for every load in flight there (the whole ring drained before
+// the first step).
+template <int NTW>
+using ZeroT = std::conditional_t<NTW == 1, uint8_t, std::conditional_t<NTW == 2, uint16_t, uint32_t>>;
 template <int MT, int NTW, int GPU, bool RNG = false>
 struct Unit {
   u32x4 xa[MT == 1 ? 4 : 1];
   u32x4 w[NTW];
   f32x4 s[RNG ? 1 : GPU];
-  uint32_t z[RNG ? 1 : GPU];
+  ZeroT<NTW> z[RNG ? 1 : GPU];
   float sr[RNG ? NTW : 1];
-  uint32_t zr[RNG ? NTW : 1];
+  uint8_t zr[RNG ? NTW : 1];
 };
 
 // K split (one 16-row weight tile per workgroup): the partial tile of split sp
@@ -138,10 +146,15 @@ __device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int s
     v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                          rp, 16 * l, __builtin_amdgcn_readfirstlane(qq * kTile), kSc1));
   }
+  // the adds select rather than branch: behind a branch per split the
+  // compiler sank each load to its add, one round trip per split
+  __builtin_amdgcn_sched_barrier(0);
   sum = v[0];
 #pragma unroll
-  for (int q = 1; q < kMaxSplits; ++q)
-    if (q < a.splits) sum += v[q];
+  for (int q = 1; q < kMaxSplits; ++q) {
+    const f32x4 t = sum + v[q];
+    sum = q < a.splits ? t : sum;
+  }
   if (l == 0) __hip_atomic_store(&a.counters[wg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
 }
@@ -149,10 +162,13 @@ __device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int s
 // RNG: the workgroup takes NTW consecutive 16-row tiles t0 = wg NTW .. of the
 // 4 n_panels tiles (5 or 6 of them, so that one pass over the CUs covers more
 // than one 64-row panel per CU), the last ones clamped and not stored.
-template <int MT, int NTW, int GPU, bool GATHER, bool RNG>
+// SPLIT: a K range of a split weight workgroup (a.splits > 1); a variant of its
+// own, so that unsplit launches carry none of its index arithmetic.
+template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
   static_assert(!RNG || (MT == 1 && GPU == 1), "tile ranges are built for up to 16 rows, gs >= 128");
+  static_assert(!SPLIT || (MT == 1 && NTW == 1 && !RNG), "the K split is built for one 16-row tile");
   using UnitT = Unit<MT, NTW, GPU, RNG>;
   constexpr bool RING = MT > 1;
   // MT = 4: the ring holds half units (64 columns, k-steps 0-1 or 2-3), two
@@ -185,7 +201,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // are numbered 8 apart: they share an XCD, and the second read of its
   // weights mostly hits that XCD's L2 (a placement preference only).
   int wg = blockIdx.x, mb = 0, sp = 0;
-  if (MT == 1 && NTW == 1 && !RNG && a.splits > 1) {
+  if constexpr (SPLIT) {
     // K split (one activation block): the splits of a weight workgroup are
     // consecutive blocks
     wg = blockIdx.x / a.splits;
@@ -205,9 +221,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // steps of this workgroup: the unit quads q_lo .. q_lo + steps - 1 (all of
   // them unsplit; split sp takes quads Q sp / splits .. Q (sp + 1) / splits - 1)
   const int Q = U / kKW;
-  const bool split = MT == 1 && NTW == 1 && !RNG && a.splits > 1;
-  const int q_lo = split ? sp * Q / a.splits : 0;
-  const int steps = split ? (sp + 1) * Q / a.splits - q_lo : Q;
+  const int q_lo = SPLIT ? sp * Q / a.splits : 0;
+  const int steps = SPLIT ? (sp + 1) * Q / a.splits - q_lo : Q;
   const int ln = l & 15, h = l >> 4;
   const int row0 = 64 * panel + 4 * ln + jb;  // first of the lane's NTW rows
   // RNG: tile j of the range (clamped to the last tile), its lane row and the
@@ -411,7 +426,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         }
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
-          const uint32_t zq = RNG ? un.zr[j] & 0xFFu : (un.z[gp] >> (8 * j)) & 0xFFu;
+          const uint32_t zq = RNG ? (uint32_t)un.zr[j] : ((uint32_t)un.z[gp] >> (8 * j)) & 0xFFu;
           const f16x2 nz = as_f16x2(neg_magic_zero_x2(zq));
           const uint32_t w0 = un.w[j][2 * half], w1 = un.w[j][2 * half + 1];
           const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
@@ -458,9 +473,14 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       }
       // this wave's X copies have landed (only the ring's loads may still be
       // in flight) and its table writes are done; after the barrier so are
-      // every wave's
+      // every wave's. The scheduling fences keep step 0's unpacking below the
+      // barrier: hoisted above it, it made every wave wait for the first
+      // weight batch before the barrier, and the first gathers started only
+      // then (Qwen q_o 3584 x 3584, M = 16: 8.6 against 8.2 us).
+      __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt_lgkm0<(kDW - 1) * (RNG ? 3 * NTW : NTW + 2 * GPU)>();
       barrier_only();
+      __builtin_amdgcn_sched_barrier(0);
       table_read(0);
       gather_issue();
       table_read(1);
@@ -538,8 +558,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 #pragma unroll
       for (int k = 1; k < kKW; ++k) sum[j] += red[((k * MT + mt) * NTW + j) * 64 + l];
     }
-    if constexpr (MT == 1 && !RNG && NTW == 1) {
-      if (split && !combine_splits(a, wg, sp, l, sum[0])) return;
+    if constexpr (SPLIT) {
+      if (!combine_splits(a, wg, sp, l, sum[0])) return;
     }
     if (!RNG && row0 >= N) return;
     // lane (n, h): rows 16 mt + 4 h + i of the activations, weight rows row0 + j
@@ -570,33 +590,46 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   }
 }
 
+// Launches one kernel variant; GATHER variants get their dynamic LDS beyond
+// the 64 KiB default allowed once per variant and device.
+template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT>
+hipError_t launch_variant(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
+  const dim3 block((kKW + (MT == 1 ? 0 : kProd)) * 64);
+  size_t lds = 0;
+  if constexpr (GATHER) {
+    static std::atomic<uint64_t> allowed{0};
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(allowed.load() & bit)) {
+      if (hipError_t e = hipFuncSetAttribute(
+              reinterpret_cast<const void*>(&w4a16_tgemm_kernel<MT, NTW, GPU, true, RNG, SPLIT>),
+              hipFuncAttributeMaxDynamicSharedMemorySize, kXGLds);
+          e != hipSuccess)
+        return e;
+      allowed.fetch_or(bit);
+    }
+    const size_t need = (size_t)a.M * (2 * a.K + 16) + 4 * (size_t)a.K;
+    const size_t red = (size_t)kKW * NTW * 64 * 16;
+    lds = need > red ? need : red;
+  }
+  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU, GATHER, RNG, SPLIT>), dim3(c.grid), block, lds,
+                     stream, a);
+  return hipGetLastError();
+}
+
 template <int MT, int NTW, int GPU, bool RNG = false>
 hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
-  const dim3 block((kKW + (MT == 1 ? 0 : kProd)) * 64);
   if constexpr (MT == 1) {
-    if (a.perm) {
-      // dynamic LDS beyond the 64 KiB default: allowed once per variant and device
-      static std::atomic<uint64_t> allowed{0};
-      int dev = 0;
-      if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
-      const uint64_t bit = 1ull << (dev & 63);
-      if (!(allowed.load() & bit)) {
-        if (hipError_t e = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&w4a16_tgemm_kernel<1, NTW, GPU, true, RNG>),
-                hipFuncAttributeMaxDynamicSharedMemorySize, kXGLds);
-            e != hipSuccess)
-          return e;
-        allowed.fetch_or(bit);
+    if constexpr (NTW == 1 && !RNG) {
+      if (a.splits > 1) {
+        if (a.perm) return launch_variant<1, 1, GPU, true, false, true>(c, a, stream);
+        return launch_variant<1, 1, GPU, false, false, true>(c, a, stream);
       }
-      const size_t need = (size_t)a.M * (2 * a.K + 16) + 4 * (size_t)a.K;
-      const size_t red = (size_t)kKW * NTW * 64 * 16;
-      hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW, GPU, true, RNG>), dim3(c.grid), block,
-                         need > red ? need : red, stream, a);
-      return hipGetLastError();
     }
+    if (a.perm) return launch_variant<1, NTW, GPU, true, RNG, false>(c, a, stream);
   }
-  hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU, false, RNG>), dim3(c.grid), block, 0, stream, a);
-  return hipGetLastError();
+  return launch_variant<MT, NTW, GPU, false, RNG, false>(c, a, stream);
 }
 
 template <int MT, int NTW>
@@ -690,20 +723,20 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   }
   c.grid_m = (int)((M + 16 * c.mt - 1) / (16 * c.mt));
   c.grid = c.grid_m == 1 ? c.n_wg : (int)((c.n_wg + 7) / 8 * 8 * c.grid_m);
-  // 9-16 rows with the weight workgroups on at most half of the CUs (narrow
-  // layers): split K into ranges of whole unit quads, as many as fit one pass
-  // over the CUs, at most kMaxSplits; the last split of each workgroup adds the
-  // partial tiles. Measured on MI355X at M = 16 (us, unsplit -> split): 512 x
-  // 3584 6.6 -> 5.6 (4 splits; act_order 8.1 -> 7.5), 1024 x 4096 7.0 -> 6.3
-  // (4), 2048 x 4096 7.0 -> 6.5 (2), 512 x 8192 11.4 -> 6.9 (4). The combine
-  // costs about three device-scope round trips: 7 or 8 one-quad splits were
-  // slower than 4 (512 x 3584: 6.8), and at 8 rows no split gained.
+  // Up to 16 rows with the weight workgroups on at most a quarter of the CUs
+  // (narrow layers): split K into kMaxSplits ranges of whole unit quads; the
+  // last split of each workgroup adds the partial tiles (one round trip for
+  // all of them). Measured on MI355X (us, unsplit -> 4 splits): 512 x 3584 at
+  // M = 8 / 16 5.3 / 6.6 -> 4.9 / 5.2 (act_order 6.6 / 8.0 -> 6.0 / 6.8), 1024 x
+  // 4096 at M = 16 6.9 -> 5.9 (act_order 8.7 -> 7.9), 512 x 8192 at M = 8 8.8 ->
+  // 5.8. Two splits gained nothing (2048 x 4096 at M = 16: 7.0 either way), and
+  // more than one pass over the CUs loses (three there: 9.4).
   c.splits = 1;
   c.ws_split = 0;
   static const int env_split = [] { const char* e = getenv("PMI_TGEMM_SPLIT"); return e ? atoi(e) : -1; }();
   if (c.mt == 1 && c.grid_m == 1 && !c.rng && c.ntw == 1 && env_split != 0 &&
-      (M > 8 || env_split > 0) && c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
-    int64_t s = env_split > 0 ? env_split : cus / c.n_wg;
+      c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
+    int64_t s = env_split > 0 ? env_split : (cus / c.n_wg >= kMaxSplits ? kMaxSplits : 1);
     if (s > (K >> 9)) s = K >> 9;
     if (s > kMaxSplits) s = kMaxSplits;
     if (s >= 2) {

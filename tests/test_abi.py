@@ -121,15 +121,15 @@ def test_kernel_choice(L):
 
 
 def test_tgemm_splits(L):
-    # K ranges of the tiled GEMM at 9..16 rows where its workgroups fill at most
-    # half of the 256 CUs: as many as fit one pass, at most 4, one unit quad each
+    # K ranges of the tiled GEMM up to 16 rows where its workgroups fill at most
+    # a quarter of the 256 CUs: 4 (fewer only where K has fewer unit quads)
     assert L.pmi_tgemm_splits(16, 512, 3584, 128, 0) == 4    # 32 workgroups
     assert L.pmi_tgemm_splits(16, 512, 3584, 128, 1) == 4    # act_order (in-kernel gather)
     assert L.pmi_tgemm_splits(16, 1024, 4096, 128, 0) == 4   # 64 workgroups
-    assert L.pmi_tgemm_splits(12, 2048, 4096, 128, 0) == 2   # 128 workgroups
+    assert L.pmi_tgemm_splits(12, 2048, 4096, 128, 0) == 1   # 128 workgroups: unsplit
     assert L.pmi_tgemm_splits(16, 512, 1536, 128, 0) == 3    # 3 quads
     assert L.pmi_tgemm_splits(9, 200, 8192, 32, 0) == 4
-    assert L.pmi_tgemm_splits(8, 512, 3584, 128, 0) == 1     # up to 8 rows: unsplit
+    assert L.pmi_tgemm_splits(8, 512, 3584, 128, 0) == 4     # 8 rows too
     assert L.pmi_tgemm_splits(16, 3584, 3584, 128, 0) == 1   # 224 workgroups: unsplit
     assert L.pmi_tgemm_splits(17, 512, 3584, 128, 0) == 1    # past 16 rows: unsplit
     assert L.pmi_tgemm_splits(16, 512, 1000, 128, 0) == 1    # not a tiled GEMM shape

@@ -183,13 +183,14 @@ def test_tgemm_rows(M):
 
 
 SPLIT_CASES = [
-    # (M, N, K, gs, act_order): narrow layers at 9..16 rows, K split over
+    # (M, N, K, gs, act_order): narrow layers up to 16 rows, K split over
     # workgroups (even and uneven quads per split, one quad per split, ragged
     # N, gs 32 / 64 / 256 and act_order with the in-kernel gather)
     (16, 512, 3584, 128, False), (16, 512, 3584, 128, True), (16, 1024, 4096, 128, False),
-    (16, 1024, 3584, 128, True), (12, 2048, 4096, 128, False), (9, 512, 1536, 128, False),
-    (12, 200, 2048, 32, False), (16, 1028, 3072, 64, False), (10, 512, 3584, 256, False),
-    (16, 520, 8192, 128, False), (9, 512, 3584, 128, True), (13, 1024, 4096, 128, True)]
+    (16, 1024, 3584, 128, True), (8, 1024, 4096, 128, False), (9, 512, 1536, 128, False),
+    (12, 200, 2048, 32, False), (16, 1024, 3072, 64, False), (10, 512, 3584, 256, False),
+    (16, 520, 8192, 128, False), (4, 512, 3584, 128, True), (13, 1024, 4096, 128, True),
+    (5, 512, 8192, 128, False), (3, 200, 1536, 128, True)]
 
 
 @pytest.mark.gpu
@@ -209,7 +210,7 @@ def test_tgemm_split_k(M, N, K, gs, act_order):
 def test_tgemm_split_k_counters_reset():
     """Calls of different split counts and workgroup counts alternate on one
     stream and one workspace: every call leaves the counters at zero."""
-    shapes = [(16, 512, 3584), (16, 1024, 4096), (12, 2048, 4096), (16, 512, 1536)]
+    shapes = [(16, 512, 3584), (16, 1024, 4096), (12, 2048, 4096), (16, 512, 1536), (8, 200, 2048)]
     for M, N, K in shapes + shapes[::-1]:
         _tgemm_case(M, N, K, 128, seed=M + N + K)
 
