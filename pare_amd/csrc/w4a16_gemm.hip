@@ -413,9 +413,9 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
     // Last to arrive: sum the partials in split order (deterministic). Every
     // split's partial, this one's included, is in the workspace. The loads of
     // kB splits are issued together, so the sum costs one round trip per kB
-    // splits rather than one per split.
-    constexpr int kB = MT * kNT >= 16 ? 2 : (MT * kNT >= 8 ? 4 : 8);
-    f32x4 tot[MT][kNT];
+    // splits rather than one per split; kB keeps them within 64 VGPRs.
+    constexpr int kB = MT * kNT >= 16 ? 1 : 16 / (MT * kNT);
+    f32x4 tot[MT][kNT] = {};
     for (int q0 = 0; q0 < a.splits; q0 += kB) {
       f32x4 part[kB][MT][kNT];
 #pragma unroll
@@ -429,14 +429,19 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm_kernel(GemmArgs a) {
             part[b][mt][j] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, vlane + (mt * kNT + j) * 1024, soff, kSc1));
       }
+      // the adds select rather than break: behind the break the compiler sank
+      // the loads of later splits to their adds, one round trip per split
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int b = 0; b < kB; ++b) {
-        if (q0 + b >= a.splits) break;
+        const bool use = q0 + b < a.splits;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int j = 0; j < kNT; ++j)
-            tot[mt][j] = q0 + b == 0 ? part[b][mt][j] : tot[mt][j] + part[b][mt][j];
+          for (int j = 0; j < kNT; ++j) {
+            const f32x4 t = q0 + b == 0 ? part[b][mt][j] : tot[mt][j] + part[b][mt][j];
+            tot[mt][j] = use ? t : tot[mt][j];
+          }
       }
     }
 #pragma unroll

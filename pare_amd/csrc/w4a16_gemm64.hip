@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm64_kernel(Gemm64Args a)
     // split's partial, this one's included, is in the workspace; the loads of
     // kB splits are issued together (one round trip per kB splits).
     constexpr int kB = MT >= 2 ? 2 : 4;
-    f32x16 tot[MT];
+    f32x16 tot[MT] = {};
     for (int q0 = 0; q0 < a.splits; q0 += kB) {
       f32x16 part[kB][MT];
 #pragma unroll
@@ -349,11 +349,17 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm64_kernel(Gemm64Args a)
             for (int e = 0; e < 4; ++e) part[sb][mt][4 * b + e] = v[e];
           }
       }
+      // the adds select rather than break: behind the break the compiler sank
+      // the loads of later splits to their adds, one round trip per split
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int sb = 0; sb < kB; ++sb) {
-        if (q0 + sb >= a.splits) break;
+        const bool use = q0 + sb < a.splits;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) tot[mt] = q0 + sb == 0 ? part[sb][mt] : tot[mt] + part[sb][mt];
+        for (int mt = 0; mt < MT; ++mt) {
+          const f32x16 t = q0 + sb == 0 ? part[sb][mt] : tot[mt] + part[sb][mt];
+          tot[mt] = use ? t : tot[mt];
+        }
       }
     }
 #pragma unroll
