@@ -411,16 +411,23 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
       a0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l, off, kSc1));
       a1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 8 * l + 4, off, kSc1));
     }
+    // the updates select rather than skip: behind a branch on the loaded max
+    // the compiler sank the later splits' loads to their updates, one round
+    // trip each
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      if (s0 + k >= S || ms[k] == -INFINITY) continue;  // uniform across the wave
+      const bool use = s0 + k < S && ms[k] != -INFINITY;  // uniform across the wave
       const float nm = fmaxf(mx, ms[k]);
       const float fo = mx == -INFINITY ? 0.f : __expf(mx - nm);
       const float fn = __expf(ms[k] - nm);
-      tot = fmaf(tot, fo, ls[k] * fn);
-      o0 = fmaf(o0, fo, a0[k] * fn);
-      o1 = fmaf(o1, fo, a1[k] * fn);
-      mx = nm;
+      const float t = fmaf(tot, fo, ls[k] * fn);
+      const float p0 = fmaf(o0, fo, a0[k] * fn);
+      const float p1 = fmaf(o1, fo, a1[k] * fn);
+      tot = use ? t : tot;
+      o0 = use ? p0 : o0;
+      o1 = use ? p1 : o1;
+      mx = use ? nm : mx;
     }
   }
   const float inv = 1.f / tot;
