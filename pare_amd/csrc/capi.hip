@@ -192,6 +192,16 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
     if (gathers ? (M >= 3 || N >= 3072) : (M >= 5 || (M >= 3 && N >= 3072) || (N >= 8192 && N <= 20480)))
       return 5;
   }
+  // Long rows (K > 8192, down_proj) up to 16 rows, where the tiled GEMM splits
+  // K four ways over 64-row workgroups: Llama down 4096 x 14336 at M = 4 / 16
+  // takes 10.3 / 11.8 against 14.0 us for the MFMA GEMM; Qwen down 3584 x 18944
+  // 11.9 / 12.9 against 15.8 / 15.3. With act_order past 2 rows X[:, perm] is
+  // gathered into the workspace first (M = 16: 17.6 against 20.0 us).
+  if (has_tiled && M >= 2 && M <= 16 && K > 8192 && pmi::tgemm_supported(M, N, K, group_size)) {
+    const pmi::TgemmConfig c =
+        pmi::tgemm_config(M, N, K, group_size, has_perm && pmi::tgemm_gather_supported(M, K));
+    if (c.splits > 1 && c.ntw == 4) return 5;
+  }
   // Past 64 rows on narrow layers, while the tiled GEMM's 64-row blocks still
   // take one pass over the CUs: against the register-streamed GEMM, whose K
   // splits these layers need, k/v 1024 x 4096 at M = 256 takes 10.3 against

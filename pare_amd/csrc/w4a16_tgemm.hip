@@ -116,44 +116,52 @@ struct Unit {
   uint8_t zr[RNG ? NTW : 1];
 };
 
-// K split (one 16-row weight tile per workgroup): the partial tile of split sp
-// goes to the workspace; the last split of weight workgroup wg to arrive adds
-// all of them in split order (so the result does not depend on the arrival
-// order) and returns true with the sum in `sum`. Stores and loads carry the
-// device-scope cache policy (sc1), as agent-scope atomics do, so they are
-// coherent across the XCDs' L2 caches without a release fence: the stores
-// complete (s_waitcnt) before the counter increment, and the last split loads
-// only after its increment has returned the count. All kMaxSplits loads are
-// issued together (one round trip; past the last split they re-read it).
+// K split: the NTW partial 16 x 16 tiles of split sp go to the workspace;
+// the last split of weight workgroup wg to arrive adds all of them in split
+// order (so the result does not depend on the arrival order) and returns
+// true with the sums in `sum`. Stores and loads carry the device-scope cache
+// policy (sc1), as agent-scope atomics do, so they are coherent across the
+// XCDs' L2 caches without a release fence: the stores complete (s_waitcnt)
+// before the counter increment, and the last split loads only after its
+// increment has returned the count. All kMaxSplits loads of a tile are issued
+// together (one round trip; past the last split they re-read it).
 constexpr int kMaxSplits = 4;
-__device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int sp, int l, f32x4& sum) {
+template <int NTW>
+__device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int sp, int l, f32x4 (&sum)[NTW]) {
   constexpr int kTile = 1024;  // bytes of a 16 x 16 fp32 tile
   constexpr int kSc1 = 16;
   const __amdgpu_buffer_rsrc_t rp =
-      rsrc(a.part + (size_t)wg * a.splits * (kTile / 4), (int64_t)a.splits * kTile);
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), rp, 16 * l,
-                                         __builtin_amdgcn_readfirstlane(sp * kTile), kSc1);
+      rsrc(a.part + (size_t)wg * a.splits * NTW * (kTile / 4), (int64_t)a.splits * NTW * kTile);
+#pragma unroll
+  for (int j = 0; j < NTW; ++j)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[j]), rp, 16 * l,
+                                           __builtin_amdgcn_readfirstlane((sp * NTW + j) * kTile), kSc1);
   __builtin_amdgcn_s_waitcnt(0);
   int old = 0;
   if (l == 0)
     old = __hip_atomic_fetch_add(&a.counters[wg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __builtin_amdgcn_readfirstlane(old);
   if (old != a.splits - 1) return false;
-  f32x4 v[kMaxSplits];
+  f32x4 v[kMaxSplits][NTW];
 #pragma unroll
   for (int q = 0; q < kMaxSplits; ++q) {
     const int qq = q < a.splits ? q : a.splits - 1;
-    v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                         rp, 16 * l, __builtin_amdgcn_readfirstlane(qq * kTile), kSc1));
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+      v[q][j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rp, 16 * l, __builtin_amdgcn_readfirstlane((qq * NTW + j) * kTile), kSc1));
   }
   // the adds select rather than branch: behind a branch per split the
   // compiler sank each load to its add, one round trip per split
   __builtin_amdgcn_sched_barrier(0);
-  sum = v[0];
 #pragma unroll
-  for (int q = 1; q < kMaxSplits; ++q) {
-    const f32x4 t = sum + v[q];
-    sum = q < a.splits ? t : sum;
+  for (int j = 0; j < NTW; ++j) {
+    sum[j] = v[0][j];
+#pragma unroll
+    for (int q = 1; q < kMaxSplits; ++q) {
+      const f32x4 t = sum[j] + v[q][j];
+      sum[j] = q < a.splits ? t : sum[j];
+    }
   }
   if (l == 0) __hip_atomic_store(&a.counters[wg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
@@ -168,7 +176,7 @@ template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
   static_assert(!RNG || (MT == 1 && GPU == 1), "tile ranges are built for up to 16 rows, gs >= 128");
-  static_assert(!SPLIT || (MT == 1 && NTW == 1 && !RNG), "the K split is built for one 16-row tile");
+  static_assert(!SPLIT || (MT == 1 && !RNG), "the K split is built for up to 16 rows");
   using UnitT = Unit<MT, NTW, GPU, RNG>;
   constexpr bool RING = MT > 1;
   // MT = 4: the ring holds half units (64 columns, k-steps 0-1 or 2-3), two
@@ -559,7 +567,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       for (int k = 1; k < kKW; ++k) sum[j] += red[((k * MT + mt) * NTW + j) * 64 + l];
     }
     if constexpr (SPLIT) {
-      if (!combine_splits(a, wg, sp, l, sum[0])) return;
+      if (!combine_splits<NTW>(a, wg, sp, l, sum)) return;
     }
     if (!RNG && row0 >= N) return;
     // lane (n, h): rows 16 mt + 4 h + i of the activations, weight rows row0 + j
@@ -621,10 +629,11 @@ hipError_t launch_variant(const TgemmConfig& c, const TgemmArgs& a, hipStream_t 
 template <int MT, int NTW, int GPU, bool RNG = false>
 hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
   if constexpr (MT == 1) {
-    if constexpr (NTW == 1 && !RNG) {
+    // K split: one tile per workgroup at every group size, 2 or 4 at gs >= 128
+    if constexpr (!RNG && (NTW == 1 || GPU == 1)) {
       if (a.splits > 1) {
-        if (a.perm) return launch_variant<1, 1, GPU, true, false, true>(c, a, stream);
-        return launch_variant<1, 1, GPU, false, false, true>(c, a, stream);
+        if (a.perm) return launch_variant<1, NTW, GPU, true, false, true>(c, a, stream);
+        return launch_variant<1, NTW, GPU, false, false, true>(c, a, stream);
       }
     }
     if (a.perm) return launch_variant<1, NTW, GPU, true, RNG, false>(c, a, stream);
@@ -734,15 +743,28 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   c.splits = 1;
   c.ws_split = 0;
   static const int env_split = [] { const char* e = getenv("PMI_TGEMM_SPLIT"); return e ? atoi(e) : -1; }();
-  if (c.mt == 1 && c.grid_m == 1 && !c.rng && c.ntw == 1 && env_split != 0 &&
-      c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
+  // Long rows (K > 8192) up to 16 rows, where 64-row workgroups fill at most a
+  // quarter of the CUs (down_proj: N <= 4096): four 16-row tiles per
+  // workgroup, K split four ways, so that each workgroup reads a quarter of
+  // the activation rows once for four tiles (unsplit, every tile re-reads all
+  // of them). Against the MFMA GEMM (us): Llama down 4096 x 14336 at M = 4 / 8
+  // / 16 10.3 / 10.5 / 11.8 against 14.0; Qwen down 3584 x 18944 11.9 / 11.9 /
+  // 12.9 against 15.8 / 15.5 / 15.3. Two splits, or four tiles unsplit, lose.
+  if (c.mt == 1 && c.grid_m == 1 && !c.rng && gs % 128 == 0 && K > 8192 && env_split != 0 &&
+      env_ntw == 0 && panels * kMaxSplits <= cus && panels <= (int64_t)(kWsCounterBytes / 4)) {
+    c.ntw = 4;
+    c.n_wg = (int)panels;
+    c.grid = c.n_wg;
+  }
+  if (c.mt == 1 && c.grid_m == 1 && !c.rng && (c.ntw == 1 || (gs % 128 == 0 && (env_split > 0 || K > 8192))) &&
+      env_split != 0 && c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
     int64_t s = env_split > 0 ? env_split : (cus / c.n_wg >= kMaxSplits ? kMaxSplits : 1);
     if (s > (K >> 9)) s = K >> 9;
     if (s > kMaxSplits) s = kMaxSplits;
     if (s >= 2) {
       c.splits = (int)s;
       c.grid = c.n_wg * c.splits;
-      c.ws_split = ws_align((size_t)c.n_wg * c.splits * 1024);
+      c.ws_split = ws_align((size_t)c.n_wg * c.splits * c.ntw * 1024);
     }
   }
   return c;

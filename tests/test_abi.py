@@ -70,7 +70,11 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(64, 4096, 4096, 64, 0) == 1    # without the copy: GEMV
     assert L.pmi_matmul_kernel_choice(8, 4096, 4096, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(32, 6144, 4096, 32, 1) == 5
-    assert L.pmi_matmul_kernel_choice(16, 4096, 14336, 128, 1) != 5   # K > 8192
+    assert L.pmi_matmul_kernel_choice(16, 4096, 14336, 128, 1) == 5   # long rows: K split, 64-row tiles
+    assert L.pmi_matmul_kernel_choice(2, 4096, 14336, 128, 1) == 5
+    assert L.pmi_matmul_kernel_choice(1, 4096, 14336, 128, 1) == 1    # one row: GEMV
+    assert L.pmi_matmul_kernel_choice(17, 4096, 14336, 128, 1) != 5   # past 16 rows
+    assert L.pmi_matmul_kernel_choice(16, 14336, 14336, 128, 1) != 5  # 224 panels: no room to split
     assert L.pmi_matmul_kernel_choice(16, 1024, 4096, 128, 1) == 5    # narrow layers too
     assert L.pmi_matmul_kernel_choice(8, 512, 3584, 128, 1) == 5
     assert L.pmi_matmul_kernel_choice(4, 1024, 4096, 128, 1) == 1     # narrow at 4 rows: GEMV
@@ -86,7 +90,8 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(16, 3584, 3584, 128, TP) == 5
     assert L.pmi_matmul_kernel_choice(1, 3584, 3584, 128, TP) == 1
     assert L.pmi_matmul_kernel_choice(4, 512, 3584, 128, _lib.PMI_CHOICE_PERM) == 1  # no copy
-    assert L.pmi_matmul_kernel_choice(16, 3584, 18944, 128, TP) != 5  # K past the tiled GEMM
+    assert L.pmi_matmul_kernel_choice(16, 3584, 18944, 128, TP) == 5  # long rows, X gathered first
+    assert L.pmi_matmul_kernel_choice(2, 3584, 18944, 128, TP) == 5
     # GEMV for M <= 2 (M <= 4 for N < 8192); skinny MFMA kernel up to M = 16 for
     # N <= 8192 while the activations fit the LDS budget; MFMA GEMM otherwise
     assert L.pmi_matmul_kernel_choice(1, 4096, 4096, 128, 0) == 1
@@ -133,6 +138,9 @@ def test_tgemm_splits(L):
     assert L.pmi_tgemm_splits(16, 3584, 3584, 128, 0) == 1   # 224 workgroups: unsplit
     assert L.pmi_tgemm_splits(17, 512, 3584, 128, 0) == 1    # past 16 rows: unsplit
     assert L.pmi_tgemm_splits(16, 512, 1000, 128, 0) == 1    # not a tiled GEMM shape
+    assert L.pmi_tgemm_splits(4, 4096, 14336, 128, 0) == 4   # long rows: 64 workgroups of 4 tiles
+    assert L.pmi_tgemm_splits(16, 3584, 18944, 128, 1) == 4
+    assert L.pmi_tgemm_splits(16, 14336, 14336, 128, 0) == 1
     # the workspace covers the partial tiles (1 KiB per workgroup and split)
     # after the counter block
     assert L.pmi_matmul_workspace_bytes(16, 512, 3584, 128, 0) >= 64 * 1024 + 32 * 4 * 1024

@@ -190,7 +190,12 @@ SPLIT_CASES = [
     (16, 1024, 3584, 128, True), (8, 1024, 4096, 128, False), (9, 512, 1536, 128, False),
     (12, 200, 2048, 32, False), (16, 1024, 3072, 64, False), (10, 512, 3584, 256, False),
     (16, 520, 8192, 128, False), (4, 512, 3584, 128, True), (13, 1024, 4096, 128, True),
-    (5, 512, 8192, 128, False), (3, 200, 1536, 128, True)]
+    (5, 512, 8192, 128, False), (3, 200, 1536, 128, True),
+    # long rows (K > 8192): four 16-row tiles per workgroup, K split four ways;
+    # act_order gathered into the workspace first (the in-kernel gather stops at
+    # K = 8192), one row included
+    (4, 1024, 14336, 128, False), (16, 3584, 18944, 128, False), (2, 512, 18944, 128, True),
+    (7, 1024, 18944, 128, True), (1, 512, 14336, 128, True)]
 
 
 @pytest.mark.gpu
@@ -203,7 +208,10 @@ def test_tgemm_split_k(M, N, K, gs, act_order):
     y = _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order)
     y2 = _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order)
     assert torch.equal(y, y2)
-    _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order, no_workspace=True)
+    # without a workspace act_order needs the in-kernel gather (K <= 8192, X and
+    # the perm table within the kernel's LDS)
+    if not act_order or (K <= 8192 and M * (2 * K + 16) + 4 * K <= 159 * 1024):
+        _tgemm_case(M, N, K, gs, seed=M * 7 + N, act_order=act_order, no_workspace=True)
 
 
 @pytest.mark.gpu
