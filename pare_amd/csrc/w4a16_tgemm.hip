@@ -750,13 +750,19 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   // of them). Against the MFMA GEMM (us): Llama down 4096 x 14336 at M = 4 / 8
   // / 16 10.3 / 10.5 / 11.8 against 14.0; Qwen down 3584 x 18944 11.9 / 11.9 /
   // 12.9 against 15.8 / 15.5 / 15.3. Two splits, or four tiles unsplit, lose.
-  if (c.mt == 1 && c.grid_m == 1 && !c.rng && gs % 128 == 0 && K > 8192 && env_split != 0 &&
+  // The same at 13-16 rows for shorter rows where one-tile workgroups already
+  // fill more than a quarter of the CUs (1024 < N <= 4096; not with the
+  // act_order gather, whose every workgroup stages all of X): 2048 x 4096 at
+  // M = 16 6.2 against 6.9 us, Qwen q_o 3584 x 3584 6.6 against 7.0, 4096 x
+  // 4096 7.1 against 7.2; at M = 8 it loses (4096 x 4096: 7.0 against 6.0).
+  const bool wide_split = K > 8192 || (M > 12 && !gather && 4 * panels * kMaxSplits > cus);
+  if (c.mt == 1 && c.grid_m == 1 && !c.rng && gs % 128 == 0 && wide_split && env_split != 0 &&
       env_ntw == 0 && panels * kMaxSplits <= cus && panels <= (int64_t)(kWsCounterBytes / 4)) {
     c.ntw = 4;
     c.n_wg = (int)panels;
     c.grid = c.n_wg;
   }
-  if (c.mt == 1 && c.grid_m == 1 && !c.rng && (c.ntw == 1 || (gs % 128 == 0 && (env_split > 0 || K > 8192))) &&
+  if (c.mt == 1 && c.grid_m == 1 && !c.rng && (c.ntw == 1 || (gs % 128 == 0 && (env_split > 0 || wide_split))) &&
       env_split != 0 && c.n_wg <= (int64_t)(kWsCounterBytes / 4)) {
     int64_t s = env_split > 0 ? env_split : (cus / c.n_wg >= kMaxSplits ? kMaxSplits : 1);
     if (s > (K >> 9)) s = K >> 9;

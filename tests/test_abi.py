@@ -132,10 +132,14 @@ def test_tgemm_splits(L):
     assert L.pmi_tgemm_splits(16, 512, 3584, 128, 1) == 4    # act_order (in-kernel gather)
     assert L.pmi_tgemm_splits(16, 1024, 4096, 128, 0) == 4   # 64 workgroups
     assert L.pmi_tgemm_splits(12, 2048, 4096, 128, 0) == 1   # 128 workgroups: unsplit
+    assert L.pmi_tgemm_splits(16, 2048, 4096, 128, 0) == 4   # 13-16 rows: four tiles per workgroup
+    assert L.pmi_tgemm_splits(16, 3584, 3584, 128, 0) == 4
+    assert L.pmi_tgemm_splits(16, 3584, 3584, 128, 1) == 1   # not with the act_order gather
+    assert L.pmi_tgemm_splits(16, 6144, 4096, 128, 0) == 1   # 96 panels: more than a quarter
     assert L.pmi_tgemm_splits(16, 512, 1536, 128, 0) == 3    # 3 quads
     assert L.pmi_tgemm_splits(9, 200, 8192, 32, 0) == 4
     assert L.pmi_tgemm_splits(8, 512, 3584, 128, 0) == 4     # 8 rows too
-    assert L.pmi_tgemm_splits(16, 3584, 3584, 128, 0) == 1   # 224 workgroups: unsplit
+    assert L.pmi_tgemm_splits(8, 3584, 3584, 128, 0) == 1    # 224 workgroups at 8 rows: unsplit
     assert L.pmi_tgemm_splits(17, 512, 3584, 128, 0) == 1    # past 16 rows: unsplit
     assert L.pmi_tgemm_splits(16, 512, 1000, 128, 0) == 1    # not a tiled GEMM shape
     assert L.pmi_tgemm_splits(4, 4096, 14336, 128, 0) == 4   # long rows: 64 workgroups of 4 tiles

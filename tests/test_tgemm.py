@@ -195,7 +195,9 @@ SPLIT_CASES = [
     # act_order gathered into the workspace first (the in-kernel gather stops at
     # K = 8192), one row included
     (4, 1024, 14336, 128, False), (16, 3584, 18944, 128, False), (2, 512, 18944, 128, True),
-    (7, 1024, 18944, 128, True), (1, 512, 14336, 128, True)]
+    (7, 1024, 18944, 128, True), (1, 512, 14336, 128, True),
+    # 13-16 rows, 1024 < N <= 4096: four tiles per workgroup, K split four ways
+    (16, 2048, 4096, 128, False), (13, 4036, 2048, 128, False)]
 
 
 @pytest.mark.gpu
