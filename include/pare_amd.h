@@ -312,11 +312,13 @@ PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t gr
                                      int flags);
 
 /* The K ranges the tiled-weight GEMM (kernel 5) splits this shape into when
- * the call has a workspace of pmi_matmul_workspace_bytes() bytes: up to 16
- * rows on layers whose weight workgroups fill at most half of the CUs, each
- * range on its own workgroup, the last to finish adding the fp32 partial
- * tiles in range order; 1 = unsplit (always without a workspace). has_perm:
- * an act_order perm. Host-only diagnostic; no reference counterpart. */
+ * the call has a workspace of pmi_matmul_workspace_bytes() bytes. Up to 16
+ * rows: four ranges where its one-tile workgroups fill at most a quarter of
+ * the CUs (narrow layers), and four ranges over four-tile workgroups for
+ * K > 8192 (and at 13-16 rows for N <= 4096 without act_order). Each range
+ * runs on its own workgroup; the last to finish adds the fp32 partial tiles
+ * in range order. 1 = unsplit (always without a workspace). has_perm: an
+ * act_order perm. Host-only diagnostic; no reference counterpart. */
 PMI_API int pmi_tgemm_splits(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm);
 
 /* Forces pmi_matmul_w4a16 onto one kernel (1 to 5 as above; 0 restores the
