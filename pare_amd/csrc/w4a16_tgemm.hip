@@ -1,5 +1,5 @@
-// Tiled-weight MFMA INT4 W4A16 GEMM for 2..64 activation rows, gfx950
-// (v_mfma_f32_16x16x32_f16).
+// Tiled-weight MFMA INT4 W4A16 GEMM for 2..64 activation rows (more as
+// 16-row blocks on narrow layers), gfx950 (v_mfma_f32_16x16x32_f16).
 //
 // Why a tiled copy of the weights. At these row counts the kernel is a weight
 // stream, and how the stream meets the DRAM decides its speed: on MI355X a
@@ -24,9 +24,10 @@
 // take the units u = 4 s + w (w = wave) and are added through LDS at the end;
 // the four waves of a workgroup read four consecutive blocks at every step.
 // NTW is the largest of 4, 2, 1 that still gives about a workgroup per CU.
-// Only narrow layers at 9-16 rows, whose tiles leave half of the CUs idle,
-// split K: 2-4 workgroups per tile take ranges of unit quads, and the last to
-// finish adds the fp32 partial tiles in range order (combine_splits).
+// Up to 16 rows, layers whose workgroups would leave most CUs idle (narrow
+// layers; long rows, K > 8192, with four tiles per workgroup) split K: four
+// workgroups per tile set take ranges of unit quads, and the last to finish
+// adds the fp32 partial tiles in range order (combine_splits).
 //
 // Activations. Up to 16 rows (MT = 1) every compute wave loads the A operands
 // of its own units with the weights (16 rows x 256 bytes per unit, L2
