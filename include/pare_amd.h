@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 12
+#define PMI_ABI_VERSION 13
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -206,6 +206,28 @@ PMI_API int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* 
 PMI_API int pmi_matmul_w4a16_glu(const void* gate_up, const uint8_t* w, const float* scales,
                                  const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,
                                  int64_t K, int64_t group_size, void* stream);
+
+/* y = silu(x . dequant(Wg)^T) * (x . dequant(Wu)^T), the fused gate/up
+ * projection of a gated MLP with its activation in the epilogue (one launch
+ * instead of the matmul and pmi_silu_mul_f16). x: fp16 [M, K]; y: fp16
+ * [M, N / 2], each element formed as pmi_silu_mul_f16 forms it from the fp16
+ * gate and up outputs, so y equals pmi_matmul_w4a16 on the fused [Wg; Wu]
+ * followed by pmi_silu_mul_f16 bit for bit. w_tiled, scales_gm, zeros_gm:
+ * the pmi_tile_w4a16 and pmi_sz_group_major copies of the fused weight with
+ * its rows interleaved in fours: row 64p + 4n + j holds gate row 32p + 2n + j
+ * for j < 2 and up row 32p + 2n + j - 2 for j >= 2 (p < N / 64, n < 16).
+ * For the shapes pmi_gate_up_silu_supported accepts (the tiled GEMM with four
+ * 16-row tiles per workgroup: M <= 16, N % 64 == 0; no act_order), else
+ * PMI_ERR_UNSUPPORTED. No reference counterpart: the reference runs SiLU and
+ * the product as HuggingFace PyTorch ops after QuantizedLinear
+ * (pare/eval/throughput.py:84-126). */
+PMI_API int pmi_matmul_w4a16_gate_up_silu(const void* x, const uint8_t* w_tiled,
+                                          const float* scales_gm, const uint8_t* zeros_gm,
+                                          void* y, int64_t M, int64_t N, int64_t K,
+                                          int64_t group_size, void* stream);
+
+/* 1 when pmi_matmul_w4a16_gate_up_silu runs this shape, else 0. Host-only. */
+PMI_API int pmi_gate_up_silu_supported(int64_t M, int64_t N, int64_t K, int64_t group_size);
 
 /* y = (RMSNorm(x + residual) * norm_weight) . dequant(W)^T for M <= 4: a
  * decoder's residual add and pre-norm fused into the GEMV that consumes them.

@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -64,6 +64,8 @@ SIGNATURES = {
     "pmi_rtn_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp]),
     "pmi_matmul_kernel_choice": (_i, [_i64, _i64, _i64, _i64, _i]),
     "pmi_tgemm_splits": (_i, [_i64, _i64, _i64, _i64, _i]),
+    "pmi_matmul_w4a16_gate_up_silu": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "pmi_gate_up_silu_supported": (_i, [_i64, _i64, _i64, _i64]),
     "pmi_set_kernel_override": (_i, [_i]),
     "pmi_add_rmsnorm_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "pmi_rope_kv_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

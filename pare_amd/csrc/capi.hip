@@ -263,6 +263,30 @@ int pmi_matmul_w4a16_glu(const void* gate_up, const uint8_t* w, const float* sca
                   fn);
 }
 
+int pmi_gate_up_silu_supported(int64_t M, int64_t N, int64_t K, int64_t group_size) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
+  return pmi::tgemm_glu_supported(M, N, K, group_size) ? 1 : 0;
+}
+
+int pmi_matmul_w4a16_gate_up_silu(const void* x, const uint8_t* w_tiled, const float* scales_gm,
+                                  const uint8_t* zeros_gm, void* y, int64_t M, int64_t N,
+                                  int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_matmul_w4a16_gate_up_silu";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
+  if (M == 0 || N == 0) return ok();
+  if (!pmi::tgemm_glu_supported(M, N, K, group_size))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: shape not on the four-tile tiled GEMM (M=%lld N=%lld "
+                "K=%lld gs=%lld; see pmi_gate_up_silu_supported)", fn, (long long)M, (long long)N,
+                (long long)K, (long long)group_size);
+  if (!x || !w_tiled || !scales_gm || !zeros_gm || !y) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(x, 16) || !aligned(w_tiled, 16) || !aligned(scales_gm, 16) || !aligned(y, 4))
+    return fail(PMI_ERR_INVALID, "%s: x, w_tiled and scales_gm must be 16-byte aligned, y 4-byte", fn);
+  return from_hip(pmi::launch_tgemm_glu(x, w_tiled, scales_gm, zeros_gm, y, M, N, K, group_size,
+                                        (hipStream_t)stream),
+                  fn);
+}
+
 int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const void* norm_weight,
                              float eps, void* h_out, const uint8_t* w, const float* scales,
                              const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,

@@ -47,6 +47,20 @@ PMI_DEV void unpack_word_minus_zero(uint32_t w, uint32_t nz, f16x2& d0, f16x2& d
 PMI_DEV uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 PMI_DEV uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
+// silu(g) * u of two fp16 pairs, each half rounded as pmi_silu_mul_f16 rounds
+// it: the gate's silu to fp16 first, then the product.
+PMI_DEV uint32_t glu_pair(uint32_t g, uint32_t u) {
+  const f16x2 gh = as_f16x2(g), uh = as_f16x2(u);
+  f16x2 o;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float gf = (float)gh[e];
+    const float sg = (float)(f16)(gf * __builtin_amdgcn_rcpf(1.f + __expf(-gf)));
+    o[e] = (f16)(sg * (float)uh[e]);
+  }
+  return as_u32(o);
+}
+
 PMI_DEV float dot2_acc(f16x2 a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(a, as_f16x2(b), c, false);
 }

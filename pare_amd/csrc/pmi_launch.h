@@ -226,5 +226,13 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
                         const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
                         int64_t N, int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
                         size_t part_offset, hipStream_t stream);
+// silu(gate) * up from a fused gate/up weight whose rows are interleaved in
+// groups of four (rows 4n + {0, 1} of a 64-row panel p: gate rows 32 p + 2 n +
+// {0, 1}; rows 4n + {2, 3}: the matching up rows), y fp16 [M, N / 2]; for the
+// shapes the tiled GEMM runs with four tiles per workgroup, no K split
+bool tgemm_glu_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
+hipError_t launch_tgemm_glu(const void* x, const uint8_t* w_tiled, const float* scales_gm,
+                            const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K,
+                            int64_t gs, hipStream_t stream);
 
 }  // namespace pmi

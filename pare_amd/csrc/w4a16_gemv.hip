@@ -303,20 +303,6 @@ PMI_DEV void reduce_batch(const Batch<U, SPW, ZU8>& bt, const uint32_t (&xp)[SPW
 // with one slice wave the results go straight to y, otherwise each wave
 // parks its per-row partial in LDS and one barrier precedes the fixed-order
 // sum over slice waves (deterministic; no atomics, no workspace).
-// silu(g) * u of two fp16 pairs, each half rounded as pmi_silu_mul_f16 rounds
-// it: the gate's silu to fp16 first, then the product.
-PMI_DEV uint32_t glu_pair(uint32_t g, uint32_t u) {
-  const f16x2 gh = as_f16x2(g), uh = as_f16x2(u);
-  f16x2 o;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const float gf = (float)gh[e];
-    const float sg = (float)(f16)(gf * __builtin_amdgcn_rcpf(1.f + __expf(-gf)));
-    o[e] = (f16)(sg * (float)uh[e]);
-  }
-  return as_u32(o);
-}
-
 // h = x + r per fp16 pair, rounded as add_rmsnorm_kernel rounds it.
 PMI_DEV uint32_t add_pair(uint32_t x, uint32_t r) {
   const f16x2 xh = as_f16x2(x), rh = as_f16x2(r);

@@ -95,6 +95,8 @@ struct TgemmArgs {
   int splits;  // K ranges per weight workgroup (MT = 1, one activation block), else 1
   int* counters;  // splits > 1: one per weight workgroup, zero between calls
   float* part;    // splits > 1: [n_wg][splits][NTW] partial 16 x 16 fp32 tiles
+  int glu;        // NTW = 4: rows 4n + {0, 1} of a panel are gate, 4n + {2, 3} the
+                  // matching up rows; y is [M, N / 2] = silu(gate) * up
 };
 
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
@@ -586,6 +588,15 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       uint16_t v[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int j = 0; j < NTW && j < 4; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(sum[j][i]));
+      if constexpr (NTW == 4) {
+        if (a.glu) {
+          // columns 32 p + 2 n and + 1 of the activation, each formed as
+          // pmi_silu_mul_f16 forms it from the fp16 gate and up outputs
+          *reinterpret_cast<uint32_t*>(a.y + (size_t)m * (N >> 1) + 32 * panel + 2 * ln) =
+              glu_pair((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+          continue;
+        }
+      }
       f16* dst = a.y + (size_t)m * N + row0;
       if constexpr (NTW == 4) {
         *reinterpret_cast<uint2*>(dst) = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16),
@@ -808,9 +819,43 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   a.splits = c.splits;
   a.counters = (int*)workspace;
   a.part = c.splits > 1 ? (float*)((uint8_t*)workspace + part_offset) : nullptr;
+  a.glu = 0;
   if (c.mt == 1) return launch_mt<1>(c, a, stream);
   if (c.mt == 2) return launch_mt<2>(c, a, stream);
   return launch_mt<4>(c, a, stream);
+}
+
+
+bool tgemm_glu_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
+  if (!tgemm_supported(M, N, K, gs) || M > 16 || N % 64 != 0) return false;
+  const TgemmConfig c = tgemm_config(M, N, K, gs, false);
+  return c.mt == 1 && c.ntw == 4 && !c.rng && c.splits == 1 && c.grid_m == 1;
+}
+
+hipError_t launch_tgemm_glu(const void* x, const uint8_t* w_tiled, const float* scales_gm,
+                            const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K,
+                            int64_t gs, hipStream_t stream) {
+  if (!tgemm_glu_supported(M, N, K, gs)) return hipErrorInvalidValue;
+  const TgemmConfig c = tgemm_config(M, N, K, gs, false);
+  TgemmArgs a;
+  a.x = (const f16*)x;
+  a.perm = nullptr;
+  a.wt = w_tiled;
+  a.s_gm = scales_gm;
+  a.z_gm = zeros_gm;
+  a.y = (f16*)y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.gs = (int)gs;
+  a.n_wg = c.n_wg;
+  a.grid_m = c.grid_m;
+  a.n_tiles = (int)(4 * (N / 64));
+  a.splits = 1;
+  a.counters = nullptr;
+  a.part = nullptr;
+  a.glu = 1;
+  return launch_mt<1>(c, a, stream);
 }
 
 }  // namespace pmi

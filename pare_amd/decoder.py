@@ -36,7 +36,9 @@ import torch.nn.functional as F
 
 from . import _lib
 from .config import QuantConfig
-from .kernels import _stream_handle, kernel_choice, matmul_w4a16_glu, matmul_w4a16_rmsnorm
+from .kernels import (_stream_handle, gate_up_silu_supported, glu_row_order, kernel_choice,
+                      matmul_w4a16_gate_up_silu, matmul_w4a16_glu, matmul_w4a16_rmsnorm)
+from .pack import sz_group_major, tile_w4a16
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .quant import rtn_quantize
 
@@ -260,8 +262,13 @@ class DecoderLayer(nn.Module):
             qkv, h = self._norm_linear(self.qkv.fused, h, d, self.attn_norm.weight)
             a = decode_attention_rope(qkv.reshape(B, -1), cos_t, sin_t, pos, cache_k, cache_v,
                                       1.0 / math.sqrt(cfg.head_dim))
-            gu, h = self._norm_linear(self.gate_up.fused, h, self.o(a.reshape(B, 1, cfg.hidden)),
-                                      self.mlp_norm.weight)
+            o = self.o(a.reshape(B, 1, cfg.hidden))
+            if B > 1:
+                # several sequences: the norm runs on its own and the MLP may
+                # take the one-launch gate/up + SiLU path
+                n2, h = add_rmsnorm(h, o, self.mlp_norm.weight, cfg.rms_eps)
+                return h, self._mlp(n2, B, T)
+            gu, h = self._norm_linear(self.gate_up.fused, h, o, self.mlp_norm.weight)
             return h, self._down(gu, B, T)
         n1, h = add_rmsnorm(h, d, self.attn_norm.weight, cfg.rms_eps)
         qkv = self.qkv.fused(n1)
@@ -298,7 +305,31 @@ class DecoderLayer(nn.Module):
         return lin(n), h
 
     def _mlp(self, n2, B: int, T: int):
-        return self._down(self.gate_up.fused(n2), B, T)
+        M = B * T
+        gu = self.gate_up.fused
+        if M >= 2 and gu.g_idx is None and gu.bias is None and \
+                gate_up_silu_supported(M, gu.out_features, gu.in_features, gu._group_size()):
+            # 2..16 tokens on the tiled GEMM: SiLU(gate) * up in its epilogue, one
+            # launch less than the fused matmul + silu_mul
+            w_t, sz = self._glu_buffers()
+            act = matmul_w4a16_gate_up_silu(n2.reshape(M, -1).contiguous(), w_t, sz,
+                                            gu._group_size(), gu.out_features)
+            return self.down(act.reshape(B, T, -1))
+        return self._down(gu(n2), B, T)
+
+    def _glu_buffers(self):
+        """Tiled and group-major copies of the fused gate/up weight with its rows
+        in glu_row_order, built on first use (outside graph capture) and kept."""
+        if getattr(self, "_glu", None) is None:
+            gu = self.gate_up.fused
+            w_k, z_u8, _, _ = gu._kernel_buffers()
+            idx = glu_row_order(gu.out_features // 2, w_k.device)
+            gs = gu._group_size()
+            s = gu.scale.reshape(gu.out_features, -1)
+            self._glu = (tile_w4a16(w_k[idx].contiguous(), gs),
+                         sz_group_major(s[idx].contiguous(),
+                                        z_u8.reshape(gu.out_features, -1)[idx].contiguous()))
+        return self._glu
 
     def _down(self, gu, B: int, T: int):
         if B * T == 1 and self.down.g_idx is None:

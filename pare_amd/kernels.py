@@ -231,6 +231,50 @@ def matmul_w4a16_glu(gate_up: torch.Tensor, packed_weight: torch.Tensor, scales:
     return out
 
 
+def glu_row_order(F: int, device=None) -> torch.Tensor:
+    """Row order of a fused [gate (F rows); up (F rows)] weight that
+    ``matmul_w4a16_gate_up_silu`` reads: row 64p + 4n + j of the reordered
+    weight is gate row 32p + 2n + j for j < 2 and up row 32p + 2n + j - 2 for
+    j >= 2, so that each 64-row panel holds 32 gate rows and their up rows.
+    F % 32 == 0."""
+    assert F % 32 == 0, "the interleave needs F % 32 == 0"
+    r = torch.arange(2 * F, device=device)
+    p, t = r // 64, r % 64
+    n, j = t // 4, t % 4
+    return torch.where(j < 2, 32 * p + 2 * n + j, F + 32 * p + 2 * n + j - 2)
+
+
+def gate_up_silu_supported(M: int, N: int, K: int, group_size: int) -> bool:
+    """Whether ``matmul_w4a16_gate_up_silu`` runs this shape (N: rows of the
+    fused gate/up weight)."""
+    return bool(_lib.lib().pmi_gate_up_silu_supported(M, N, K, group_size))
+
+
+def matmul_w4a16_gate_up_silu(x: torch.Tensor, w_tiled: torch.Tensor,
+                              sz_gm: tuple[torch.Tensor, torch.Tensor], group_size: int,
+                              N: int) -> torch.Tensor:
+    """silu(x @ Wg^T) * (x @ Wu^T) in one launch: the tiled GEMM over the fused
+    gate/up weight with its rows in ``glu_row_order`` (``w_tiled``, ``sz_gm``:
+    the tiled and group-major copies of the reordered weight), the activation
+    formed in its epilogue. x fp16 [M, K]; returns fp16 [M, N / 2], equal to
+    the fused matmul followed by ``silu_mul`` bit for bit."""
+    L = _lib.lib()
+    if not x.is_cuda:
+        raise RuntimeError("matmul_w4a16_gate_up_silu requires HIP (cuda) tensors.")
+    assert x.dtype == torch.float16 and x.dim() == 2 and x.is_contiguous(), \
+        "x must be a contiguous float16 [M, K] tensor"
+    M, K = x.shape
+    s_gm, z_gm = sz_gm
+    dev = x.device
+    out = torch.empty(M, N // 2, device=dev, dtype=torch.float16)
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16_gate_up_silu(
+            _aligned16(x).data_ptr(), _aligned16(w_tiled).data_ptr(), _aligned16(s_gm).data_ptr(),
+            z_gm.data_ptr(), out.data_ptr(), M, N, K, group_size, _stream_handle(dev)),
+            "pmi_matmul_w4a16_gate_up_silu")
+    return out
+
+
 def matmul_w4a16_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor,
                          eps: float, packed_weight: torch.Tensor, scales: torch.Tensor,
                          zeros_u8: torch.Tensor, group_size: int):

@@ -272,6 +272,79 @@ def test_glu_down_rejects_what_it_does_not_run():
                                   None) == _lib.PMI_ERR_UNSUPPORTED
 
 
+def _gate_up_layer(F, K, seed):
+    """Fused gate/up weight RTN-quantised on the device: kernel layout [2F,
+    K/2], fp32 scales and u8 zeros [2F, G], and the storage-layout codes and
+    fp32 zeros the oracle dequantises."""
+    from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
+
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    w = torch.randn(2 * F, K, generator=g, device=DEV) * 0.02
+    packed, s, z = P.rtn_quantize(w, 128)
+    return (repack_int4_for_kernel(packed, 128), s.reshape(2 * F, -1).contiguous(),
+            zeros_to_u8(z).reshape(2 * F, -1).contiguous(), packed, s, z)
+
+
+@pytest.mark.parametrize("M,F,K", [(2, 14336, 4096), (4, 14336, 4096), (12, 7168, 1536),
+                                   (16, 7168, 2048), (7, 6144, 3072)])
+def test_gate_up_silu_matches_matmul_then_silu_mul(M, F, K):
+    """The tiled GEMM with SiLU(gate) * up in its epilogue, over the fused weight
+    with its rows in glu_row_order, against the fused matmul on the tiled GEMM
+    (same configuration: four tiles per workgroup) followed by silu_mul: each
+    output row's sum is formed the same way, so the result is equal bit for
+    bit; and against the fp32 oracle within the usual tolerance."""
+    from oracle import pare_oracle as O
+    from pare_amd.kernels import (force_kernel, gate_up_silu_supported, glu_row_order,
+                                  matmul_w4a16, matmul_w4a16_gate_up_silu)
+
+    N = 2 * F
+    assert gate_up_silu_supported(M, N, K, 128)
+    wk, s, zu, packed, s_raw, z_raw = _gate_up_layer(F, K, M + F + K)
+    x = (torch.randn(M, K, generator=torch.Generator(device=DEV).manual_seed(K), device=DEV)).half()
+    with force_kernel("tgemm"):
+        ref = silu_mul(matmul_w4a16(x, wk, s, zu, 128, sz_gm=P.sz_group_major(s, zu),
+                                    w_tiled=P.tile_w4a16(wk, 128)))
+    idx = glu_row_order(F, DEV)
+    got = matmul_w4a16_gate_up_silu(x, P.tile_w4a16(wk[idx].contiguous(), 128),
+                                    P.sz_group_major(s[idx].contiguous(), zu[idx].contiguous()),
+                                    128, N)
+    assert got.shape == (M, F)
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+    # the oracle: fp32-accumulated gate/up outputs rounded to fp16, then
+    # SiLU(gate) * up in fp32
+    w_ref = O.dequantize_packed(packed.cpu().numpy(), s_raw.cpu().numpy(), z_raw.cpu().numpy())
+    gu = torch.from_numpy(O.linear_fp32(x.float().cpu().numpy(), w_ref)).half().float()
+    act = torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]
+    err = (got.float().cpu() - act).abs()
+    print(f"[parity] gate_up_silu M={M} F={F} K={K}: max_abs={err.max().item():.3e}", flush=True)
+    assert torch.allclose(got.float().cpu(), act, rtol=1e-2, atol=1e-2)
+
+
+def test_gate_up_silu_rejects_what_it_does_not_run():
+    L = _lib.lib()
+    assert L.pmi_gate_up_silu_supported(4, 28672, 4096, 128) == 1
+    assert L.pmi_gate_up_silu_supported(4, 2048, 4096, 128) == 0    # one tile per workgroup there
+    assert L.pmi_gate_up_silu_supported(4, 14336, 1024, 128) == 0   # K < 1536
+    assert L.pmi_gate_up_silu_supported(32, 28672, 4096, 128) == 0  # past 16 rows
+    assert L.pmi_matmul_w4a16_gate_up_silu(None, None, None, None, None, 4, 2048, 4096, 128,
+                                           None) == _lib.PMI_ERR_UNSUPPORTED
+
+
+def test_decoder_mlp_gate_up_silu_equals_two_launches():
+    """A full-size decoder layer's MLP at 4 tokens (the batch-4 decode step) on
+    the one-launch gate/up + SiLU path equals the fused matmul + silu_mul +
+    down path bit for bit."""
+    from pare_amd.decoder import DecoderLayer
+
+    layer = DecoderLayer(DecoderConfig(), torch.Generator(device=DEV).manual_seed(9), DEV)
+    n2 = (torch.randn(4, 1, 4096, generator=torch.Generator(device=DEV).manual_seed(2),
+                      device=DEV)).half()
+    got = layer._mlp(n2, 4, 1)
+    ref = layer._down(layer.gate_up.fused(n2), 4, 1)
+    assert layer._glu is not None, "the gate/up + SiLU path did not run"
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("rows,n", [(1, 128256), (4, 128256), (3, 2000), (2, 8), (1, 16392)])
 def test_argmax_matches_torch(rows, n):
     from pare_amd.decoder import argmax_into
