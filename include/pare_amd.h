@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 13
+#define PMI_ABI_VERSION 14
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -244,6 +244,30 @@ PMI_API int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const 
                                      float eps, void* h_out, const uint8_t* w, const float* scales,
                                      const void* zeros, int zero_dtype, void* y, int64_t M,
                                      int64_t N, int64_t K, int64_t group_size, void* stream);
+
+/* The same residual add and pre-norm on the tiled GEMM, for up to 4 rows:
+ * y = (RMSNorm(x + residual) * norm_weight) . dequant(W)^T, or with glu != 0
+ * (the gate/up layout of pmi_matmul_w4a16_gate_up_silu) y = SiLU(gate) * up of
+ * it, [M, N/2]. x, residual (nullable), h_out: fp16 [M, K]; norm_weight fp16
+ * [K]; w_tiled / scales_gm / zeros_gm as for pmi_matmul_w4a16's tiled GEMM.
+ * Every workgroup forms the normalised rows in LDS once, before its first
+ * weight batch, with the rounding and the summation order of
+ * pmi_add_rmsnorm_f16, so y equals pmi_add_rmsnorm_f16 followed by the
+ * matmul (or the gate/up launch) bit for bit; workgroup 0 writes h = x +
+ * residual to h_out. For the shapes pmi_tiled_rmsnorm_supported accepts (M <=
+ * 4, K <= 4096, group_size % 128 == 0, one 16-row activation block), else
+ * PMI_ERR_UNSUPPORTED. No reference counterpart (the reference runs the norm
+ * in PyTorch, pare/eval/throughput.py:84-126). */
+PMI_API int pmi_matmul_w4a16_tiled_rmsnorm(const void* x, const void* residual,
+                                           const void* norm_weight, float eps, void* h_out,
+                                           const uint8_t* w_tiled, const float* scales_gm,
+                                           const uint8_t* zeros_gm, void* y, int64_t M,
+                                           int64_t N, int64_t K, int64_t group_size, int glu,
+                                           void* stream);
+
+/* 1 when pmi_matmul_w4a16_tiled_rmsnorm runs this shape, else 0. Host-only. */
+PMI_API int pmi_tiled_rmsnorm_supported(int64_t M, int64_t N, int64_t K, int64_t group_size,
+                                        int glu);
 
 /* Workspace bytes pmi_matmul_w4a16 uses at full speed for this shape (0 when
  * the chosen kernel needs none). Host-only. No reference counterpart: the

@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -66,6 +66,9 @@ SIGNATURES = {
     "pmi_tgemm_splits": (_i, [_i64, _i64, _i64, _i64, _i]),
     "pmi_matmul_w4a16_gate_up_silu": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "pmi_gate_up_silu_supported": (_i, [_i64, _i64, _i64, _i64]),
+    "pmi_matmul_w4a16_tiled_rmsnorm": (_i, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp,
+                                            _i64, _i64, _i64, _i64, _i, _vp]),
+    "pmi_tiled_rmsnorm_supported": (_i, [_i64, _i64, _i64, _i64, _i]),
     "pmi_set_kernel_override": (_i, [_i]),
     "pmi_add_rmsnorm_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "pmi_rope_kv_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -287,6 +287,38 @@ int pmi_matmul_w4a16_gate_up_silu(const void* x, const uint8_t* w_tiled, const f
                   fn);
 }
 
+int pmi_tiled_rmsnorm_supported(int64_t M, int64_t N, int64_t K, int64_t group_size, int glu) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
+  return pmi::tgemm_norm_supported(M, N, K, group_size, glu != 0) ? 1 : 0;
+}
+
+int pmi_matmul_w4a16_tiled_rmsnorm(const void* x, const void* residual, const void* norm_weight,
+                                   float eps, void* h_out, const uint8_t* w_tiled,
+                                   const float* scales_gm, const uint8_t* zeros_gm, void* y,
+                                   int64_t M, int64_t N, int64_t K, int64_t group_size, int glu,
+                                   void* stream) {
+  const char* fn = "pmi_matmul_w4a16_tiled_rmsnorm";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
+  if (M == 0 || N == 0) return ok();
+  if (!pmi::tgemm_norm_supported(M, N, K, group_size, glu != 0))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: shape not on the fused-norm tiled GEMM (M=%lld N=%lld "
+                "K=%lld gs=%lld glu=%d; see pmi_tiled_rmsnorm_supported)", fn, (long long)M,
+                (long long)N, (long long)K, (long long)group_size, glu);
+  if (!x || !norm_weight || !w_tiled || !scales_gm || !zeros_gm || !y)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (residual && !h_out) return fail(PMI_ERR_INVALID, "%s: a residual needs h_out", fn);
+  if (!aligned(x, 16) || (residual && !aligned(residual, 16)) || !aligned(norm_weight, 16) ||
+      (h_out && !aligned(h_out, 16)) || !aligned(w_tiled, 16) || !aligned(scales_gm, 16) ||
+      !aligned(y, 8))
+    return fail(PMI_ERR_INVALID, "%s: x, residual, norm_weight, h_out, w_tiled and scales_gm must "
+                "be 16-byte aligned, y 8-byte", fn);
+  return from_hip(pmi::launch_tgemm_norm(x, residual, norm_weight, eps, h_out, w_tiled, scales_gm,
+                                         zeros_gm, y, M, N, K, group_size, glu != 0,
+                                         (hipStream_t)stream),
+                  fn);
+}
+
 int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const void* norm_weight,
                              float eps, void* h_out, const uint8_t* w, const float* scales,
                              const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,

@@ -144,6 +144,15 @@ PMI_DEV void copy_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff
 // memory accesses across it.
 PMI_DEV void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
+// Sum over the 64 lanes of a wave, halving distances 32 .. 1: the order of
+// the additions is part of the residual RMSNorm's result, which both the
+// add + RMSNorm kernel and the tiled GEMM's fused norm prologue form with it.
+PMI_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 // MFMA B operand: 8 nibbles (the low nibbles of the bytes of t0, t1, already
 // masked to 0x0F0F0F0F) as fp16 (q - z) in byte order, exact: v_perm_b32 puts
 // each nibble under a 0x64 exponent byte (1024 + q) and a packed add of

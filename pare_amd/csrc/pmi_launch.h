@@ -234,5 +234,13 @@ bool tgemm_glu_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 hipError_t launch_tgemm_glu(const void* x, const uint8_t* w_tiled, const float* scales_gm,
                             const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K,
                             int64_t gs, hipStream_t stream);
+// The residual add + RMSNorm fused into the tiled GEMM's activation load (y =
+// (RMSNorm(x + r) * norm_w) . W^T, or its silu(gate) * up with glu), up to 4
+// rows, K <= 4096, gs % 128 == 0; h = x + r to h_out when r is given.
+bool tgemm_norm_supported(int64_t M, int64_t N, int64_t K, int64_t gs, bool glu);
+hipError_t launch_tgemm_norm(const void* x, const void* r, const void* norm_w, float eps, void* h_out,
+                             const uint8_t* w_tiled, const float* scales_gm, const uint8_t* zeros_gm,
+                             void* y, int64_t M, int64_t N, int64_t K, int64_t gs, bool glu,
+                             hipStream_t stream);
 
 }  // namespace pmi

@@ -50,6 +50,13 @@
 // one step ahead of the MFMAs. A workgroup reads X once either way, so the
 // gather adds the 4K-byte table to its L2 traffic and no launch.
 //
+// Residual add + RMSNorm (NORM, up to 4 rows, K <= 4096). Every workgroup
+// reads the rows of x and of the residual ahead of its first weight loads,
+// forms h = x + r, the per-row statistic and the normalised rows exactly as
+// the add + RMSNorm kernel does (same per-thread chunks and summation order),
+// and keeps them in LDS; the compute waves read their A operands there. The
+// launch then equals the norm launch followed by the plain one bit for bit.
+//
 // Pipeline. Each compute wave keeps a three-deep register ring of units
 // (weights, scales, zero points and, for MT = 1, activations): the loads of
 // step s + 2 are issued before step s is computed. The loop runs whole rounds
@@ -97,6 +104,13 @@ struct TgemmArgs {
   float* part;    // splits > 1: [n_wg][splits][NTW] partial 16 x 16 fp32 tiles
   int glu;        // NTW = 4: rows 4n + {0, 1} of a panel are gate, 4n + {2, 3} the
                   // matching up rows; y is [M, N / 2] = silu(gate) * up
+  // NORM: the activations are RMSNorm(x + r) * nw (r nullable), formed once
+  // per workgroup into LDS; workgroup 0 writes h = x + r to h_out when r is
+  // given
+  const f16* r;
+  const f16* nw;
+  f16* h_out;
+  float eps;
 };
 
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
@@ -117,6 +131,7 @@ struct Unit {
   ZeroT<NTW> z[RNG ? 1 : GPU];
   float sr[RNG ? NTW : 1];
   uint8_t zr[RNG ? NTW : 1];
+  int xo;  // NORM: byte offset of the unit's 128 columns in an LDS activation row
 };
 
 // K split: the NTW partial 16 x 16 tiles of split sp go to the workspace;
@@ -175,9 +190,11 @@ __device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int s
 // than one 64-row panel per CU), the last ones clamped and not stored.
 // SPLIT: a K range of a split weight workgroup (a.splits > 1); a variant of its
 // own, so that unsplit launches carry none of its index arithmetic.
-template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false>
+template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false, bool NORM = false>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
+  static_assert(!NORM || (MT == 1 && GPU == 1 && !GATHER && !RNG && !SPLIT),
+                "the fused norm is built for up to 4 rows, gs % 128 == 0, one K range");
   static_assert(!RNG || (MT == 1 && GPU == 1), "tile ranges are built for up to 16 rows, gs >= 128");
   static_assert(!SPLIT || (MT == 1 && !RNG), "the K split is built for up to 16 rows");
   using UnitT = Unit<MT, NTW, GPU, RNG>;
@@ -201,9 +218,12 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // GATHER: the activation rows and the perm table in dynamic LDS sized by the
   // host (max(M (2K + 16) + 4K, the partial tiles)), so that small row counts
   // leave room for other workgroups; reused after the loop for the partial tiles
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s[GATHER ? 16 : kLds0];
+  // NORM: the normalised activation rows (stride 2K + 16 bytes) in dynamic LDS
+  // of max(M (2K + 16), the partial tiles)
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s[GATHER || NORM ? 16 : kLds0];
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_d[];
-  uint8_t* const lds = GATHER ? lds_d : lds_s;
+  uint8_t* const lds = GATHER || NORM ? lds_d : lds_s;
+  __shared__ float npart[NORM ? 4 * kKW : 1];  // NORM: per-row, per-wave sums of h^2
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -311,7 +331,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     int xrow = 0;                     // GATHER: LDS offset of the lane's row
     if constexpr (MT == 1) {
       const int mg = m0 + ln < M ? m0 + ln : M - 1;
-      if constexpr (GATHER) {
+      if constexpr (GATHER || NORM) {
         xrow = mg * xstride;
       } else {
         rxd = rsrc(a.x, (int64_t)M * K * 2);
@@ -378,11 +398,12 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       // past the range: re-read the wave's last unit (loaded, never computed)
       const int u = kKW * (q_lo + (s < steps ? s : steps - 1)) + kw;
       const int uu = __builtin_amdgcn_readfirstlane(u);
-      if constexpr (MT == 1 && !GATHER) {
+      if constexpr (MT == 1 && !GATHER && !NORM) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           un.xa[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rxd, vxd, uu * 256 + 64 * t, 0));
       }
+      if constexpr (NORM) un.xo = uu * 256;
       if constexpr (RNG) {
         const int g = uu / upg;
 #pragma unroll
@@ -429,7 +450,9 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         f16x8 A[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          if constexpr (MT == 1) A[mt] = __builtin_bit_cast(f16x8, un.xa[t]);
+          if constexpr (NORM)
+            A[mt] = *reinterpret_cast<const f16x8*>(lds + xrow + un.xo + 64 * t + 16 * h);
+          else if constexpr (MT == 1) A[mt] = __builtin_bit_cast(f16x8, un.xa[t]);
           else if constexpr (HALF)
             A[mt] = *reinterpret_cast<const f16x8*>(xb + (16 * mt + ln) * RB +
                                                      (((4 * (t & 1) + h) ^ ((ln >> 1) % CH)) << 4));
@@ -466,9 +489,85 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       stage_issue();
       __builtin_amdgcn_sched_barrier(0);
     }
+    // NORM: x, r and the norm weight of every thread's columns, issued ahead
+    // of the ring's first loads so that waiting for them leaves those in
+    // flight. Thread t holds columns (i * 256 + t) * 8 .. + 7 of every row,
+    // i < 2, the chunks pmi_add_rmsnorm_f16's thread t holds (K <= 4096).
+    u32x4 nx[NORM ? 4 : 1][2], nr[NORM ? 4 : 1][2], nwv[2];
+    if constexpr (NORM) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = (i * 256 + tid) * 8, cc = c < K ? c : 0;
+        nwv[i] = *reinterpret_cast<const u32x4*>(a.nw + cc);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int mm = m < M ? m : M - 1;
+          nx[m][i] = *reinterpret_cast<const u32x4*>(a.x + (size_t)mm * K + cc);
+          if (a.r) nr[m][i] = *reinterpret_cast<const u32x4*>(a.r + (size_t)mm * K + cc);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int d = 0; d < kDW - 1; ++d) {
       issue(ring[d], d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (NORM) {
+      // h = x + r rounded to fp16 and sum(h^2) per row in the order of
+      // pmi_add_rmsnorm_f16 (each thread's chunks in column order, then the
+      // wave butterfly, then the four waves in order), so that the normalised
+      // activations are bit-identical to its output
+      wait_vmcnt_lgkm0<(kDW - 1) * (NTW + 2 * GPU)>();
+      __builtin_amdgcn_sched_barrier(0);
+      f16x8 hv[4][2];
+      float ss[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        ss[m] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int c = (i * 256 + tid) * 8;
+          const f16x8 xv = __builtin_bit_cast(f16x8, nx[m][i]);
+          f16x8 hh = xv;
+          if (a.r) {
+            const f16x8 rv = __builtin_bit_cast(f16x8, nr[m][i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hh[e] = (f16)((float)xv[e] + (float)rv[e]);
+          }
+          hv[m][i] = hh;
+          if (c < K && m < M) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss[m] += (float)hh[e] * (float)hh[e];
+            if (a.r && blockIdx.x == 0) *reinterpret_cast<f16x8*>(a.h_out + (size_t)m * K + c) = hh;
+          }
+        }
+        ss[m] = wave_sum(ss[m]);
+        if (l == 0) npart[4 * m + wv] = ss[m];
+      }
+      wait_vmcnt_lgkm0<(kDW - 1) * (NTW + 2 * GPU)>();
+      barrier_only();
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= M) break;
+        const float inv = rsqrtf((npart[4 * m] + npart[4 * m + 1] + npart[4 * m + 2] + npart[4 * m + 3]) /
+                                     (float)K + a.eps);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int c = (i * 256 + tid) * 8;
+          if (c >= K) continue;
+          const f16x8 wv8 = __builtin_bit_cast(f16x8, nwv[i]);
+          f16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (f16)((float)hv[m][i][e] * inv * (float)wv8[e]);
+          *reinterpret_cast<f16x8*>(lds + m * xstride + 2 * c) = o;
+        }
+      }
+      // every row is in LDS before any wave reads it; the scheduling fences
+      // keep the loop's work below the barrier
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt_lgkm0<(kDW - 1) * (NTW + 2 * GPU)>();
+      barrier_only();
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (GATHER) {
@@ -635,6 +734,18 @@ hipError_t launch_variant(const TgemmConfig& c, const TgemmArgs& a, hipStream_t 
   }
   hipLaunchKernelGGL((w4a16_tgemm_kernel<MT, NTW, GPU, GATHER, RNG, SPLIT>), dim3(c.grid), block, lds,
                      stream, a);
+  return hipGetLastError();
+}
+
+// The fused-norm variants (one activation block, one K range): the
+// normalised rows in dynamic LDS, at most 4 (2 * 4096 + 16) bytes, within the
+// default limit.
+template <int NTW>
+hipError_t launch_norm_variant(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
+  const size_t need = (size_t)a.M * (2 * a.K + 16);
+  const size_t red = (size_t)kKW * NTW * 64 * 16;
+  hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW, 1, false, false, false, true>), dim3(c.grid),
+                     dim3(kKW * 64), need > red ? need : red, stream, a);
   return hipGetLastError();
 }
 
@@ -856,6 +967,50 @@ hipError_t launch_tgemm_glu(const void* x, const uint8_t* w_tiled, const float* 
   a.part = nullptr;
   a.glu = 1;
   return launch_mt<1>(c, a, stream);
+}
+
+// The residual add and RMSNorm in the tiled GEMM (up to 4 rows, K <= 4096,
+// gs % 128 == 0), where the plain launch takes one K range and one activation
+// block (so that both add the same products in the same order; a K split
+// would also form the norm once per range).
+bool tgemm_norm_supported(int64_t M, int64_t N, int64_t K, int64_t gs, bool glu) {
+  if (!tgemm_supported(M, N, K, gs) || M > 4 || K > 4096 || gs % 128 != 0) return false;
+  const TgemmConfig c = tgemm_config(M, N, K, gs, false);
+  if (c.mt != 1 || c.rng || c.grid_m != 1 || c.splits > 1) return false;
+  return !glu || (c.ntw == 4 && N % 64 == 0);
+}
+
+hipError_t launch_tgemm_norm(const void* x, const void* r, const void* norm_w, float eps, void* h_out,
+                             const uint8_t* w_tiled, const float* scales_gm, const uint8_t* zeros_gm,
+                             void* y, int64_t M, int64_t N, int64_t K, int64_t gs, bool glu,
+                             hipStream_t stream) {
+  if (!tgemm_norm_supported(M, N, K, gs, glu)) return hipErrorInvalidValue;
+  const TgemmConfig c = tgemm_config(M, N, K, gs, false);
+  TgemmArgs a;
+  a.x = (const f16*)x;
+  a.perm = nullptr;
+  a.wt = w_tiled;
+  a.s_gm = scales_gm;
+  a.z_gm = zeros_gm;
+  a.y = (f16*)y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.gs = (int)gs;
+  a.n_wg = c.n_wg;
+  a.grid_m = 1;
+  a.n_tiles = (int)(4 * ((N + 63) / 64));
+  a.splits = 1;
+  a.counters = nullptr;
+  a.part = nullptr;
+  a.glu = glu ? 1 : 0;
+  a.r = (const f16*)r;
+  a.nw = (const f16*)norm_w;
+  a.h_out = (f16*)h_out;
+  a.eps = eps;
+  if (c.ntw == 4) return launch_norm_variant<4>(c, a, stream);
+  if (c.ntw == 2) return launch_norm_variant<2>(c, a, stream);
+  return launch_norm_variant<1>(c, a, stream);
 }
 
 }  // namespace pmi

@@ -37,7 +37,8 @@ import torch.nn.functional as F
 from . import _lib
 from .config import QuantConfig
 from .kernels import (_stream_handle, gate_up_silu_supported, glu_row_order, kernel_choice,
-                      matmul_w4a16_gate_up_silu, matmul_w4a16_glu, matmul_w4a16_rmsnorm)
+                      matmul_w4a16_gate_up_silu, matmul_w4a16_glu, matmul_w4a16_rmsnorm,
+                      matmul_w4a16_tiled_rmsnorm, tiled_rmsnorm_supported)
 from .pack import sz_group_major, tile_w4a16
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .quant import rtn_quantize
@@ -264,10 +265,9 @@ class DecoderLayer(nn.Module):
                                       1.0 / math.sqrt(cfg.head_dim))
             o = self.o(a.reshape(B, 1, cfg.hidden))
             if B > 1:
-                # several sequences: the norm runs on its own and the MLP may
-                # take the one-launch gate/up + SiLU path
-                n2, h = add_rmsnorm(h, o, self.mlp_norm.weight, cfg.rms_eps)
-                return h, self._mlp(n2, B, T)
+                # several sequences: the gate/up launch on the tiled GEMM forms
+                # the norm and SiLU(gate) * up itself where it can
+                return self._norm_mlp(h, o, B, T)
             gu, h = self._norm_linear(self.gate_up.fused, h, o, self.mlp_norm.weight)
             return h, self._down(gu, B, T)
         n1, h = add_rmsnorm(h, d, self.attn_norm.weight, cfg.rms_eps)
@@ -301,8 +301,40 @@ class DecoderLayer(nn.Module):
             if lin.bias is not None:
                 y = y + lin.bias
             return y.reshape(B, T, -1), h2.reshape(B, T, K)
+        # 2..4 rows on the tiled GEMM: the norm formed in its prologue
+        if 2 <= M <= 4 and lin.g_idx is None and \
+                tiled_rmsnorm_supported(M, lin.out_features, K, lin._group_size()) and \
+                kernel_choice(M, lin.out_features, K, lin._group_size(), tiled=True) == "tgemm":
+            w_k, _, _, sz_gm = lin._kernel_buffers()
+            w_t = lin._tiled_buffer(w_k, M)
+            if w_t is not None:
+                y, h2 = matmul_w4a16_tiled_rmsnorm(
+                    h.reshape(M, K), d.reshape(M, K) if d is not None else None, norm_w,
+                    self.cfg.rms_eps, w_t, sz_gm, lin._group_size(), lin.out_features)
+                if lin.bias is not None:
+                    y = y + lin.bias
+                return y.reshape(B, T, -1), h2.reshape(B, T, K)
         n, h = add_rmsnorm(h, d, norm_w, self.cfg.rms_eps)
         return lin(n), h
+
+    def _norm_mlp(self, h, o, B: int, T: int):
+        """(h + o, the MLP of RMSNorm(h + o)) for several one-token sequences:
+        one gate/up launch with the norm in its prologue and SiLU(gate) * up in
+        its epilogue where the tiled GEMM takes the shape, else add_rmsnorm and
+        _mlp."""
+        M, K = B * T, h.shape[-1]
+        gu = self.gate_up.fused
+        gs = gu._group_size()
+        if 2 <= M <= 4 and gu.g_idx is None and gu.bias is None and \
+                gate_up_silu_supported(M, gu.out_features, K, gs) and \
+                tiled_rmsnorm_supported(M, gu.out_features, K, gs, glu=True):
+            w_t, sz = self._glu_buffers()
+            act, h2 = matmul_w4a16_tiled_rmsnorm(
+                h.reshape(M, K).contiguous(), o.reshape(M, K).contiguous(), self.mlp_norm.weight,
+                self.cfg.rms_eps, w_t, sz, gs, gu.out_features, glu=True)
+            return h2.reshape(B, T, K), self.down(act.reshape(B, T, -1))
+        n2, h = add_rmsnorm(h, o, self.mlp_norm.weight, self.cfg.rms_eps)
+        return h, self._mlp(n2, B, T)
 
     def _mlp(self, n2, B: int, T: int):
         M = B * T

@@ -315,6 +315,49 @@ def matmul_w4a16_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, norm_we
     return out, h
 
 
+def tiled_rmsnorm_supported(M: int, N: int, K: int, group_size: int, glu: bool = False) -> bool:
+    """True when ``matmul_w4a16_tiled_rmsnorm`` runs this shape (2..4 rows in
+    practice, K <= 4096, group_size % 128 == 0)."""
+    return bool(_lib.lib().pmi_tiled_rmsnorm_supported(M, N, K, group_size, int(glu)))
+
+
+def matmul_w4a16_tiled_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None,
+                               norm_weight: torch.Tensor, eps: float, w_tiled: torch.Tensor,
+                               sz_gm: tuple[torch.Tensor, torch.Tensor], group_size: int, N: int,
+                               glu: bool = False):
+    """(Y, h) with h = x + residual (x when residual is None) and
+    Y = (RMSNorm(h) * norm_weight) @ dequant(W)^T on the tiled GEMM, one
+    launch; with ``glu`` the weight is the gate/up layout of
+    ``matmul_w4a16_gate_up_silu`` and Y = silu(gate) * up, [M, N / 2]. Equal
+    bit for bit to ``add_rmsnorm`` followed by the matmul (or the gate/up
+    launch). x, residual fp16 [M, K]; norm_weight fp16 [K]; ``w_tiled``,
+    ``sz_gm`` the tiled and group-major copies."""
+    L = _lib.lib()
+    if not x.is_cuda:
+        raise RuntimeError("matmul_w4a16_tiled_rmsnorm requires HIP (cuda) tensors.")
+    assert x.dtype == torch.float16 and x.dim() == 2 and x.is_contiguous(), \
+        "x must be a contiguous float16 [M, K] tensor"
+    M, K = x.shape
+    assert norm_weight.dtype == torch.float16 and norm_weight.numel() == K
+    s_gm, z_gm = sz_gm
+    dev = x.device
+    r = None
+    h = x
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == torch.float16
+        r = _aligned16(residual.contiguous())
+        h = torch.empty_like(x)   # never aliases x or residual: other workgroups still read them
+    out = torch.empty(M, N // 2 if glu else N, device=dev, dtype=torch.float16)
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16_tiled_rmsnorm(
+            _aligned16(x).data_ptr(), r.data_ptr() if r is not None else None,
+            _aligned16(norm_weight.contiguous()).data_ptr(), eps,
+            h.data_ptr() if r is not None else None, _aligned16(w_tiled).data_ptr(),
+            _aligned16(s_gm).data_ptr(), z_gm.data_ptr(), out.data_ptr(), M, N, K, group_size,
+            int(glu), _stream_handle(dev)), "pmi_matmul_w4a16_tiled_rmsnorm")
+    return out, h
+
+
 _KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4, "tgemm": 5}
 
 

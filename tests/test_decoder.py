@@ -345,6 +345,112 @@ def test_decoder_mlp_gate_up_silu_equals_two_launches():
     assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
 
 
+def _norm_inputs(M, K, seed, residual=True):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=DEV).half()
+    r = torch.randn(M, K, generator=g, device=DEV).half() if residual else None
+    nw = (1.0 + 0.1 * torch.randn(K, generator=g, device=DEV)).half()
+    return x, r, nw
+
+
+@pytest.mark.parametrize("M,N,K,res", [(4, 6144, 4096, True), (2, 6144, 4096, False),
+                                       (3, 4096, 4096, True), (4, 4608, 3584, True),
+                                       (4, 4096, 2048, True), (1, 6144, 4096, True)])
+def test_tiled_rmsnorm_matches_add_rmsnorm_then_matmul(M, N, K, res):
+    """The residual add and RMSNorm formed in the tiled GEMM's prologue against
+    add_rmsnorm followed by the matmul on the tiled GEMM (the same unsplit
+    configuration): the normalised activations are formed with the same
+    roundings and summation order, so y and h are equal bit for bit; and y
+    against the fp32 oracle on those activations."""
+    from oracle import pare_oracle as O
+    from pare_amd.kernels import (force_kernel, matmul_w4a16, matmul_w4a16_tiled_rmsnorm,
+                                  tiled_rmsnorm_supported)
+    from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
+
+    assert tiled_rmsnorm_supported(M, N, K, 128)
+    g = torch.Generator(device=DEV).manual_seed(M * N + K)
+    w = torch.randn(N, K, generator=g, device=DEV) * 0.02
+    packed, s_raw, z_raw = P.rtn_quantize(w, 128)
+    wk = repack_int4_for_kernel(packed, 128)
+    s = s_raw.reshape(N, -1).contiguous()
+    zu = zeros_to_u8(z_raw).reshape(N, -1).contiguous()
+    sz, wt = P.sz_group_major(s, zu), P.tile_w4a16(wk, 128)
+    x, r, nw = _norm_inputs(M, K, N + K, res)
+    eps = 1e-5
+    n_ref, h_ref = add_rmsnorm(x, r, nw, eps)
+    with force_kernel("tgemm"):
+        y_ref = matmul_w4a16(n_ref, wk, s, zu, 128, sz_gm=sz, w_tiled=wt)
+    for _ in range(2):
+        y, h = matmul_w4a16_tiled_rmsnorm(x, r, nw, eps, wt, sz, 128, N)
+        assert torch.equal(h, h_ref)
+        assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
+    w_ref = O.dequantize_packed(packed.cpu().numpy(), s_raw.cpu().numpy(), z_raw.cpu().numpy())
+    ref = torch.from_numpy(O.linear_fp32(n_ref.float().cpu().numpy(), w_ref))
+    err = (y.float().cpu() - ref).abs()
+    print(f"[parity] tiled_rmsnorm M={M} N={N} K={K}: max_abs={err.max().item():.3e}", flush=True)
+    assert torch.allclose(y.float().cpu(), ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("M,F,K", [(4, 14336, 4096), (2, 14336, 4096), (3, 18944, 3584)])
+def test_tiled_rmsnorm_glu_matches_norm_then_gate_up_silu(M, F, K):
+    """Norm in the prologue and SiLU(gate) * up in the epilogue of one gate/up
+    launch against add_rmsnorm followed by the gate/up + SiLU launch, bit for
+    bit."""
+    from pare_amd.kernels import (glu_row_order, matmul_w4a16_gate_up_silu,
+                                  matmul_w4a16_tiled_rmsnorm, tiled_rmsnorm_supported)
+
+    N = 2 * F
+    assert tiled_rmsnorm_supported(M, N, K, 128, glu=True)
+    wk, s, zu, _, _, _ = _gate_up_layer(F, K, M + F + K)
+    idx = glu_row_order(F, DEV)
+    wt = P.tile_w4a16(wk[idx].contiguous(), 128)
+    sz = P.sz_group_major(s[idx].contiguous(), zu[idx].contiguous())
+    x, r, nw = _norm_inputs(M, K, F + K)
+    n_ref, h_ref = add_rmsnorm(x, r, nw, 1e-5)
+    ref = matmul_w4a16_gate_up_silu(n_ref, wt, sz, 128, N)
+    got, h = matmul_w4a16_tiled_rmsnorm(x, r, nw, 1e-5, wt, sz, 128, N, glu=True)
+    assert got.shape == (M, F)
+    assert torch.equal(h, h_ref)
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+
+
+def test_tiled_rmsnorm_rejects_what_it_does_not_run():
+    L = _lib.lib()
+    assert L.pmi_tiled_rmsnorm_supported(4, 6144, 4096, 128, 0) == 1
+    assert L.pmi_tiled_rmsnorm_supported(4, 28672, 4096, 128, 1) == 1
+    assert L.pmi_tiled_rmsnorm_supported(5, 6144, 4096, 128, 0) == 0   # past 4 rows
+    assert L.pmi_tiled_rmsnorm_supported(4, 6144, 8192, 128, 0) == 0   # K > 4096
+    assert L.pmi_tiled_rmsnorm_supported(4, 6144, 4096, 64, 0) == 0    # gs 64
+    assert L.pmi_tiled_rmsnorm_supported(4, 6144, 4096, 128, 1) == 0   # glu needs four-tile workgroups
+    assert L.pmi_tiled_rmsnorm_supported(4, 512, 4096, 128, 0) == 0    # the plain launch splits K
+    assert L.pmi_matmul_w4a16_tiled_rmsnorm(None, None, None, 1e-5, None, None, None, None, None,
+                                            5, 6144, 4096, 128, 0, None) == _lib.PMI_ERR_UNSUPPORTED
+
+
+def test_decoder_norm_paths_equal_separate_launches():
+    """A full-size decoder layer at 4 tokens (the batch-4 decode step): q/k/v
+    and the gate/up + SiLU launch with the norm in their prologue equal
+    add_rmsnorm followed by the layer's own launches, bit for bit, with and
+    without the pending residual."""
+    from pare_amd.decoder import DecoderLayer
+
+    cfg = DecoderConfig()
+    layer = DecoderLayer(cfg, torch.Generator(device=DEV).manual_seed(9), DEV)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    h = torch.randn(4, 1, 4096, generator=g, device=DEV).half()
+    d = torch.randn(4, 1, 4096, generator=g, device=DEV).half()
+    for pending in (d, None):
+        y, h2 = layer._norm_linear(layer.qkv.fused, h, pending, layer.attn_norm.weight)
+        n, h_ref = add_rmsnorm(h, pending, layer.attn_norm.weight, cfg.rms_eps)
+        assert torch.equal(h2, h_ref)
+        assert torch.equal(y, layer.qkv.fused(n)), (y.float() - layer.qkv.fused(n).float()).abs().max()
+    h3, out = layer._norm_mlp(h, d, 4, 1)
+    n2, h_ref2 = add_rmsnorm(h, d, layer.mlp_norm.weight, cfg.rms_eps)
+    assert layer._glu is not None, "the gate/up + SiLU path did not run"
+    assert torch.equal(h3, h_ref2)
+    assert torch.equal(out, layer._mlp(n2, 4, 1))
+
+
 @pytest.mark.parametrize("rows,n", [(1, 128256), (4, 128256), (3, 2000), (2, 8), (1, 16392)])
 def test_argmax_matches_torch(rows, n):
     from pare_amd.decoder import argmax_into
