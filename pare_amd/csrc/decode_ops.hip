@@ -242,7 +242,9 @@ __global__ __launch_bounds__(1024) void decode_attention_kernel(
 // batches too small to fill the chip with one workgroup per (b, KV head).
 // Workgroup (split s, b * KV + kh) takes positions 64 s .. 64 s + 63, one
 // wave per query head of the group and one lane per position for the
-// scores. It writes the split's partial (max m, sum l, unnormalised P V) to
+// scores; the split's K and V rows are staged in LDS once for all its waves
+// (coalesced buffer -> LDS copies issued first thing). It writes the split's
+// partial (max m, sum l, unnormalised P V) to
 // the workspace; the last workgroup of a (b, kh) to arrive, counted with an
 // agent-scope atomic, combines the splits in order (deterministic) and
 // resets the counter. Partials are stored and loaded with the device-scope
@@ -267,6 +269,11 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
   __shared__ int last_flag;
   __shared__ __attribute__((aligned(16))) f16 qrot[ROPE ? 4 : 1][D];
   __shared__ __attribute__((aligned(16))) f16 kvnew[ROPE ? 2 : 1][D];
+  // the split's K and V rows (64 x 256 bytes each); 16-byte chunk c of row r
+  // sits in slot c ^ (r % 16) of the row, so that the 16 lanes reading chunk c
+  // of 16 different rows, and the 16 lanes reading 16 chunks of one row, hit
+  // 16 different bank groups
+  __shared__ __attribute__((aligned(16))) uint8_t kvs[2][kSplitPos * D * 2];
   const int sidx = blockIdx.x, bk = blockIdx.y;
   const int b = bk / KV, kh = bk - (bk / KV) * KV;
   const int group = H / KV;
@@ -283,6 +290,25 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
   // byte offset of this split's record (wave-uniform)
   const int rec = __builtin_amdgcn_readfirstlane(((b * H + h) * S + sidx) * kPartFloats * 4);
   const int pc = (int)(p < 0 ? 0 : (p >= L ? L - 1 : p));  // the new token's cache row
+
+  // Stage the split's K and V rows once for all query-head waves, straight
+  // into LDS, before anything waits: 16 copies of 1 KiB (4 rows) per tensor,
+  // dealt to the waves; rows past the cache are clamped into it (read, never
+  // used). Every lane then reads its rows from LDS: loaded by each lane from
+  // L2 (a 256-byte row per lane, the same rows in every wave) the score loads
+  // touched 64 lines per instruction.
+  {
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kb, (int64_t)L * D * 2);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(vb, (int64_t)L * D * 2);
+    const int nwv = (int)(blockDim.x >> 6);
+    for (int c = g; c < kSplitPos / 4; c += nwv) {
+      const int r = 4 * c + (l >> 4);
+      const int jr = min(j0 + r, L - 1);
+      const int voff = jr * (D * 2) + 16 * ((l & 15) ^ (r & 15));
+      copy_to_lds<16>(rk, kvs[0] + c * 1024, voff, 0);
+      copy_to_lds<16>(rv, kvs[1] + c * 1024, voff, 0);
+    }
+  }
 
   if constexpr (ROPE) {
     if (j1 > j0) {
@@ -309,8 +335,10 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
         cache_v[crow + d + D / 2] = v2;
       }
     }
-    __syncthreads();
   }
+  // the staged rows (counted as pending LDS stores by the fence) and the
+  // rotated q / new row are in LDS
+  __syncthreads();
 
   float m = -INFINITY, lsum = 0.f;
   float acc[8];
@@ -326,27 +354,17 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
       const u32x4 v = q4[i];
       qp[4 * i] = v.x; qp[4 * i + 1] = v.y; qp[4 * i + 2] = v.z; qp[4 * i + 3] = v.w;
     }
-    // V rows of this lane's positions (j0 + 4k + ps), issued before the scores
-    // so that they are in flight during the K loads and the softmax (the new
-    // token's row comes from LDS under ROPE)
-    u32x4 vv[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int j = j0 + 4 * k + ps;
-      const int jj = j < j1 ? j : j0;
-      const f16* vrow = (ROPE && jj == pc) ? &kvnew[ROPE ? 1 : 0][0] : vb + (size_t)jj * D;
-      vv[k] = *reinterpret_cast<const u32x4*>(vrow + 8 * dc);
-    }
     const int j = j0 + l;
     const bool live = j < j1;
     float sc = -INFINITY;
     if (live) {
-      const f16* krow = (ROPE && j == pc) ? &kvnew[0][0] : kb + (size_t)j * D;
-      const u32x4* k4 = reinterpret_cast<const u32x4*>(krow);
+      // row l of the split, or the new token's k (LDS under ROPE)
+      const bool fresh = ROPE && j == pc;
+      const uint8_t* krow = fresh ? reinterpret_cast<const uint8_t*>(&kvnew[0][0]) : kvs[0] + l * (D * 2);
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < D / 8; ++i) {
-        const u32x4 kv = k4[i];
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(krow + 16 * (fresh ? i : (i ^ (l & 15))));
         d = dot2_acc(as_f16x2(kv.x), qp[4 * i], d);
         d = dot2_acc(as_f16x2(kv.y), qp[4 * i + 1], d);
         d = dot2_acc(as_f16x2(kv.z), qp[4 * i + 2], d);
@@ -357,10 +375,18 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
     m = wave_max(sc);
     const float e = live ? __expf(sc - m) : 0.f;
     lsum = wave_sum(e);
+    // P V: lane (ps, dc) takes dims 8 dc .. 8 dc + 7 of positions j0 + 4 k + ps
+    // (positions past j1 read row 0 of the split, weighted 0)
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
+      const int jv = j0 + 4 * k + ps;
+      const int r = jv < j1 ? 4 * k + ps : 0;
+      const bool fresh = ROPE && j0 + r == pc;
+      const u32x4 vv = *reinterpret_cast<const u32x4*>(
+          fresh ? reinterpret_cast<const uint8_t*>(&kvnew[ROPE ? 1 : 0][0]) + 16 * dc
+                : kvs[1] + r * (D * 2) + 16 * (dc ^ (r & 15)));
       const float pk = __shfl(e, 4 * k + ps);  // 0 for positions past j1
-      const f16x8 h8 = __builtin_bit_cast(f16x8, vv[k]);
+      const f16x8 h8 = __builtin_bit_cast(f16x8, vv);
 #pragma unroll
       for (int x = 0; x < 8; ++x) acc[x] = fmaf(pk, (float)h8[x], acc[x]);
     }
@@ -390,14 +416,15 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
   if (!last_flag) return;
 
   // Last to arrive: combine the S splits of head h in split order, with the
-  // running max rescaling, eight splits per round of loads (each lane reads
-  // the splits' (m, l) and its dims 2l and 2l + 1).
+  // running max rescaling, sixteen splits per round of loads (each lane reads
+  // the splits' (m, l) and its dims 2l and 2l + 1): one round trip up to 1024
+  // cache positions.
   const int rec0 = __builtin_amdgcn_readfirstlane((b * H + h) * S * kPartFloats * 4);
   float mx = -INFINITY, tot = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int s0 = 0; s0 < S; s0 += 8) {
-    float ms[8], ls[8], a0[8], a1[8];
+  for (int s0 = 0; s0 < S; s0 += 16) {
+    float ms[16], ls[16], a0[16], a1[16];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < 16; ++k) {
       const int sk = min(s0 + k, S - 1);  // past the end: skipped below
       const int off = __builtin_amdgcn_readfirstlane(rec0 + sk * kPartFloats * 4);
       ms[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, 4 * D, off, kSc1));
@@ -410,7 +437,7 @@ __global__ __launch_bounds__(256) void decode_attention_split_kernel(
     // trip each
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < 16; ++k) {
       const bool use = s0 + k < S && ms[k] != -INFINITY;  // uniform across the wave
       const float nm = fmaxf(mx, ms[k]);
       const float fo = mx == -INFINITY ? 0.f : __expf(mx - nm);
