@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 14
+#define PMI_ABI_VERSION 15
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -244,6 +244,38 @@ PMI_API int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const 
                                      float eps, void* h_out, const uint8_t* w, const float* scales,
                                      const void* zeros, int zero_dtype, void* y, int64_t M,
                                      int64_t N, int64_t K, int64_t group_size, void* stream);
+
+/* The residual add moved into the launch that forms the residual stream, one
+ * activation row: h = residual + (x . dequant(W)^T), each element rounded to
+ * fp16 and then added as pmi_add_rmsnorm_f16 adds (h may alias residual);
+ * with glu != 0, x is the fused gate/up output [1, 2K] consumed as
+ * SiLU(gate) * up (as pmi_matmul_w4a16_glu). stats[g] receives workgroup g's
+ * sum of h^2 over its rows, pmi_residual_stats_count(N, K, glu) floats, for a
+ * following pmi_matmul_w4a16_prenormed. zeros u8 [N, G], kernel layout, no
+ * act_order. PMI_ERR_UNSUPPORTED where the count is 0 (rows of one GEMV
+ * slice, K <= 2048). No reference counterpart (the reference adds the
+ * residual in PyTorch, pare/eval/throughput.py:84-126). */
+PMI_API int pmi_matmul_w4a16_residual(const void* x, int glu, const void* residual, float* stats,
+                                      const uint8_t* w, const float* scales,
+                                      const uint8_t* zeros_u8, void* h, int64_t N, int64_t K,
+                                      int64_t group_size, void* stream);
+
+/* Number of stats floats pmi_matmul_w4a16_residual writes for this shape, 0
+ * when it does not run it. Host-only. */
+PMI_API int pmi_residual_stats_count(int64_t N, int64_t K, int glu);
+
+/* y = (RMSNorm(x) * norm_weight) . dequant(W)^T for one activation row x
+ * fp16 [1, K] that a pmi_matmul_w4a16_residual launch formed, with its n_stats
+ * partial sums of x^2 (1 <= n_stats <= 512): every wave adds them in one fixed
+ * order, so the launch needs no whole-row reduction or barrier before its
+ * first weight batch. The activations are formed as pmi_add_rmsnorm_f16 forms
+ * them; the mean's sum runs in another order, so an activation can differ by
+ * one fp16 ulp. norm_weight fp16 [K]; zeros u8 [N, G]; kernel layout; no
+ * act_order. No reference counterpart (pare/eval/throughput.py:84-126). */
+PMI_API int pmi_matmul_w4a16_prenormed(const void* x, const float* stats, int n_stats,
+                                       const void* norm_weight, float eps, const uint8_t* w,
+                                       const float* scales, const uint8_t* zeros_u8, void* y,
+                                       int64_t N, int64_t K, int64_t group_size, void* stream);
 
 /* The same residual add and pre-norm on the tiled GEMM, for up to 4 rows:
  * y = (RMSNorm(x + residual) * norm_weight) . dequant(W)^T, or with glu != 0

@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -69,6 +69,10 @@ SIGNATURES = {
     "pmi_matmul_w4a16_tiled_rmsnorm": (_i, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp,
                                             _i64, _i64, _i64, _i64, _i, _vp]),
     "pmi_tiled_rmsnorm_supported": (_i, [_i64, _i64, _i64, _i64, _i]),
+    "pmi_matmul_w4a16_residual": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "pmi_residual_stats_count": (_i, [_i64, _i64, _i]),
+    "pmi_matmul_w4a16_prenormed": (_i, [_vp, _vp, _i, _vp, ctypes.c_float, _vp, _vp, _vp, _vp,
+                                        _i64, _i64, _i64, _vp]),
     "pmi_set_kernel_override": (_i, [_i]),
     "pmi_add_rmsnorm_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "pmi_rope_kv_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

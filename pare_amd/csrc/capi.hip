@@ -319,6 +319,67 @@ int pmi_matmul_w4a16_tiled_rmsnorm(const void* x, const void* residual, const vo
                   fn);
 }
 
+int pmi_residual_stats_count(int64_t N, int64_t K, int glu) {
+  if (N <= 0 || K <= 0 || K % 32 != 0) return 0;
+  const pmi::GemvConfig c = pmi::gemv_config(1, N, K, glu ? 2 : 0);
+  if (c.slice_waves < 2 || c.grid > pmi::kGemvMaxStats) return 0;
+  return c.grid;
+}
+
+int pmi_matmul_w4a16_residual(const void* x, int glu, const void* residual, float* stats,
+                              const uint8_t* w, const float* scales, const uint8_t* zeros_u8,
+                              void* h, int64_t N, int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_matmul_w4a16_residual";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (N == 0) return ok();
+  if (pmi_residual_stats_count(N, K, glu) == 0)
+    return fail(PMI_ERR_UNSUPPORTED, "%s: needs rows of at least two GEMV slices and at most %d "
+                "workgroups (N=%lld K=%lld; see pmi_residual_stats_count)", fn, pmi::kGemvMaxStats,
+                (long long)N, (long long)K);
+  if (!x || !residual || !stats || !w || !scales || !zeros_u8 || !h)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(x, 16) || !aligned(w, 16))
+    return fail(PMI_ERR_INVALID, "%s: x and the packed weight must be 16-byte aligned", fn);
+  if (!aligned(scales, 4) || !aligned(stats, 4) || !aligned(h, 2) || !aligned(residual, 2))
+    return fail(PMI_ERR_INVALID, "%s: scales and stats must be 4-byte aligned, h and residual 2-byte",
+                fn);
+  pmi::GemvXform xf;
+  xf.mode = glu ? 2 : 0;
+  xf.res = residual;
+  xf.stats = stats;
+  return from_hip(pmi::launch_gemv(x, w, scales, zeros_u8, 1, nullptr, h, 1, N, K, group_size,
+                                   (hipStream_t)stream, &xf),
+                  fn);
+}
+
+int pmi_matmul_w4a16_prenormed(const void* x, const float* stats, int n_stats,
+                               const void* norm_weight, float eps, const uint8_t* w,
+                               const float* scales, const uint8_t* zeros_u8, void* y, int64_t N,
+                               int64_t K, int64_t group_size, void* stream) {
+  const char* fn = "pmi_matmul_w4a16_prenormed";
+  if (int rc = check_shape(N, K, group_size, fn)) return rc;
+  if (N == 0) return ok();
+  if (n_stats < 1 || n_stats > pmi::kGemvMaxStats)
+    return fail(PMI_ERR_INVALID, "%s: n_stats must be in [1, %d] (got %d)", fn, pmi::kGemvMaxStats,
+                n_stats);
+  if (!x || !stats || !norm_weight || !w || !scales || !zeros_u8 || !y)
+    return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(x, 16) || !aligned(norm_weight, 16) || !aligned(w, 16))
+    return fail(PMI_ERR_INVALID, "%s: x, norm_weight and the packed weight must be 16-byte aligned",
+                fn);
+  if (!aligned(scales, 4) || !aligned(stats, 4) || !aligned(y, 2))
+    return fail(PMI_ERR_INVALID, "%s: scales and stats must be 4-byte aligned, y 2-byte", fn);
+  pmi::GemvXform xf;
+  xf.mode = 5;
+  xf.w = norm_weight;
+  xf.eps = eps;
+  xf.stats = const_cast<float*>(stats);
+  xf.n_stats = n_stats;
+  return from_hip(pmi::launch_gemv(x, w, scales, zeros_u8, 1, nullptr, y, 1, N, K, group_size,
+                                   (hipStream_t)stream, &xf),
+                  fn);
+}
+
 int pmi_matmul_w4a16_rmsnorm(const void* x, const void* residual, const void* norm_weight,
                              float eps, void* h_out, const uint8_t* w, const float* scales,
                              const void* zeros, int zero_dtype, void* y, int64_t M, int64_t N,

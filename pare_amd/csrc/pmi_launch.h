@@ -101,6 +101,8 @@ size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool ha
 //   mode 2: x is the fused gate/up output [M, 2K], consumed as silu(gate) * up;
 //   mode 3: x is the residual stream [M, K], consumed as RMSNorm(x + r) * w
 //           (r nullable; h = x + r written to h_out when r is given);
+//   mode 5: x is a residual stream, consumed as RMSNorm(x) * w, with sum(x^2)
+//           from per-workgroup partials a launch with `res` left;
 //   mode 4: act_order, x[:, perm] gathered from a copy of x staged in LDS by
 //           each workgroup (needs gemv_perm_lds_fits), instead of every lane
 //           gathering from global memory.
@@ -116,7 +118,14 @@ struct GemvXform {
   const void* w = nullptr;
   float eps = 0.f;
   void* h_out = nullptr;
+  // mode 5: the partial sums of h^2 (n_stats of them, at most kGemvMaxStats)
+  // left by the launch that formed x; with res (one row, at least two slice
+  // waves): y = y + res, and that launch's partials are written to stats
+  const void* res = nullptr;
+  float* stats = nullptr;
+  int n_stats = 0;
 };
+constexpr int kGemvMaxStats = 512;
 hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, const void* zeros,
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream,

@@ -120,6 +120,24 @@ PMI_DEV float dpp_add(float keep, float send) {
   return keep + __builtin_bit_cast(float, moved);
 }
 
+// The sum of v over the 64 lanes, the same value in every lane: within each
+// row of 16 lanes by DPP (pairs, quads, halves, rows: quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror), then the four rows read
+// out in order. A fixed order, so every wave of every workgroup forms the
+// same float; no LDS round trip (a ds_bpermute butterfly took six).
+PMI_DEV float wave_total(float v) {
+  v = dpp_add<0xB1>(v, v);
+  v = dpp_add<0x4E>(v, v);
+  v = dpp_add<0x141>(v, v);
+  v = dpp_add<0x140>(v, v);
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // One transpose step with partner lane^o for o = 32 or 16. After
 // v_permlane{32,16}_swap_b32 a, b the pair (a, b) holds, per lane, the own
 // and the partner value of one index, so a + b is the pair sum of index i on
@@ -336,7 +354,14 @@ PMI_DEV float sq_pairs(const uint32_t (&v)[8], float acc) {
 // per workgroup (16-byte loads) and gathered from there;
 // 2 the fused gate/up output [M, 2K], consumed as silu(gate) * up;
 // 3 RMSNorm(x + r) * w of the residual stream (xf.r nullable), with
-// h = x + r written to xf.h_out by workgroup 0.
+// h = x + r written to xf.h_out by workgroup 0; 5 RMSNorm(x) * w of a
+// residual stream x whose sum of squares the launch that formed it left as
+// per-workgroup partials (xf.stats, xf.n_stats of them): every wave adds them
+// in the same fixed order, so no workgroup reduces the row or waits at a
+// barrier first.
+// Epilogue (xf.res, one activation row, slice_waves > 1): y = h = y + res
+// rounded as add_rmsnorm_kernel forms h, and xf.stats[blockIdx.x] = the sum of
+// h^2 over the workgroup's rows (fixed order), for a mode-5 launch to read.
 template <int MT, int U, int D, int SPW, int XM, bool ZU8>
 __global__ void __launch_bounds__(kMaxWaves * 64)
 w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
@@ -345,6 +370,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   int n_slices, int slice_waves, int row_waves, int rows_per_wg, GemvXform xf) {
   extern __shared__ float part[];  // [rows_per_wg][slice_waves][MT] when slice_waves > 1
   __shared__ float nrm[XM == 3 ? kMaxWaves * 4 : 1];  // per-wave sums of h^2 (XM 3)
+  __shared__ float hred[kMaxWaves];                    // per-wave sums of h^2 (epilogue)
   constexpr int VP = Pow2Ceil<U * MT>::value;
   constexpr int LOGV = Log2<VP>::value;
 
@@ -372,9 +398,10 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   int boff[SPW], grp[SPW];
   bool act[SPW];
   uint32_t xa[SPW][MT][8], xb[SPW][MT][8];
-  constexpr int kXS = XM >= 2 ? SPW : 1, kXM = XM >= 2 ? MT : 1, kNS = XM == 3 ? SPW : 1;
+  constexpr int kXS = XM == 2 || XM == 3 ? SPW : 1, kXM = XM == 2 || XM == 3 ? MT : 1;
+  constexpr int kNS = XM == 3 || XM == 5 ? SPW : 1;
   uint32_t ua[kXS][kXM][8], ub[kXS][kXM][8];  // up (XM 2) or residual (XM 3)
-  uint32_t wa[kNS][8], wb[kNS][8];            // norm weight (XM 3)
+  uint32_t wa[kNS][8], wb[kNS][8];            // norm weight (XM 3, 5)
   constexpr int kPS = XM == 4 ? SPW : 1;
   int pl[kPS][16], ph[kPS][16];                // permuted columns (XM 4)
   int klo[SPW];
@@ -390,7 +417,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     grp[sp] = t;
     const int k_lo = t * gs + j;
     klo[sp] = k_lo;
-    if constexpr (XM == 3)
+    if constexpr (XM == 3 || XM == 5)
       load_x_raw<false>(reinterpret_cast<const f16*>(xf.w), perm, k_lo, k_lo + hgs, K, wa[sp],
                         wb[sp]);
 #pragma unroll
@@ -426,6 +453,29 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
       const int c = (int)threadIdx.x + i * (int)blockDim.x;
       xst[i] = c < n_xch ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
     }
+  }
+  // XM 5: the producing launch's partials of sum(h^2), lane l holding
+  // l, l + 64, ... (the host checks 1 <= n_stats <= 64 kSt). The loads are
+  // unconditional (clamped index) and the entries past n_stats are dropped
+  // only in setup_x, below the ring's first weight loads: selected here, the
+  // values made the compiler wait for these loads before issuing the ring.
+  constexpr int kSt = XM == 5 ? 8 : 1;
+  float st[kSt];
+  if constexpr (XM == 5) {
+#pragma unroll
+    for (int i = 0; i < kSt; ++i) {
+      const int q = lane + 64 * i;
+      st[i] = xf.stats[q < xf.n_stats ? q : xf.n_stats - 1];
+    }
+  }
+  // epilogue residual: each thread's first output row, fetched now (clamped
+  // to the workgroup's last row; used only for threads that own a row)
+  const bool res_on = xf.res != nullptr;
+  f16 rpre = (f16)0.f;
+  if (res_on) {
+    const int e = min((int)threadIdx.x, (row_lim - row0) * MT - 1);
+    const int lr = e / MT, m = e - lr * MT;
+    rpre = reinterpret_cast<const f16*>(xf.res)[(int64_t)m * N + row0 + lr];
   }
 
   const int my_row0 = row0 + wr * U;
@@ -515,6 +565,23 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         }
       }
     }
+    if constexpr (XM == 5) {
+      // the whole row's sum of squares from the partials, the same fixed
+      // order in every wave; then RMSNorm(x) * w rounded as add_rmsnorm_kernel
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < kSt; ++i) acc += lane + 64 * i < xf.n_stats ? st[i] : 0.f;
+      const float inv = rsqrtf(wave_total(acc) / (float)K + xf.eps);
+#pragma unroll
+      for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xa[sp][m][i] = norm_pair(xa[sp][m][i], wa[sp][i], inv);
+            xb[sp][m][i] = norm_pair(xb[sp][m][i], wb[sp][i], inv);
+          }
+    }
 #pragma unroll
     for (int sp = 0; sp < SPW; ++sp)
 #pragma unroll
@@ -595,11 +662,38 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   if (slice_waves == 1) return;
   __syncthreads();
   const int nr = row_lim - row0;
+  float hsq = 0.f;
   for (int e = threadIdx.x; e < nr * MT; e += blockDim.x) {
     const int lr = e / MT, m = e - (e / MT) * MT;
     float s = 0.f;
     for (int q = 0; q < slice_waves; ++q) s += part[(lr * slice_waves + q) * MT + m];
-    y[(int64_t)m * N + row0 + lr] = f32_to_f16_rne(s);
+    f16 yv = f32_to_f16_rne(s);
+    if (res_on) {
+      const f16 rv = e == (int)threadIdx.x ? rpre
+                                           : reinterpret_cast<const f16*>(xf.res)[(int64_t)m * N + row0 + lr];
+      yv = (f16)((float)yv + (float)rv);
+      hsq = fmaf((float)yv, (float)yv, hsq);
+    }
+    y[(int64_t)m * N + row0 + lr] = yv;
+  }
+  if (res_on) {
+    // the workgroup's sum of h^2: per wave, then the waves in order; when its
+    // rows fit wave 0 (one row per lane above), wave 0 alone, no barrier
+    if (nr * MT <= 64) {
+      if (wave == 0) {
+        const float t = wave_total(hsq);
+        if (lane == 0) xf.stats[blockIdx.x] = t;
+      }
+    } else {
+      hsq = wave_total(hsq);
+      if (lane == 0) hred[wave] = hsq;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float t = 0.f;
+        for (int q = 0; q < (int)(blockDim.x >> 6); ++q) t += hred[q];
+        xf.stats[blockIdx.x] = t;
+      }
+    }
   }
 }
 
@@ -617,11 +711,12 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
   hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
                      (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,       \
                      c.slice_waves, c.row_waves, c.rows_per_wg, xf)
-  if (xf.mode == 2 || xf.mode == 3) {
+  if (xf.mode == 2 || xf.mode == 3 || xf.mode == 5) {
     // the transformed activations are built for u8 zero points and no permutation only
     if (!zero_u8 || perm) return hipErrorInvalidValue;
     if (xf.mode == 2) PMI_GEMV_LAUNCH(2, true);
-    else PMI_GEMV_LAUNCH(3, true);
+    else if (xf.mode == 3) PMI_GEMV_LAUNCH(3, true);
+    else PMI_GEMV_LAUNCH(5, true);
   } else if (perm_lds) {
     if (zero_u8) PMI_GEMV_LAUNCH(4, true);
     else PMI_GEMV_LAUNCH(4, false);
@@ -753,8 +848,13 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   // 9.1 us for pairs at three)
   else if (mt == 1 && rows_per_cu >= 20 && xmode == 3) { c.rows_per_wave = 1; wpc = 2; }
   // act_order staged in LDS (mode 4) reads X and the int32 permutation once per
-  // workgroup: one per CU (6144 x 4096: 6.7 against 9.4 us at three)
-  else if (mt == 1 && rows_per_cu >= 20) { c.rows_per_wave = 2; wpc = xmode == 4 ? 1 : 3; }
+  // workgroup: one per CU (6144 x 4096: 6.7 against 9.4 us at three); so does
+  // the norm from partials (mode 5), whose prologue then overlaps a three-deep
+  // ring instead of a wave's only batch (6.2 against 7.3 us)
+  else if (mt == 1 && rows_per_cu >= 20) {
+    c.rows_per_wave = 2;
+    wpc = xmode == 4 || xmode == 5 ? 1 : 3;
+  }
   else if (mt > 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 2; }
   else one_batch = true;
   if (one_batch || c.rows_per_wave > max_u) {

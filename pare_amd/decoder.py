@@ -37,8 +37,9 @@ import torch.nn.functional as F
 from . import _lib
 from .config import QuantConfig
 from .kernels import (_stream_handle, gate_up_silu_supported, glu_row_order, kernel_choice,
-                      matmul_w4a16_gate_up_silu, matmul_w4a16_glu, matmul_w4a16_rmsnorm,
-                      matmul_w4a16_tiled_rmsnorm, tiled_rmsnorm_supported)
+                      matmul_w4a16_gate_up_silu, matmul_w4a16_glu, matmul_w4a16_prenormed,
+                      matmul_w4a16_residual, matmul_w4a16_rmsnorm, matmul_w4a16_tiled_rmsnorm,
+                      residual_stats_count, tiled_rmsnorm_supported)
 from .pack import sz_group_major, tile_w4a16
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .quant import rtn_quantize
@@ -177,6 +178,32 @@ def decode_attention_rope(qkv, cos, sin, pos, cache_k, cache_v, scale: float):
 
 
 _ARGMAX_WORKSPACES: dict = {}
+_STATS_BUFFERS: dict = {}
+
+
+def _stats_buffer(dev: torch.device) -> torch.Tensor:
+    """The fp32 partials of sum(h^2) that a residual-forming GEMV leaves for
+    the next pre-normed one, one buffer per (device, stream): launches on a
+    stream are ordered, and every consumer runs before the next producer.
+    Allocated by the first (eager) call, so graph captures reuse it."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           _stream_handle(dev))
+    buf = _STATS_BUFFERS.get(key)
+    if buf is None:
+        buf = torch.zeros(512, dtype=torch.float32, device=dev)
+        _STATS_BUFFERS[key] = buf
+    return buf
+
+
+class _Summed:
+    """The pending residual of a one-token layer that already added it: the
+    residual stream h is complete, and ``stats[:n]`` are the partial sums of
+    h^2 its last GEMV left for the next layer's pre-normed q/k/v."""
+    __slots__ = ("stats", "n")
+
+    def __init__(self, stats: torch.Tensor, n: int):
+        self.stats, self.n = stats, n
+
 
 
 def argmax_into(x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
@@ -256,6 +283,10 @@ class DecoderLayer(nn.Module):
         device). Returns the new (h, d)."""
         cfg = self.cfg
         B, T, _ = h.shape
+        if not causal and T == 1 and B == 1 and self._summed_ok():
+            return self._forward_summed(h, d, cos_t, sin_t, cache_k, cache_v, pos)
+        if isinstance(d, _Summed):
+            d = None
         if not causal and T == 1:
             # one new token: each residual add + RMSNorm runs inside the GEMV that
             # consumes it where that is the GEMV, and RoPE, the cache write and
@@ -283,6 +314,62 @@ class DecoderLayer(nn.Module):
             a = a.reshape(B, 1, cfg.hidden)
         n2, h = add_rmsnorm(h, self.o(a), self.mlp_norm.weight, cfg.rms_eps)
         return h, self._mlp(n2, B, T)
+
+    def _summed_ok(self) -> bool:
+        """One-token layers can carry the residual stream as (h, partials): every
+        linear on the GEMV with u8 zero points, no act_order, no bias on o and
+        down, and the residual-forming launches supported."""
+        lins = (self.qkv.fused, self.o, self.gate_up.fused, self.down)
+        if not (all(getattr(l, "use_kernel", False) and l.g_idx is None for l in lins)
+                and self.o.bias is None and self.down.bias is None):
+            return False
+        shapes_ok = getattr(self, "_summed_shapes", None)  # shape-only, so kept
+        if shapes_ok is None:
+            cfg = self.cfg
+            shapes_ok = (
+                all(kernel_choice(1, l.out_features, l.in_features, l._group_size()) == "gemv"
+                    for l in lins)
+                and 0 < residual_stats_count(cfg.hidden, self.o.in_features) <= 512
+                and 0 < residual_stats_count(cfg.hidden, self.down.in_features, glu=True) <= 512)
+            self._summed_shapes = shapes_ok
+        return shapes_ok
+
+    def _forward_summed(self, h, d, cos_t, sin_t, cache_k, cache_v, pos):
+        """A one-token layer whose residual adds run in the epilogues of the o
+        and down GEMVs, each leaving per-workgroup partials of sum(h^2) for the
+        next GEMV's RMSNorm (q/k/v of the next layer, gate/up of this one): no
+        launch reduces a whole row before its first weight batch. Returns (h,
+        _Summed)."""
+        cfg = self.cfg
+        K = cfg.hidden
+        stats = _stats_buffer(h.device)
+        qf = self.qkv.fused
+        if isinstance(d, _Summed):
+            w_k, z_u8, _, _ = qf._kernel_buffers()
+            qkv = matmul_w4a16_prenormed(h.reshape(1, K), d.stats, d.n, self.attn_norm.weight,
+                                         cfg.rms_eps, w_k, qf.scale, z_u8, qf._group_size())
+            if qf.bias is not None:
+                qkv = qkv + qf.bias
+        else:
+            qkv, h = self._norm_linear(qf, h, d, self.attn_norm.weight)
+            qkv = qkv.reshape(1, -1)
+        a = decode_attention_rope(qkv, cos_t, sin_t, pos, cache_k, cache_v,
+                                  1.0 / math.sqrt(cfg.head_dim))
+        w_o, z_o, _, _ = self.o._kernel_buffers()
+        h2 = torch.empty_like(h)
+        n = matmul_w4a16_residual(a.reshape(1, -1), h.reshape(1, K), stats, w_o, self.o.scale, z_o,
+                                  self.o._group_size(), out=h2.reshape(1, K))
+        gl = self.gate_up.fused
+        w_g, z_g, _, _ = gl._kernel_buffers()
+        gu = matmul_w4a16_prenormed(h2.reshape(1, K), stats, n, self.mlp_norm.weight, cfg.rms_eps,
+                                    w_g, gl.scale, z_g, gl._group_size())
+        if gl.bias is not None:
+            gu = gu + gl.bias
+        w_d, z_d, _, _ = self.down._kernel_buffers()
+        h3 = torch.empty_like(h)
+        n = matmul_w4a16_residual(gu, h2.reshape(1, K), stats, w_d, self.down.scale, z_d,
+                                  self.down._group_size(), glu=True, out=h3.reshape(1, K))
+        return h3, _Summed(stats, n)
 
     def _norm_linear(self, lin: QuantizedLinear, h, d, norm_w):
         """(lin(RMSNorm(h + d) * norm_w), h + d) for one token per sequence: one
@@ -416,6 +503,8 @@ class QuantizedDecoder(nn.Module):
             d = None
             for layer, (ck, cv) in zip(self.layers, cache):
                 x, d = layer.forward_fused(x, d, cos, sin, ck, cv, pos, causal)
+            if isinstance(d, _Summed):
+                d = None  # x already holds the residual stream
             if last_only:
                 x = x[:, -1:].contiguous()
                 d = d[:, -1:].contiguous() if d is not None else None

@@ -315,6 +315,67 @@ def matmul_w4a16_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, norm_we
     return out, h
 
 
+def residual_stats_count(N: int, K: int, glu: bool = False) -> int:
+    """Partials of sum(h^2) that ``matmul_w4a16_residual`` writes for this
+    shape (0 when it does not run it)."""
+    return int(_lib.lib().pmi_residual_stats_count(N, K, int(glu)))
+
+
+def matmul_w4a16_residual(x: torch.Tensor, residual: torch.Tensor, stats: torch.Tensor,
+                          packed_weight: torch.Tensor, scales: torch.Tensor,
+                          zeros_u8: torch.Tensor, group_size: int, glu: bool = False,
+                          out: torch.Tensor | None = None) -> int:
+    """One activation row: ``out`` = residual + x @ dequant(W)^T (each output
+    rounded to fp16, then added as ``add_rmsnorm`` adds), with x the fused
+    gate/up output consumed as SiLU(gate) * up when ``glu``. Writes the
+    per-workgroup partial sums of out^2 to ``stats`` (fp32) and returns how
+    many, for ``matmul_w4a16_prenormed``. ``out`` may be ``residual``."""
+    L = _lib.lib()
+    N, K_half = packed_weight.shape
+    K = 2 * K_half
+    assert x.dtype == torch.float16 and x.is_contiguous() and x.numel() == (2 * K if glu else K)
+    assert residual.dtype == torch.float16 and residual.is_contiguous() and residual.numel() == N
+    assert stats.dtype == torch.float32 and stats.is_contiguous()
+    n = residual_stats_count(N, K, glu)
+    if n == 0 or stats.numel() < n:
+        raise RuntimeError(f"matmul_w4a16_residual: shape N={N} K={K} glu={glu} not supported "
+                           f"(or stats holds fewer than {n} floats)")
+    out = residual if out is None else out
+    dev = x.device
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16_residual(
+            _aligned16(x).data_ptr(), int(glu), residual.data_ptr(), stats.data_ptr(),
+            _aligned16(packed_weight.contiguous()).data_ptr(), _to_2d(scales).float().contiguous().data_ptr(),
+            _to_2d(zeros_u8).contiguous().data_ptr(), out.data_ptr(), N, K, group_size,
+            _stream_handle(dev)), "pmi_matmul_w4a16_residual")
+    return n
+
+
+def matmul_w4a16_prenormed(x: torch.Tensor, stats: torch.Tensor, n_stats: int,
+                           norm_weight: torch.Tensor, eps: float, packed_weight: torch.Tensor,
+                           scales: torch.Tensor, zeros_u8: torch.Tensor,
+                           group_size: int) -> torch.Tensor:
+    """(RMSNorm(x) * norm_weight) @ dequant(W)^T for one row x [1, K] formed
+    by ``matmul_w4a16_residual``, whose ``n_stats`` partial sums of x^2 give
+    the norm; returns fp16 [1, N]."""
+    L = _lib.lib()
+    N, K_half = packed_weight.shape
+    K = 2 * K_half
+    assert x.dtype == torch.float16 and x.is_contiguous() and x.numel() == K
+    assert norm_weight.dtype == torch.float16 and norm_weight.numel() == K
+    assert stats.dtype == torch.float32 and stats.numel() >= n_stats
+    dev = x.device
+    out = torch.empty(1, N, device=dev, dtype=torch.float16)
+    with _DeviceGuard(dev):
+        _lib.check(L.pmi_matmul_w4a16_prenormed(
+            _aligned16(x).data_ptr(), stats.data_ptr(), n_stats,
+            _aligned16(norm_weight.contiguous()).data_ptr(), eps,
+            _aligned16(packed_weight.contiguous()).data_ptr(), _to_2d(scales).float().contiguous().data_ptr(),
+            _to_2d(zeros_u8).contiguous().data_ptr(), out.data_ptr(), N, K, group_size,
+            _stream_handle(dev)), "pmi_matmul_w4a16_prenormed")
+    return out
+
+
 def tiled_rmsnorm_supported(M: int, N: int, K: int, group_size: int, glu: bool = False) -> bool:
     """True when ``matmul_w4a16_tiled_rmsnorm`` runs this shape (2..4 rows in
     practice, K <= 4096, group_size % 128 == 0)."""

@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == _lib.ABI_VERSION == 14
+    assert L.pmi_abi_version() == _lib.ABI_VERSION == 15
 
 
 def test_kernel_choice(L):

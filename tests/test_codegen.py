@@ -120,7 +120,8 @@ def _gemv_kernels(asm: str) -> dict[tuple, str]:
     """Body of every w4a16_gemv_kernel<MT, U, D, SPW, XM, ZU8> instantiation,
     keyed by (MT, U, D, SPW, XM, ZU8, mangled name). XM: 0 plain activations,
     1 act_order gather from global memory, 2 silu(gate) * up, 3 residual add +
-    RMSNorm, 4 act_order gather from activations staged in LDS."""
+    RMSNorm, 4 act_order gather from activations staged in LDS, 5 RMSNorm with
+    sum(x^2) from a residual launch's partials."""
     out = {}
     pat = r"^(_ZN\S*w4a16_gemv_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d)ELb(\d)E\S*):"
     for m in re.finditer(pat, asm, re.M):

@@ -235,6 +235,120 @@ def test_rmsnorm_gemv_matches_norm_then_matmul(M, N, K, with_residual):
     assert err <= 2e-3 * scale + 1e-3
 
 
+def _gemv_layer(N, K, seed):
+    from pare_amd.pack import repack_int4_for_kernel, zeros_to_u8
+
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    w = torch.randn(N, K, generator=g, device=DEV) * 0.02
+    packed, s, z = P.rtn_quantize(w, 128)
+    return repack_int4_for_kernel(packed, 128), s, zeros_to_u8(z)
+
+
+@pytest.mark.parametrize("N,K,glu", [(4096, 4096, False), (4096, 14336, True), (3584, 18944, True),
+                                     (1000, 4096, False), (4096, 2560, False)])
+def test_residual_gemv_adds_as_add_rmsnorm_does(N, K, glu):
+    """The GEMV that adds the residual in its epilogue: h equals the plain
+    launch's fp16 output added to the residual and rounded as add_rmsnorm
+    adds, bit for bit (also in place), and the partials add up to sum(h^2)."""
+    from pare_amd.kernels import (matmul_w4a16, matmul_w4a16_glu, matmul_w4a16_residual,
+                                  residual_stats_count)
+
+    wk, s, zu = _gemv_layer(N, K, N + K)
+    g = torch.Generator(device=DEV).manual_seed(K)
+    x = (torch.randn(1, 2 * K if glu else K, generator=g, device=DEV) * (2 if glu else 1)).half()
+    r = torch.randn(1, N, generator=g, device=DEV).half()
+    n = residual_stats_count(N, K, glu)
+    assert 0 < n <= 512
+    stats = torch.full((512,), float("nan"), device=DEV)
+    h = torch.empty_like(r)
+    assert matmul_w4a16_residual(x, r, stats, wk, s, zu, 128, glu=glu, out=h) == n
+    y = matmul_w4a16_glu(x, wk, s, zu, 128) if glu else matmul_w4a16(x, wk, s, zu, 128)
+    ref = (y.float() + r.float()).half()
+    assert torch.equal(h, ref), (h.float() - ref.float()).abs().max().item()
+    tot = stats[:n].double().sum().item()
+    assert abs(tot - (ref.double() ** 2).sum().item()) <= 1e-5 * tot
+    r2 = r.clone()
+    matmul_w4a16_residual(x, r2, stats, wk, s, zu, 128, glu=glu)  # in place
+    assert torch.equal(r2, ref)
+
+
+@pytest.mark.parametrize("N,K", [(6144, 4096), (28672, 4096), (1024, 4096), (37888, 3584)])
+def test_prenormed_gemv_matches_norm_then_matmul(N, K):
+    """The GEMV whose RMSNorm takes sum(h^2) from a residual launch's partials,
+    against add_rmsnorm followed by the plain matmul: within the fp16 ulp the
+    differently ordered mean can move an activation by."""
+    from pare_amd.kernels import (matmul_w4a16, matmul_w4a16_prenormed, matmul_w4a16_residual)
+
+    wk_o, s_o, z_o = _gemv_layer(K, K, K)   # forms h, [1, K]
+    wk, s, zu = _gemv_layer(N, K, N + K)
+    g = torch.Generator(device=DEV).manual_seed(N)
+    a = torch.randn(1, K, generator=g, device=DEV).half()
+    r = torch.randn(1, K, generator=g, device=DEV).half()
+    nw = (1 + 0.1 * torch.randn(K, generator=g, device=DEV)).half()
+    stats = torch.zeros(512, device=DEV)
+    h = torch.empty_like(r)
+    n = matmul_w4a16_residual(a, r, stats, wk_o, s_o, z_o, 128, out=h)
+    y = matmul_w4a16_prenormed(h, stats, n, nw, 1e-5, wk, s, zu, 128)
+    n_ref, _ = add_rmsnorm(h, None, nw, 1e-5)
+    y_ref = matmul_w4a16(n_ref, wk, s, zu, 128)
+    err = (y.float() - y_ref.float()).abs().max().item()
+    scale = y_ref.float().abs().max().item()
+    print(f"[prenormed-gemv] N={N} K={K}: max_abs={err:.3e} (max {scale:.2f})", flush=True)
+    assert err <= 2e-3 * scale + 1e-3
+
+
+def test_residual_and_prenormed_reject_what_they_do_not_run():
+    L = _lib.lib()
+    assert L.pmi_residual_stats_count(4096, 4096, 0) == 256
+    assert L.pmi_residual_stats_count(1024, 1024, 0) == 0    # one GEMV slice per row
+    assert L.pmi_matmul_w4a16_residual(None, 0, None, None, None, None, None, None, 1024, 1024,
+                                       128, None) == _lib.PMI_ERR_UNSUPPORTED
+    assert L.pmi_matmul_w4a16_prenormed(None, None, 0, None, 1e-5, None, None, None, None, 4096,
+                                        4096, 128, None) == _lib.PMI_ERR_INVALID
+    assert L.pmi_matmul_w4a16_prenormed(None, None, 513, None, 1e-5, None, None, None, None, 4096,
+                                        4096, 128, None) == _lib.PMI_ERR_INVALID
+
+
+def test_decoder_one_token_summed_path_matches_the_norm_launch_path():
+    """A full-width two-layer decoder at batch 1: the one-token layers that add
+    the residual in the o / down epilogues and take the norm from their partials
+    against the same model with that path off (norm inside each consuming GEMV),
+    over a prefill and greedy decode: equal tokens, logits within tolerance,
+    and graph replay equal to eager."""
+    from pare_amd.decoder import DecoderLayer
+
+    cfg = DecoderConfig(layers=2, vocab=4000)
+    model = QuantizedDecoder(cfg, DEV, seed=11)
+    assert all(layer._summed_ok() for layer in model.layers)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    prompt = torch.randint(0, cfg.vocab, (1, 24), generator=g, device=DEV)
+    on_eager, _ = model.generate(prompt, 10, use_graph=False)
+    on_graph, _ = model.generate(prompt, 10, use_graph=True)
+    orig = DecoderLayer._summed_ok
+    DecoderLayer._summed_ok = lambda self: False
+    try:
+        off_eager, _ = model.generate(prompt, 10, use_graph=False)
+        cos, sin = model.rope_tables(32)
+        pos = torch.tensor([24], device=DEV)
+        tok = on_eager[:, :1]
+        with torch.no_grad():
+            cache = model.new_cache(1, 32)
+            model.forward_tokens(prompt, cos, sin, cache, torch.arange(24, device=DEV), None, True)
+            off = model.forward_tokens(tok, cos, sin, cache, pos, None, False).float()
+    finally:
+        DecoderLayer._summed_ok = orig
+    with torch.no_grad():
+        cache = model.new_cache(1, 32)
+        model.forward_tokens(prompt, cos, sin, cache, torch.arange(24, device=DEV), None, True)
+        on = model.forward_tokens(tok, cos, sin, cache, pos, None, False).float()
+    err = (on - off).abs().max().item()
+    print(f"[decoder] summed path: tokens {on_eager[0].tolist()} vs {off_eager[0].tolist()}, "
+          f"logit max_abs {err:.3e}", flush=True)
+    assert torch.equal(on_eager, on_graph)
+    assert torch.equal(on_eager, off_eager)
+    assert err <= 1e-2 + 1e-2 * off.abs().max().item()
+
+
 @pytest.mark.parametrize("M,N,F", [(1, 4096, 14336), (2, 4096, 14336), (3, 1024, 4096),
                                    (4, 4096, 14336), (1, 136, 512), (4, 200, 1024)])
 def test_glu_down_matches_silu_then_matmul(M, N, F):
