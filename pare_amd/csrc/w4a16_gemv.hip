@@ -362,7 +362,7 @@ PMI_DEV float sq_pairs(const uint32_t (&v)[8], float acc) {
 // Epilogue (xf.res, one activation row, slice_waves > 1): y = h = y + res
 // rounded as add_rmsnorm_kernel forms h, and xf.stats[blockIdx.x] = the sum of
 // h^2 over the workgroup's rows (fixed order), for a mode-5 launch to read.
-template <int MT, int U, int D, int SPW, int XM, bool ZU8>
+template <int MT, int U, int D, int SPW, int XM, bool ZU8, bool RES = false>
 __global__ void __launch_bounds__(kMaxWaves * 64)
 w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   const float* __restrict__ scales, const void* __restrict__ zeros,
@@ -370,7 +370,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   int n_slices, int slice_waves, int row_waves, int rows_per_wg, GemvXform xf) {
   extern __shared__ float part[];  // [rows_per_wg][slice_waves][MT] when slice_waves > 1
   __shared__ float nrm[XM == 3 ? kMaxWaves * 4 : 1];  // per-wave sums of h^2 (XM 3)
-  __shared__ float hred[kMaxWaves];                    // per-wave sums of h^2 (epilogue)
+  __shared__ float hred[RES ? kMaxWaves : 1];          // per-wave sums of h^2 (RES)
   constexpr int VP = Pow2Ceil<U * MT>::value;
   constexpr int LOGV = Log2<VP>::value;
 
@@ -468,11 +468,12 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
       st[i] = xf.stats[q < xf.n_stats ? q : xf.n_stats - 1];
     }
   }
-  // epilogue residual: each thread's first output row, fetched now (clamped
-  // to the workgroup's last row; used only for threads that own a row)
-  const bool res_on = xf.res != nullptr;
+  // RES: each thread's first output row of the residual, fetched now
+  // (clamped to the workgroup's last row; used only by threads that own a
+  // row). A template flag, so that no other launch carries this code.
+  static_assert(!RES || MT == 1, "the residual epilogue is built for one activation row");
   f16 rpre = (f16)0.f;
-  if (res_on) {
+  if constexpr (RES) {
     const int e = min((int)threadIdx.x, (row_lim - row0) * MT - 1);
     const int lr = e / MT, m = e - lr * MT;
     rpre = reinterpret_cast<const f16*>(xf.res)[(int64_t)m * N + row0 + lr];
@@ -668,7 +669,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     float s = 0.f;
     for (int q = 0; q < slice_waves; ++q) s += part[(lr * slice_waves + q) * MT + m];
     f16 yv = f32_to_f16_rne(s);
-    if (res_on) {
+    if constexpr (RES) {
       const f16 rv = e == (int)threadIdx.x ? rpre
                                            : reinterpret_cast<const f16*>(xf.res)[(int64_t)m * N + row0 + lr];
       yv = (f16)((float)yv + (float)rv);
@@ -676,7 +677,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     }
     y[(int64_t)m * N + row0 + lr] = yv;
   }
-  if (res_on) {
+  if constexpr (RES) {
     // the workgroup's sum of h^2: per wave, then the waves in order; when its
     // rows fit wave 0 (one row per lane above), wave 0 alone, no barrier
     if (nr * MT <= 64) {
@@ -711,6 +712,25 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
   hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
                      (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,       \
                      c.slice_waves, c.row_waves, c.rows_per_wg, xf)
+  if (xf.res) {
+    // the residual epilogue: one activation row, plain or SiLU(gate) * up
+    // activations, u8 zero points, no permutation
+    if constexpr (MT == 1) {
+      if (!zero_u8 || perm || (xf.mode != 0 && xf.mode != 2) || c.slice_waves < 2)
+        return hipErrorInvalidValue;
+      if (xf.mode == 2)
+        hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, 2, true, true>), dim3(c.grid), block,
+                           lds, stream, (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs,
+                           c.n_slices, c.slice_waves, c.row_waves, c.rows_per_wg, xf);
+      else
+        hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, 0, true, true>), dim3(c.grid), block,
+                           lds, stream, (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs,
+                           c.n_slices, c.slice_waves, c.row_waves, c.rows_per_wg, xf);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   if (xf.mode == 2 || xf.mode == 3 || xf.mode == 5) {
     // the transformed activations are built for u8 zero points and no permutation only
     if (!zero_u8 || perm) return hipErrorInvalidValue;
