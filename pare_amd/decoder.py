@@ -279,6 +279,9 @@ class DecoderLayer(nn.Module):
         """The same layer on the library's fused ops. The residual stream is
         carried as (h, d) with d the previous layer's pending output (None for
         the first layer): each residual add happens inside the next RMSNorm.
+        One-token layers at batch 1 return d as a ``_Summed`` instead: h then
+        already holds the residual, and d the partial sums of h^2 that the
+        next layer's q/k/v GEMV takes its RMSNorm from.
         cos_t/sin_t are the full [L, head_dim/2] tables (indexed by pos on the
         device). Returns the new (h, d)."""
         cfg = self.cfg
