@@ -54,11 +54,8 @@ namespace {
 
 constexpr int kWaves = 4;               // compute waves per workgroup
 constexpr int kProducers = 4;           // copy-issuing waves per workgroup
-constexpr int kNT = 4;                  // 16-row weight tiles per compute wave
 constexpr int kBN = 128;                // weight rows per workgroup
 constexpr int kThreads = (kWaves + kProducers) * 64;
-constexpr int kSBytes = kBN * 4;        // scales of one unit
-constexpr int kZBytes = kBN * 4;        // zero-point words of one unit
 
 // LDS rings (units are consumed in pairs, one unit per k parity):
 //   weights of a pair - 128 rows x 128 bytes, each row's 8 chunks of 16 bytes
@@ -70,8 +67,6 @@ constexpr int kZBytes = kBN * 4;        // zero-point words of one unit
 // contiguous bytes of every packed row: each weight copy fetches whole cache
 // lines (8 rows x 128 bytes), which the DRAM serves far better than the 64-byte
 // halves one unit would give.
-constexpr int kWLines = kBN * 128;                              // weight bytes of a pair
-constexpr int kWPair = kWLines + 2 * (kSBytes + kZBytes);       // weight slot of a pair
 template <int MT, int NT>
 struct Tiling {
   static constexpr int R = 16 * MT;                             // activation rows
