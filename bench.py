@@ -97,6 +97,16 @@ class Buf:
         return self._gm
 
 
+def kernel_of(buf, M):
+    """The kernel pmi_matmul_w4a16 runs when launch() passes `buf`'s buffers at
+    M rows: the tiled GEMM is a candidate only where the tiled copy was built,
+    and the act_order rules apply where the buffer carries a permutation."""
+    import pare_amd as P
+
+    return P.kernel_choice(M, buf.N, buf.K, GS, tiled=buf._tiled is not None,
+                           perm=buf.perm is not None)
+
+
 def make_decoder_layer(seed, dev):
     """One decoder layer's seven linears, RTN-quantised on the device, stored as
     the four fused launches; the seven single-linear buffers are row-block
@@ -409,6 +419,10 @@ def main():
                          "the plain read of the gate/up weights; "
                          "e2e_bs1 / e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens")
     ap.add_argument("--m", type=int, default=64, help="activation rows of --kernel-only gate")
+    ap.add_argument("--graph", action="store_true",
+                    help="--kernel-only gate_up_m1 / gate / gate_m64 / read_floor: capture one pass "
+                         "of the loop in a HIP graph and replay it, the launch mode the JSON "
+                         "line's timings use")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoder leg")
     args = ap.parse_args()
 
@@ -512,7 +526,7 @@ def main():
                 for _ in range(5):
                     gate_loop(stream.cuda_stream, M, 2 * n_layers)
                 torch.cuda.synchronize()
-                log(f"sweep M={M}: 320 launches, kernel {P.kernel_choice(M, 14336, 4096, GS, tiled=True)}")
+                log(f"sweep M={M}: 320 launches, kernel {kernel_of(single[0][4], M)}")
         return
 
     if args.kernel_only == "narrow":
@@ -540,20 +554,33 @@ def main():
         assert 1 <= m_rows <= M_MAX, f"--m must be in 1..{M_MAX}"
         sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
         n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
-        with torch.cuda.stream(stream):
-            for _ in range(5):
-                if args.kernel_only == "gate_up_m1":
-                    gate_up_loop(stream.cuda_stream, 1)
-                elif args.kernel_only == "read_floor":
-                    for f in fused:
-                        assert L.pmi_read_probe(f[2].w.data_ptr(), f[2].w.numel(), 4 * n_cu,
-                                                sink.data_ptr(), stream.cuda_stream) == 0
-                else:
-                    gate_loop(stream.cuda_stream, m_rows, 2 * n_layers)
-        torch.cuda.synchronize()
+
+        def one_pass(s):
+            if args.kernel_only == "gate_up_m1":
+                gate_up_loop(s, 1)
+            elif args.kernel_only == "read_floor":
+                for f in fused:
+                    assert L.pmi_read_probe(f[2].w.data_ptr(), f[2].w.numel(), 4 * n_cu,
+                                            sink.data_ptr(), s) == 0
+            else:
+                gate_loop(s, m_rows, 2 * n_layers)
+
+        if args.graph:
+            # the launch mode of the timed legs: one pass captured in a graph,
+            # replayed five times
+            gk = capture(one_pass, stream)
+            with torch.cuda.stream(stream):
+                for _ in range(5):
+                    gk.replay()
+            torch.cuda.synchronize()
+        else:
+            with torch.cuda.stream(stream):
+                for _ in range(5):
+                    one_pass(stream.cuda_stream)
+            torch.cuda.synchronize()
         what = ("read probe" if args.kernel_only == "read_floor" else
-                f"kernel {P.kernel_choice(m_rows, 14336, 4096, GS, tiled=True)}")
-        log(f"{args.kernel_only} (M={m_rows}): 5 passes, {what}")
+                f"kernel {kernel_of(fused[0][2], 1) if args.kernel_only == 'gate_up_m1' else kernel_of(single[0][4], m_rows)}")
+        log(f"{args.kernel_only} (M={m_rows}): 5 passes{' (graph replays)' if args.graph else ''}, {what}")
         return
 
     # --- eager vs graph: same outputs -------------------------------------
@@ -601,7 +628,7 @@ def main():
         gbs = layer_bytes(N, K, 1) / (us * 1e-6) / 1e9
         detail[name] = {"N": N, "K": K, "us": round(us, 2), "GB/s": round(gbs, 1),
                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
-                        "kernel": P.kernel_choice(1, N, K, GS)}
+                        "kernel": kernel_of(pick(0), 1)}
         log(f"  {name:8s} {N:6d}x{K:6d} M=1: {us:7.2f} us {gbs:8.1f} GB/s")
 
     for i, (name, N, K) in enumerate(LLAMA):
@@ -617,7 +644,7 @@ def main():
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     detail["gate_up"] = {"N": 28672, "K": 4096, "us": round(gu_us, 2), "GB/s": round(gu_gbs, 1),
                          "hbm_frac": round(gu_gbs / HBM_PEAK_GBS, 3),
-                         "kernel": P.kernel_choice(1, 28672, 4096, GS)}
+                         "kernel": kernel_of(fused[0][2], 1)}
     log(f"  gate_up  28672x  4096 M=1: {gu_us:7.2f} us {gu_gbs:8.1f} GB/s")
     del gg
 
@@ -631,7 +658,7 @@ def main():
     m64_gbs = layer_bytes(14336, 4096, 64) / (m64_us * 1e-6) / 1e9
     detail["gate_m64"] = {"us": round(m64_us, 2), "TFLOP/s": round(m64_tflops, 1),
                           "mfma_frac": round(m64_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                          "GB/s": round(m64_gbs, 1), "kernel": P.kernel_choice(64, 14336, 4096, GS, tiled=True)}
+                          "GB/s": round(m64_gbs, 1), "kernel": kernel_of(single[0][4], 64)}
     log(f"  gate M=64: {m64_us:.2f} us {m64_tflops:.1f} TFLOP/s {m64_gbs:.1f} GB/s")
     del gm
 
@@ -645,7 +672,7 @@ def main():
         tfl = 2 * M * 14336 * 4096 / (us * 1e-6) / 1e12
         sweep[M] = {"us": round(us, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
                     "TFLOP/s": round(tfl, 2), "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4),
-                    "kernel": P.kernel_choice(M, 14336, 4096, GS, tiled=True)}
+                    "kernel": kernel_of(single[0][4], M)}
         log(f"  sweep gate M={M:3d}: {sweep[M]}")
         del gs_
     detail["gate_sweep"] = sweep
@@ -675,7 +702,7 @@ def main():
             byt = layer_bytes(N, K, M) + 4 * K
             row[f"M{M}"] = {"us": round(us, 2), "GB/s": round(byt / (us * 1e-6) / 1e9, 1),
                             "TFLOP/s": round(2 * M * N * K / (us * 1e-6) / 1e12, 2),
-                            "kernel": P.kernel_choice(M, N, K, GS, tiled=True)}
+                            "kernel": kernel_of(bufs[0], M)}
             log(f"  qwen act_order {name:8s} {N:6d}x{K:6d} M={M:2d}: {row[f'M{M}']}")
             del gq
         qwen[name] = row

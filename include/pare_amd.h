@@ -155,7 +155,10 @@ PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N,
  * w_tiled (nullable): the pmi_tile_w4a16 copy of w. With it (and scales_gm,
  * zeros_gm) 2..64 activation rows (more on narrow layers) run on the
  * tiled-weight GEMM where that wins (pmi_matmul_kernel_choice 5); without it
- * those rows take the other kernels.
+ * those rows take the other kernels. The tiled GEMM stores up to 8 bytes per
+ * lane: with y not 8-byte aligned (a view at an odd offset) the call runs on
+ * the kernel it would pick without w_tiled (an error if the tiled GEMM is
+ * forced); y needs only 2-byte alignment otherwise.
  * workspace (nullable when workspace_bytes == 0): device scratch of
  * pmi_matmul_workspace_bytes() bytes, 256-byte aligned, zero-filled before
  * its first use; every call leaves it zero-filled again (it holds split-K

@@ -542,6 +542,11 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   const bool has_tiled = w_tiled && scales_gm && zeros_gm && N % 4 == 0;
   int choice = pmi_matmul_kernel_choice(
       M, N, K, group_size, (has_tiled ? PMI_CHOICE_TILED : 0) | (perm ? PMI_CHOICE_PERM : 0));
+  // the tiled GEMM's epilogue stores up to four fp16 outputs (8 bytes) per lane
+  if (choice == 5 && !aligned(y, 8)) {
+    if (forced) return fail(PMI_ERR_INVALID, "%s: the tiled GEMM needs y 8-byte aligned", fn);
+    choice = pmi_matmul_kernel_choice(M, N, K, group_size, perm ? PMI_CHOICE_PERM : 0);
+  }
   if (choice == 5) {
     if (!has_tiled || !pmi::tgemm_supported(M, N, K, group_size))
       return fail(PMI_ERR_UNSUPPORTED, "%s: the tiled GEMM needs w_tiled, scales_gm and zeros_gm, "

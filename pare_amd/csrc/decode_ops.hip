@@ -528,7 +528,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(const f16* __restrict__ x, 
     const int off = (r * chunks + c) * 8;
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), rp, off, 0, kSc1);
     __builtin_amdgcn_raw_buffer_store_b32((uint32_t)bi, rp, off + 4, 0, kSc1);
+    // compiler barriers: the stores stay above the wait and the increment
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
     const int old = __hip_atomic_fetch_add(&counters[r], 1, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
     last_flag = old == chunks - 1;

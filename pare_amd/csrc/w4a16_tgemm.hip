@@ -154,12 +154,19 @@ __device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int s
   for (int j = 0; j < NTW; ++j)
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[j]), rp, 16 * l,
                                            __builtin_amdgcn_readfirstlane((sp * NTW + j) * kTile), kSc1);
+  // The compiler barriers keep the partial stores above the wait and the
+  // counter increment, and the partial loads below the returned count: the
+  // waitcnt intrinsic alone is no memory clobber, and a relaxed RMW orders
+  // no plain accesses at the language level.
+  asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
   int old = 0;
   if (l == 0)
     old = __hip_atomic_fetch_add(&a.counters[wg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __builtin_amdgcn_readfirstlane(old);
   if (old != a.splits - 1) return false;
+  asm volatile("" ::: "memory");
   f32x4 v[kMaxSplits][NTW];
 #pragma unroll
   for (int q = 0; q < kMaxSplits; ++q) {

@@ -441,17 +441,24 @@ class DecoderLayer(nn.Module):
 
     def _glu_buffers(self):
         """Tiled and group-major copies of the fused gate/up weight with its rows
-        in glu_row_order, built on first use (outside graph capture) and kept."""
-        if getattr(self, "_glu", None) is None:
-            gu = self.gate_up.fused
+        in glu_row_order, built on first use and rebuilt when the weights change
+        (keyed on the fused module's weight stamp). They are never built under
+        graph capture: the copies would then only be recorded, not made."""
+        gu = self.gate_up.fused
+        stamp = gu._stamp()
+        cache = getattr(self, "_glu", None)
+        if cache is None or cache[0] != stamp:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("the gate/up SiLU copies are built on the first eager call; "
+                                   "run one eager forward before capturing a graph")
             w_k, z_u8, _, _ = gu._kernel_buffers()
             idx = glu_row_order(gu.out_features // 2, w_k.device)
             gs = gu._group_size()
             s = gu.scale.reshape(gu.out_features, -1)
-            self._glu = (tile_w4a16(w_k[idx].contiguous(), gs),
-                         sz_group_major(s[idx].contiguous(),
-                                        z_u8.reshape(gu.out_features, -1)[idx].contiguous()))
-        return self._glu
+            self._glu = cache = (stamp, tile_w4a16(w_k[idx].contiguous(), gs),
+                                 sz_group_major(s[idx].contiguous(),
+                                                z_u8.reshape(gu.out_features, -1)[idx].contiguous()))
+        return cache[1], cache[2]
 
     def _down(self, gu, B: int, T: int):
         if B * T == 1 and self.down.g_idx is None:

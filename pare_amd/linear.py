@@ -140,12 +140,17 @@ class QuantizedLinear(nn.Module):
     def _tiled_buffer(self, w_kernel: torch.Tensor, M: int, perm: torch.Tensor | None = None):
         """Tiled copy of the kernel-layout weight for the tiled-weight GEMM,
         built on the first forward whose row count runs on it (decode-only use
-        at one row never pays for it) and kept with the kernel-layout weight."""
+        at one row never pays for it) and kept with the kernel-layout weight
+        (dropped with it when the weights change). Under graph capture a copy
+        that does not exist yet is not built (it would only be recorded, and
+        eager calls would read it unfilled): the call runs without it."""
         if getattr(self, "_packed_weight_tiled", None) is None:
             if not tiled_supported(self.out_features, self.in_features, self._group_size()):
                 return None
             if kernel_choice(M, self.out_features, self.in_features, self._group_size(),
                              tiled=True, perm=perm is not None) != "tgemm":
+                return None
+            if torch.cuda.is_current_stream_capturing():
                 return None
             self._packed_weight_tiled = tile_w4a16(w_kernel, self._group_size())
         return self._packed_weight_tiled

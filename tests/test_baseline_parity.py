@@ -5,7 +5,9 @@ The layers are built by bench.py's own builders (device RTN, kernel-layout
 repack, u8 zero points, group-major scale/zero copies, fused q/k/v and gate/up
 buffers, act_order permutations) and launched through bench.py's own
 ``launch`` (the C ABI, with the bench's shared workspace), so what is checked
-here is exactly what is timed. Each layer's buffers are first checked
+here is exactly what is timed: the tiled weight copies bench.py builds are
+built here too, and every case asserts that its buffers dispatch to the kernel
+bench.py labels its row with (``bench.kernel_of``). Each layer's buffers are first checked
 byte-for-byte against the oracle's quantisation of the same seeded weights;
 outputs are then checked against the oracle's fp32-accumulated reference
 (``O.linear_fp32`` on ``O.dequantize_packed`` / ``O.dequantize_gidx``) at
@@ -91,6 +93,7 @@ def _assert_buf_matches(buf, packed, s, z):
 
 
 def _launch(buf, x: torch.Tensor) -> torch.Tensor:
+    """bench.launch on `buf`: the call bench.py times, with its workspace."""
     M = x.shape[0]
     y = torch.empty(M, buf.N, dtype=torch.float16, device=DEV)
     bench.launch(P._lib.lib(), buf, x.to(DEV).contiguous(), y, M,
@@ -101,11 +104,17 @@ def _launch(buf, x: torch.Tensor) -> torch.Tensor:
 
 @pytest.fixture(scope="module")
 def llama_layer():
-    """bench.py's decoder layer 0 (seed 0) with its group-major copies built,
-    and the oracle's buffers and dequantized weights for it."""
+    """bench.py's decoder layer 0 (seed 0) with the copies bench.py's main()
+    builds before it times anything: group-major scale/zero copies on every
+    buffer, tiled weight copies on the single gate_proj and up_proj buffers
+    (the C3 sweep and the M = 64 leg run on those), and the oracle's buffers
+    and dequantized weights for it."""
     fused, single = bench.make_decoder_layer(0, DEV)
     for b in fused + single:
         b.gm()
+    for b in single:
+        if b.name in ("gate", "up"):
+            b.tiled()
     ref = _oracle_decoder_layer(0)
     w_hat = {name: O.dequantize_packed(*ref[name]) for name in ref}
     torch.cuda.synchronize()
@@ -223,13 +232,50 @@ def test_c2_glu_down_m1(llama_layer):
 # C3: gate_proj at every M of the sweep, automatic dispatch
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 64, 128])
+# the kernel bench.py's sweep times at each row count (bench.kernel_of on the
+# tiled gate_proj buffer); asserted so that a dispatch change cannot leave a
+# timed kernel without an oracle case here
+C3_KERNELS = {1: "gemv", 2: "tgemm", 4: "tgemm", 8: "tgemm", 16: "tgemm", 32: "tgemm",
+              64: "tgemm", 128: "gemm64"}
+
+
+@pytest.mark.parametrize("M", sorted(C3_KERNELS))
 def test_c3_gate_sweep(llama_layer, M):
     bufs, _, w_hat = llama_layer
     buf = bufs["gate"]
+    assert buf._tiled is not None
+    kernel = bench.kernel_of(buf, M)
+    assert kernel == C3_KERNELS[M], f"M={M}: bench times {kernel}"
     x = torch.randn(M, 4096, generator=torch.Generator().manual_seed(100 + M)).half()
-    _check(_launch(buf, x), _ref_fp32(x, w_hat["gate"]),
-           f"C3 gate 14336x4096 M={M} ({P.kernel_choice(M, 14336, 4096, GS)})")
+    _check_twice(buf, x, _ref_fp32(x, w_hat["gate"]), f"C3 gate 14336x4096 M={M} ({kernel})")
+
+
+def _check_twice(buf, x, ref, what):
+    """_check of one launch, then the same launch again: the same bits (the K
+    split combines partials in split order, whatever the arrival order)."""
+    y = _launch(buf, x)
+    _check(y, ref, what)
+    assert torch.equal(_launch(buf, x).view(torch.int16), y.view(torch.int16)), what
+    return y
+
+
+@pytest.mark.parametrize("M", [2, 8])
+def test_c3_fused_gate_up_tiled(llama_layer, M):
+    """The plain tiled GEMM (no act_order, no K split) at 2 and 8 rows on the
+    fused gate/up shape 28672x4096: a tiled copy of the fused buffer, the
+    kernel pinned to the tiled GEMM where dispatch would pick another."""
+    from pare_amd.kernels import force_kernel
+
+    bufs, _, w_hat = llama_layer
+    fused = bufs["gate_up"]
+    buf = bench.Buf("gate_up_tiled", fused.w, fused.s, fused.z)
+    buf.tiled()
+    assert P.kernels.tgemm_splits(M, buf.N, buf.K, GS) == 1
+    x = torch.randn(M, 4096, generator=torch.Generator().manual_seed(200 + M)).half()
+    with force_kernel("tgemm"):
+        y = _launch(buf, x)
+    _check(y, _ref_fp32(x, np.concatenate([w_hat["gate"], w_hat["up"]])),
+           f"C3 fused gate_up 28672x4096 M={M} (tgemm, forced)")
 
 
 # ---------------------------------------------------------------------------
@@ -251,11 +297,20 @@ def test_prefill_sizes(llama_layer, name, M):
 # C4: Qwen2.5-7B act_order layers at M = 1 and 16, as the bench builds them
 # ---------------------------------------------------------------------------
 
+# the kernel and K split bench.py's Qwen leg times (tiled copies built, as
+# there) per (layer, M)
+C4_KERNELS = {("q_o", 1): ("gemv", 1), ("q_o", 16): ("tgemm", 1),
+              ("k_v", 1): ("gemv", 1), ("k_v", 16): ("tgemm", 4),
+              ("gate_up", 1): ("gemv", 1), ("gate_up", 16): ("tgemm", 1),
+              ("down", 1): ("gemv", 1), ("down", 16): ("tgemm", 4)}
+
+
 @pytest.mark.parametrize("qi", range(len(bench.QWEN)))
 def test_c4_qwen_act_order(qi):
     name, N, K = bench.QWEN[qi]
     seed = 7000 + 100 * qi
     buf = bench.make_act_order_layer(N, K, seed, DEV)
+    buf.tiled()   # bench.py builds the tiled copy of every Qwen layer
     g = torch.Generator(device=DEV).manual_seed(seed)
     w = torch.randn(N, K, generator=g, device=DEV) * 0.02
     perm = torch.randperm(K, generator=g, device=DEV).cpu().numpy()
@@ -266,9 +321,12 @@ def test_c4_qwen_act_order(qi):
     q[:, perm] = O.unpack_int4(packed_p)
     w_hat = O.dequantize_gidx(q, s, z, O.gidx_from_perm(perm, GS))
     for M in (1, 16):
+        kernel = bench.kernel_of(buf, M)
+        splits = P.kernels.tgemm_splits(M, N, K, GS, perm=True) if kernel == "tgemm" else 1
+        assert (kernel, splits) == C4_KERNELS[(name, M)], f"{name} M={M}: {kernel}, {splits} splits"
         x = torch.randn(M, K, generator=torch.Generator().manual_seed(M + qi)).half()
-        _check(_launch(buf, x), _ref_fp32(x, w_hat),
-               f"C4 qwen {name} {N}x{K} act_order M={M} ({P.kernel_choice(M, N, K, GS)})")
+        _check_twice(buf, x, _ref_fp32(x, w_hat),
+                     f"C4 qwen {name} {N}x{K} act_order M={M} ({kernel}, {splits} K ranges)")
 
 
 # ---------------------------------------------------------------------------

@@ -177,7 +177,7 @@ def _tgemm_case(M, N, K, gs, seed, kernel="tgemm", act_order=False, no_workspace
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 3, 5, 8, 16, 17, 24, 32, 33, 47, 64, 65, 100])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 16, 17, 24, 32, 33, 47, 64, 65, 100])
 def test_tgemm_rows(M):
     _tgemm_case(M, 1024, 2048, 128, seed=10 + M)
 
@@ -195,7 +195,7 @@ SPLIT_CASES = [
     # act_order gathered into the workspace first (the in-kernel gather stops at
     # K = 8192), one row included
     (4, 1024, 14336, 128, False), (16, 3584, 18944, 128, False), (2, 512, 18944, 128, True),
-    (7, 1024, 18944, 128, True), (1, 512, 14336, 128, True),
+    (7, 1024, 18944, 128, True), (1, 512, 14336, 128, True), (16, 3584, 18944, 128, True),
     # 13-16 rows, 1024 < N <= 4096: four tiles per workgroup, K split four ways
     (16, 2048, 4096, 128, False), (13, 4036, 2048, 128, False)]
 
@@ -242,6 +242,16 @@ def test_tgemm_narrow_many_rows(M, N, K, act_order):
 @pytest.mark.parametrize("M", [4, 16, 32, 64])
 def test_tgemm_shapes(M, N, K):
     _tgemm_case(M, N, K, 128, seed=N % 97 + M)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N", [14336, 28672])
+@pytest.mark.parametrize("M", [2, 8])
+def test_tgemm_gate_rows_2_and_8(M, N):
+    """The plain tiled GEMM (unsplit, no act_order) at 2 and 8 rows on gate_proj
+    and the fused gate/up shape."""
+    assert tgemm_splits(M, N, 4096, 128) == 1
+    _tgemm_case(M, N, 4096, 128, seed=N % 89 + M)
 
 
 @pytest.mark.gpu
