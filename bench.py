@@ -365,7 +365,9 @@ def reference_shapes(dev, stream):
     4096x4096 INT4 g128 at "BS" 1, 4, 16 of x [bs, 128, 4096], i.e. M = 128, 512,
     2048, kernel against the same module's dequantize-on-the-fly forward
     (use_kernel=False: HIP dequant to fp16, then torch's fp16 GEMM). Each path
-    is captured as a graph of 10 calls and replayed."""
+    is captured as a graph of 10 calls and replayed. Beside them, torch's plain
+    fp16 GEMM (hipBLASLt) on an fp16 weight of the same shape, the practical
+    ceiling of the matrix cores there."""
     import torch
     import torch.nn as nn
 
@@ -394,7 +396,26 @@ def reference_shapes(dev, stream):
             del g
         res["speedup"] = round(res["dequant_path_us"] / res["kernel_us"], 2)
         res["kernel_TFLOP/s"] = round(2 * M * 4096 * 4096 / (res["kernel_us"] * 1e-6) / 1e12, 1)
-        res["kernel"] = P.kernel_choice(M, 4096, 4096, GS)
+        res["kernel"] = P.kernel_choice(M, 4096, 4096, GS,
+                                        tiled=getattr(ql, "_packed_weight_tiled", None) is not None)
+        # the practical matrix-core ceiling at this shape: torch's fp16 GEMM
+        # (hipBLASLt) on an fp16 weight, eager, 4 weight copies x 10 calls
+        wf = [torch.randn(4096, 4096, device=dev).half() for _ in range(4)]
+        yf = torch.empty(M, 4096, device=dev).half()
+        with torch.cuda.stream(stream):
+            for w in wf:
+                torch.matmul(x, w.t(), out=yf)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(10):
+                for w in wf:
+                    torch.matmul(x, w.t(), out=yf)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        res["torch_fp16_gemm_us"] = round(e0.elapsed_time(e1) * 1e3 / 40, 2)
+        res["kernel_vs_fp16_gemm"] = round(res["torch_fp16_gemm_us"] / res["kernel_us"], 2)
+        del wf, yf
         rows[f"bs{bs}"] = res
         log(f"  reference shape 4096x4096 M={M}: {res}")
     ql.use_kernel = True
@@ -565,14 +586,18 @@ def main():
             else:
                 gate_loop(s, m_rows, 2 * n_layers)
 
+        timed = ""
         if args.graph:
             # the launch mode of the timed legs: one pass captured in a graph,
-            # replayed five times
+            # replayed twice untimed, then `--steps` replays timed with HIP
+            # events on the launch stream (as the JSON line's legs are)
             gk = capture(one_pass, stream)
             with torch.cuda.stream(stream):
-                for _ in range(5):
+                for _ in range(2):
                     gk.replay()
-            torch.cuda.synchronize()
+            per_pass = 2 * n_layers if args.kernel_only != "read_floor" else len(fused)
+            us = time_graph(gk, args.steps, stream) * 1e3 / per_pass
+            timed = f", {us:.3f} us per launch over {args.steps} timed replays of {per_pass} launches"
         else:
             with torch.cuda.stream(stream):
                 for _ in range(5):
@@ -580,7 +605,7 @@ def main():
             torch.cuda.synchronize()
         what = ("read probe" if args.kernel_only == "read_floor" else
                 f"kernel {kernel_of(fused[0][2], 1) if args.kernel_only == 'gate_up_m1' else kernel_of(single[0][4], m_rows)}")
-        log(f"{args.kernel_only} (M={m_rows}): 5 passes{' (graph replays)' if args.graph else ''}, {what}")
+        log(f"{args.kernel_only} (M={m_rows}): {what}{timed}")
         return
 
     # --- eager vs graph: same outputs -------------------------------------

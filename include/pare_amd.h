@@ -386,7 +386,11 @@ PMI_API int pmi_gptq_pack(const uint8_t* codes, const int32_t* inv_perm, uint8_t
  * N % 4 == 0, group_size 32, 64 or a multiple of 128; needs the w_tiled copy,
  * so it is chosen only with PMI_CHOICE_TILED in flags; with PMI_CHOICE_PERM
  * as well, up to 16 rows it gathers X[:, perm] itself when M (2K + 16) + 4K
- * bytes fit its LDS, which widens where it wins). flags 0 and 1 keep the
+ * bytes fit its LDS, which widens where it wins), 6 = the tiled GEMM's
+ * big-tile variant (same buffers; many activation rows, group_size % 128 ==
+ * 0: 256 weight rows x 128 activation rows per workgroup, B formed as
+ * fp16((q - z) * s) as the reference dequantises; with PMI_CHOICE_PERM
+ * X[:, perm] is gathered into the workspace first). flags 0 and 1 keep the
  * meaning of the former has_tiled argument. Host-only; no reference
  * counterpart (the reference has one Triton kernel). */
 PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size,
@@ -402,7 +406,7 @@ PMI_API int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t gr
  * act_order perm. Host-only diagnostic; no reference counterpart. */
 PMI_API int pmi_tgemm_splits(int64_t M, int64_t N, int64_t K, int64_t group_size, int has_perm);
 
-/* Forces pmi_matmul_w4a16 onto one kernel (1 to 5 as above; 0 restores the
+/* Forces pmi_matmul_w4a16 onto one kernel (1 to 6 as above; 0 restores the
  * automatic choice) for every thread of the process; returns the previous
  * setting, or PMI_ERR_INVALID for an unknown value. A test and benchmarking
  * hook with no reference counterpart. A forced kernel that cannot run a shape

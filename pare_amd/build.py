@@ -21,7 +21,7 @@ LIB_PATH = PKG_DIR / LIB_NAME
 
 SOURCES = ["capi.hip", "w4a16_gemv.hip", "w4a16_gemm.hip", "w4a16_gemm64.hip", "w4a16_skinny.hip",
            "w4a16_layout.hip", "decode_ops.hip", "gptq.hip", "probes.hip",
-           "w4a16_tgemm.hip"]
+           "w4a16_tgemm.hip", "w4a16_bgemm.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

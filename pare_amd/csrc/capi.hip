@@ -150,7 +150,7 @@ int pmi_storage_to_awq_gemm(const uint8_t* packed, const float* scale, const voi
 }
 
 int pmi_set_kernel_override(int kernel) {
-  if (kernel < 0 || kernel > 5)
+  if (kernel < 0 || kernel > 6)
     return fail(PMI_ERR_INVALID, "pmi_set_kernel_override: unknown kernel %d", kernel);
   ok();
   return g_kernel_override.exchange(kernel);
@@ -201,6 +201,13 @@ int pmi_matmul_kernel_choice(int64_t M, int64_t N, int64_t K, int64_t group_size
     const pmi::TgemmConfig c =
         pmi::tgemm_config(M, N, K, group_size, has_perm && pmi::tgemm_gather_supported(M, K));
     if (c.splits > 1 && c.ntw == 4) return 5;
+  }
+  // Many activation rows (prefill): the big-tile GEMM, 256 weight rows x 128
+  // activation rows per workgroup, where its tiles fill three quarters of
+  // the CUs in one pass or more.
+  if (has_tiled && M > 64 && group_size % 128 == 0 && pmi::tgemm_supported(M, N, K, group_size)) {
+    const pmi::BgemmConfig b = pmi::bgemm_config(M, N, K, group_size);
+    if (b.ok && (int64_t)b.n_bands * b.grid_m * 4 >= 3 * cus) return 6;
   }
   // Past 64 rows on narrow layers, while the tiled GEMM's 64-row blocks still
   // take one pass over the CUs: against the register-streamed GEMM, whose K
@@ -542,10 +549,29 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   const bool has_tiled = w_tiled && scales_gm && zeros_gm && N % 4 == 0;
   int choice = pmi_matmul_kernel_choice(
       M, N, K, group_size, (has_tiled ? PMI_CHOICE_TILED : 0) | (perm ? PMI_CHOICE_PERM : 0));
-  // the tiled GEMM's epilogue stores up to four fp16 outputs (8 bytes) per lane
-  if (choice == 5 && !aligned(y, 8)) {
+  // the tiled GEMM's epilogue (both variants) stores up to four fp16 outputs
+  // (8 bytes) per lane
+  if ((choice == 5 || choice == 6) && !aligned(y, 8)) {
     if (forced) return fail(PMI_ERR_INVALID, "%s: the tiled GEMM needs y 8-byte aligned", fn);
     choice = pmi_matmul_kernel_choice(M, N, K, group_size, perm ? PMI_CHOICE_PERM : 0);
+  }
+  if (choice == 6) {
+    if (!has_tiled || !pmi::tgemm_supported(M, N, K, group_size) || group_size % 128 != 0 ||
+        !pmi::bgemm_config(M, N, K, group_size).ok)
+      return fail(PMI_ERR_UNSUPPORTED, "%s: the big-tile GEMM needs w_tiled, scales_gm and zeros_gm, "
+                  "N %% 4 == 0, K %% 512 == 0, K >= 1536, group_size %% 128 == 0 and M * K < 2^30", fn);
+    // act_order: X[:, perm] gathered into the workspace first
+    const void* xs = x;
+    if (perm) {
+      if (workspace_bytes < pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K))
+        return fail(PMI_ERR_UNSUPPORTED, "%s: the big-tile GEMM with perm needs a workspace of "
+                    "pmi_matmul_workspace_bytes() bytes", fn);
+      void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
+      hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
+      if (e != hipSuccess) return from_hip(e, fn);
+      xs = xg;
+    }
+    return from_hip(pmi::launch_bgemm(xs, w_tiled, scales_gm, zeros_gm, y, M, N, K, group_size, s), fn);
   }
   if (choice == 5) {
     if (!has_tiled || !pmi::tgemm_supported(M, N, K, group_size))

@@ -228,6 +228,20 @@ bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 constexpr int kTgemmXGLds = 160 * 1024 - 1024;
 bool tgemm_gather_supported(int64_t M, int64_t K);
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gather);
+// The big-tile variant of the tiled GEMM (w4a16_bgemm.hip), for many
+// activation rows: 256 weight rows (four panels) x 128 activation rows per
+// workgroup over all of K, B formed as fp16((q - z) * s); no workspace.
+struct BgemmConfig {
+  bool ok;      // the shape is within the kernel's limits (gs % 128 == 0, K % 128 == 0)
+  int n_bands;  // bands of four 64-row panels
+  int grid_m;   // 128-row activation blocks
+  int chunk;    // (activation block, band) pairs per XCD
+  int grid;     // workgroups (8 chunk)
+};
+BgemmConfig bgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs);
+hipError_t launch_bgemm(const void* x, const uint8_t* w_tiled, const float* scales_gm,
+                        const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        hipStream_t stream);
 // perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null.
 // workspace: counters (zero between calls) at its start and the split-K partial
 // tiles at part_offset; null or too small for them, the kernel runs unsplit.

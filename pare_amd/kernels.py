@@ -419,7 +419,7 @@ def matmul_w4a16_tiled_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None,
     return out, h
 
 
-_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4, "tgemm": 5}
+_KERNEL_IDS = {"auto": 0, "gemv": 1, "gemm": 2, "skinny": 3, "gemm64": 4, "tgemm": 5, "bgemm": 6}
 
 
 class force_kernel:
@@ -441,12 +441,12 @@ class force_kernel:
 
 def kernel_choice(M: int, N: int, K: int, group_size: int, tiled: bool = False,
                   perm: bool = False) -> str:
-    """'gemv', 'gemm', 'skinny', 'gemm64' or 'tgemm': the kernel matmul_w4a16 runs
-    for this shape (``tiled``: the caller passes the tiled weight copy;
-    ``perm``: an act_order permutation)."""
+    """'gemv', 'gemm', 'skinny', 'gemm64', 'tgemm' or 'bgemm' (the tiled GEMM's
+    big-tile variant): the kernel matmul_w4a16 runs for this shape (``tiled``: the
+    caller passes the tiled weight copy; ``perm``: an act_order permutation)."""
     flags = (_lib.PMI_CHOICE_TILED if tiled else 0) | (_lib.PMI_CHOICE_PERM if perm else 0)
     c = _lib.lib().pmi_matmul_kernel_choice(M, N, K, group_size, flags)
-    return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64", 5: "tgemm"}[c]
+    return {1: "gemv", 2: "gemm", 3: "skinny", 4: "gemm64", 5: "tgemm", 6: "bgemm"}[c]
 
 
 def tgemm_splits(M: int, N: int, K: int, group_size: int, perm: bool = False) -> int:

@@ -148,7 +148,7 @@ class QuantizedLinear(nn.Module):
             if not tiled_supported(self.out_features, self.in_features, self._group_size()):
                 return None
             if kernel_choice(M, self.out_features, self.in_features, self._group_size(),
-                             tiled=True, perm=perm is not None) != "tgemm":
+                             tiled=True, perm=perm is not None) not in ("tgemm", "bgemm"):
                 return None
             if torch.cuda.is_current_stream_capturing():
                 return None

@@ -56,6 +56,9 @@ def test_kernel_choice(L):
     assert L.pmi_matmul_kernel_choice(2, 6144, 4096, 128, 1) == 1     # GEMV at 2 rows below N = 8192
     assert L.pmi_matmul_kernel_choice(1, 14336, 4096, 128, 1) == 1    # GEMV at 1 row
     assert L.pmi_matmul_kernel_choice(64, 14336, 4096, 128, 1) == 5   # 64-row blocks
+    assert L.pmi_matmul_kernel_choice(2048, 4096, 4096, 128, 1) == 6  # big tiles: 16 x 16 workgroups
+    assert L.pmi_matmul_kernel_choice(2048, 4096, 4096, 128, 0) != 6  # ... only with the tiled copy
+    assert L.pmi_matmul_kernel_choice(2048, 4096, 4096, 64, 1) != 6   # gs 64: not the big tiles
     assert L.pmi_matmul_kernel_choice(65, 14336, 4096, 128, 1) != 5   # past 64 rows
     assert L.pmi_matmul_kernel_choice(64, 28672, 4096, 128, 1) != 5   # more than one pass
     assert L.pmi_matmul_kernel_choice(256, 1024, 4096, 128, 1) == 5   # narrow: 64-row blocks, one pass

@@ -365,3 +365,78 @@ def test_tgemm_tile_ranges(M, N, K, act_order):
     range of 5-8 consecutive 16-row tiles (ragged N, and the in-kernel act_order
     gather, included)."""
     _tgemm_case(M, N, K, 128, seed=N % 101 + M, act_order=act_order, no_workspace=True)
+
+
+# ---- the big-tile variant (kernel 6): many activation rows ------------------------
+
+BGEMM_CASES = [
+    # (M, N, K): 16 x 16 tiles, a partial last activation block, a last band of
+    # three panels, a last panel of 28 rows, long rows, gs 256
+    (2048, 4096, 4096, 128), (1000, 4096, 4096, 128), (640, 14272, 4096, 128),
+    (700, 14300, 2048, 128), (1536, 4096, 14336, 128), (1024, 4096, 4096, 256)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,gs", BGEMM_CASES)
+def test_bgemm_against_oracle(M, N, K, gs):
+    """The big-tile variant against the oracle (forced, and automatic where
+    dispatch picks it); the same call twice gives the same bits."""
+    y = _tgemm_case(M, N, K, gs, seed=M + N % 97, kernel="bgemm")
+    y2 = _tgemm_case(M, N, K, gs, seed=M + N % 97, kernel="bgemm")
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_bgemm_b_operand_is_the_reference_dequant():
+    """B = fp16((q - z) * s) with the reference's roundings: with x one-hot
+    rows, each output is one dequantised weight times 1, so y equals the
+    reference's fp16 dequantisation (pare/core/functional.py:91, then
+    .to(fp16)) bit for bit, including scales whose products round to fp16
+    ties."""
+    N, K, gs = 512, 2048, 128
+    g = torch.Generator().manual_seed(4)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy().astype(np.float32)
+    packed, s, z = O.rtn_quantize(w, gs)
+    # scales with many fp32 product bits: products land near fp16 ties
+    s = (s * np.float32(1.0009765625) + np.float32(3e-9)).astype(np.float32)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    sz = P.sz_group_major(_cuda(s), zu8)
+    wt = P.tile_w4a16(wk, gs)
+    M = 256
+    cols = np.arange(M) * 7 % K
+    x = torch.zeros(M, K, dtype=torch.float16)
+    x[torch.arange(M), torch.from_numpy(cols)] = 1.0
+    with force_kernel("bgemm"):
+        y = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt)
+    torch.cuda.synchronize()
+    ref = O.dequantize_packed(packed, s, z).astype(np.float16)   # [N, K]
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), ref[:, cols].T.view(np.uint16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (512, 14336, 4096), (2048, 28672, 4096)])
+def test_bgemm_automatic_dispatch(M, N, K):
+    assert P.kernel_choice(M, N, K, 128, tiled=True) == "bgemm"
+    _tgemm_case(M, N, K, 128, seed=N % 89 + M, kernel="auto")
+
+
+@pytest.mark.gpu
+def test_bgemm_act_order_gathered():
+    """act_order past 64 rows: X[:, perm] gathered into the workspace, then the
+    big-tile GEMM."""
+    assert P.kernel_choice(2048, 4096, 4096, 128, tiled=True, perm=True) == "bgemm"
+    _tgemm_case(2048, 4096, 4096, 128, seed=11, kernel="auto", act_order=True)
+
+
+@pytest.mark.gpu
+def test_bgemm_forced_on_unsupported_shape_raises():
+    N, K, gs = 1024, 2048, 64
+    packed, s, z = _layer(N, K, gs, 1)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    sz = P.sz_group_major(_cuda(s), zu8)
+    wt = P.tile_w4a16(wk, gs)
+    x = torch.randn(256, K, device=DEV, dtype=torch.float16)
+    with force_kernel("bgemm"), pytest.raises(RuntimeError, match="big-tile"):
+        P.matmul_w4a16(x, wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt)
