@@ -673,6 +673,28 @@ def main():
     log(f"  gate_up  28672x  4096 M=1: {gu_us:7.2f} us {gu_gbs:8.1f} GB/s")
     del gg
 
+    # the same launches with native bf16 activations (the bf16 extension;
+    # the reference casts bf16 to fp16 first)
+    xb = torch.randn(1, 4096, generator=g, device=dev).to(torch.bfloat16)
+    yb = torch.empty(1, 28672, dtype=torch.bfloat16, device=dev)
+
+    def gate_up_bf16(s):
+        for _ in range(2):
+            for f in fused:
+                b = f[2]
+                rc = L.pmi_matmul_w4a16(xb.data_ptr(), _lib.PMI_BF16, b.w.data_ptr(), b.s.data_ptr(),
+                                        b.z.data_ptr(), _lib.PMI_U8, None, None, None, None,
+                                        yb.data_ptr(), _lib.PMI_BF16, 1, b.N, b.K, GS,
+                                        WORKSPACE[0].data_ptr(), WORKSPACE[0].numel(), s)
+                assert rc == 0, _lib.last_error()
+    gb16 = capture(gate_up_bf16, stream)
+    gb16.replay()
+    bf_us = time_graph(gb16, 10, stream) * 1e3 / (2 * n_layers)
+    detail["gate_up_bf16"] = {"N": 28672, "K": 4096, "us": round(bf_us, 2),
+                              "GB/s": round(gu_bytes / (bf_us * 1e-6) / 1e9, 1), "kernel": "gemv (bf16)"}
+    log(f"  gate_up bf16 28672x4096 M=1: {bf_us:7.2f} us")
+    del gb16
+
     # --- M = 64 MFMA GEMM on gate_proj --------------------------------------
     copies = 2 * n_layers
     gm = capture(lambda s: gate_loop(s, 64, copies), stream)

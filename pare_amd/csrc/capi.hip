@@ -491,10 +491,15 @@ int pmi_tgemm_splits(int64_t M, int64_t N, int64_t K, int64_t group_size, int ha
 size_t pmi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size,
                                   int has_perm) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0 || K % group_size != 0) return 0;
-  // enough for whichever kernel runs, with or without the tiled copy
+  // enough for whichever kernel runs, with or without the tiled copy, and
+  // with act_order for the gather of X[:, perm] (bf16 activations always
+  // gather into the workspace)
   const size_t other = other_workspace_bytes(M, N, K, group_size, has_perm);
   const size_t tiled = tgemm_workspace_bytes(M, N, K, group_size, has_perm != 0);
-  return other > tiled ? other : tiled;
+  size_t need = other > tiled ? other : tiled;
+  if (has_perm && need < pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K))
+    need = pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K);
+  return need;
 }
 
 int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype, float* scales_gm,
@@ -520,9 +525,10 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   if (int rc = check_shape(N, K, group_size, fn)) return rc;
   if (int rc = check_zero_dtype(zero_dtype, fn)) return rc;
   if (M < 0) return fail(PMI_ERR_INVALID, "%s: M < 0", fn);
-  if (x_dtype != PMI_F16 || y_dtype != PMI_F16)
-    return fail(PMI_ERR_UNSUPPORTED, "%s: x and y must be fp16 (got x=%d y=%d)", fn, x_dtype,
-                y_dtype);
+  const bool bf = x_dtype == PMI_BF16;
+  if (!((x_dtype == PMI_F16 && y_dtype == PMI_F16) || (bf && y_dtype == PMI_BF16)))
+    return fail(PMI_ERR_UNSUPPORTED, "%s: x and y must both be fp16 or both bf16 (got x=%d y=%d)",
+                fn, x_dtype, y_dtype);
   if (M > (1ll << 31) - 1) return fail(PMI_ERR_UNSUPPORTED, "%s: M too large", fn);
   if (M == 0 || N == 0) return ok();
   if (!x || !w || !scales || !zeros || !y) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
@@ -545,6 +551,34 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   hipStream_t s = (hipStream_t)stream;
   const int zu8 = zero_dtype == PMI_U8;
   const int forced = g_kernel_override.load();
+  if (bf) {
+    // bf16 activations (the native bf16 extension) run on the GEMV, four
+    // activation rows per launch; act_order rows are gathered into the
+    // workspace first (2-byte elements, as for fp16)
+    if (forced && forced != 1)
+      return fail(PMI_ERR_UNSUPPORTED, "%s: bf16 activations run on the GEMV only (kernel %d forced)",
+                  fn, forced);
+    const uint16_t* xp = (const uint16_t*)x;
+    if (perm) {
+      if (workspace_bytes < pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K))
+        return fail(PMI_ERR_UNSUPPORTED, "%s: bf16 with perm needs a workspace of "
+                    "pmi_matmul_workspace_bytes() bytes", fn);
+      uint16_t* xg = (uint16_t*)((uint8_t*)workspace + pmi::kWsCounterBytes);
+      hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
+      if (e != hipSuccess) return from_hip(e, fn);
+      xp = xg;
+    }
+    pmi::GemvXform bxf;
+    bxf.mode = 6;
+    uint16_t* yp = (uint16_t*)y;
+    for (int64_t m = 0; m < M; m += 4) {
+      const int64_t mt = M - m < 4 ? M - m : 4;
+      hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, nullptr, yp + m * N, mt, N, K,
+                                      group_size, s, &bxf);
+      if (e != hipSuccess) return from_hip(e, fn);
+    }
+    return ok();
+  }
   // the tiled GEMM reads the tiled weights and the group-major scale/zero copies
   const bool has_tiled = w_tiled && scales_gm && zeros_gm && N % 4 == 0;
   int choice = pmi_matmul_kernel_choice(

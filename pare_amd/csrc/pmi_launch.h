@@ -103,6 +103,8 @@ size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool ha
 //           (r nullable; h = x + r written to h_out when r is given);
 //   mode 5: x is a residual stream, consumed as RMSNorm(x) * w, with sum(x^2)
 //           from per-workgroup partials a launch with `res` left;
+//   mode 6: x and y bf16 [M, K] / [M, N] (no perm; act_order rows are
+//           gathered by the caller first);
 //   mode 4: act_order, x[:, perm] gathered from a copy of x staged in LDS by
 //           each workgroup (needs gemv_perm_lds_fits), instead of every lane
 //           gathering from global memory.

@@ -30,6 +30,14 @@
 // slice waves wait in LDS and are added in a fixed order after one barrier at
 // the end. Results are deterministic and no workspace or atomics are used.
 //
+// bf16 activations (XM 6, the native bf16 extension): the weight operand is
+// the bf16 128 + q, exact, one v_perm_b32 per pair under a 0x43 byte (bf16
+// has no packed subtract on gfx950), and v_dot2_f32_bf16 forms the exact
+// products x (128 + q); per group the lane's term is s * (sum x (128 + q) -
+// (128 + z) * Sx) with the bracket formed by one fma, which equals
+// s * sum x (q - z) up to the fp32 rounding of the accumulated sums; y is
+// rounded to bf16 (nearest even).
+//
 // Semantics follow the reference Triton kernel (pare/kernels/matmul_int4.py:
 // 105-176): w = (q - zero) * scale per group, fp32 accumulation, fp16 output.
 #include "pmi_common.h"
@@ -264,7 +272,14 @@ PMI_DEV float zero_value(uint32_t raw) {
 // row as s * (2^24 * sum_lo + 2^20 * sum_hi - z * Sx). 5 bit ops + 4 dot2 per
 // word. After the wave reduction, lane `idx`-writers hold row u's value for
 // activation row m in v[0] (idx = u * MT + m).
-template <int MT, int U, int SPW, bool ZU8>
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+PMI_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+template <int MT, int U, int SPW, bool ZU8, bool BF = false>
 PMI_DEV void reduce_batch(const Batch<U, SPW, ZU8>& bt, const uint32_t (&xp)[SPW][MT][16],
                           const float (&sx)[SPW][MT], float (&out)[Pow2Ceil<U * MT>::value],
                           int lane) {
@@ -276,6 +291,36 @@ PMI_DEV void reduce_batch(const Batch<U, SPW, ZU8>& bt, const uint32_t (&xp)[SPW
   for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int sp = 0; sp < SPW; ++sp) {
+      if constexpr (BF) {
+        // bf16: weight pairs (128 + q) in column order, one accumulator
+        float pa[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) pa[m] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t wd = bt.w[sp][u][i];
+          const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+          const uint32_t b0 = __builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u);
+          const uint32_t b1 = __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u);
+          const uint32_t b2 = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
+          const uint32_t b3 = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            pa[m] = dot2_bf16(b0, xp[sp][m][4 * i + 0], pa[m]);
+            pa[m] = dot2_bf16(b1, xp[sp][m][4 * i + 1], pa[m]);
+            pa[m] = dot2_bf16(b2, xp[sp][m][4 * i + 2], pa[m]);
+            pa[m] = dot2_bf16(b3, xp[sp][m][4 * i + 3], pa[m]);
+          }
+        }
+        const float sc = bt.s[sp][u];
+        const float zb = -(128.f + zero_value<ZU8>(bt.z[sp][u]));  // -(128 + z), exact
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          float& acc = v[u * MT + m];
+          acc = fmaf(sc, fmaf(zb, sx[sp][m], pa[m]), acc);
+        }
+        continue;
+      }
       float pl[MT], ph[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) pl[m] = ph[m] = 0.f;
@@ -349,6 +394,14 @@ PMI_DEV float sq_pairs(const uint32_t (&v)[8], float acc) {
   return acc;
 }
 
+// One output: fp16, or with BF the bf16 bits in the same 2-byte slot; both
+// round to nearest even.
+template <bool BF>
+PMI_DEV void store_y(f16* p, float v) {
+  if constexpr (BF) *reinterpret_cast<uint16_t*>(p) = f32_to_bf16_rne(v);
+  else *p = f32_to_f16_rne(v);
+}
+
 // XM selects the activation source: 0 x [M, K]; 1 x[:, perm] (act_order),
 // gathered by every lane from global memory; 4 the same, x staged in LDS once
 // per workgroup (16-byte loads) and gathered from there;
@@ -358,7 +411,7 @@ PMI_DEV float sq_pairs(const uint32_t (&v)[8], float acc) {
 // residual stream x whose sum of squares the launch that formed it left as
 // per-workgroup partials (xf.stats, xf.n_stats of them): every wave adds them
 // in the same fixed order, so no workgroup reduces the row or waits at a
-// barrier first.
+// barrier first; 6 bf16 x [M, K], y bf16 (the native bf16 extension).
 // Epilogue (xf.res, one activation row, slice_waves > 1): y = h = y + res
 // rounded as add_rmsnorm_kernel forms h, and xf.stats[blockIdx.x] = the sum of
 // h^2 over the workgroup's rows (fixed order), for a mode-5 launch to read.
@@ -594,14 +647,30 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
             xb[sp][m][i] = glu_pair(xb[sp][m][i], ub[sp][m][i]);
           }
         }
-        pair_x(xa[sp][m], xb[sp][m], xp[sp][m]);
+        if constexpr (XM == 6) {
+          // bf16: the pairs in column order, as the weight pairs are formed
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            xp[sp][m][4 * i + 0] = xa[sp][m][2 * i];
+            xp[sp][m][4 * i + 1] = xa[sp][m][2 * i + 1];
+            xp[sp][m][4 * i + 2] = xb[sp][m][2 * i];
+            xp[sp][m][4 * i + 3] = xb[sp][m][2 * i + 1];
+          }
+        } else {
+          pair_x(xa[sp][m], xb[sp][m], xp[sp][m]);
+        }
         if (!act[sp]) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) xp[sp][m][i] = 0u;
         }
         float acc = 0.f;
+        if constexpr (XM == 6) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc = dot2_acc(as_f16x2(0x3C003C00u), xp[sp][m][i], acc);
+          for (int i = 0; i < 16; ++i) acc = dot2_bf16(0x3F803F80u, xp[sp][m][i], acc);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc = dot2_acc(as_f16x2(0x3C003C00u), xp[sp][m][i], acc);
+        }
         sx[sp][m] = acc;
       }
   };
@@ -611,12 +680,12 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   // Reduces batch b and stores (or parks) its results.
   auto finish = [&](const Batch<U, SPW, ZU8>& bt, int b) {
     float v[VP];
-    reduce_batch<MT, U, SPW, ZU8>(bt, xp, sx, v, lane);
+    reduce_batch<MT, U, SPW, ZU8, XM == 6>(bt, xp, sx, v, lane);
     if (writer) {
       const int lr = wr * U + b * stride + wu;  // row within the workgroup
       if (row0 + lr < row_lim) {
         if (slice_waves == 1)
-          y[(int64_t)wm * N + row0 + lr] = f32_to_f16_rne(v[0]);
+          store_y<XM == 6>(y + (int64_t)wm * N + row0 + lr, v[0]);
         else
           part[(lr * slice_waves + ws) * MT + wm] = v[0];
       }
@@ -668,6 +737,10 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     const int lr = e / MT, m = e - (e / MT) * MT;
     float s = 0.f;
     for (int q = 0; q < slice_waves; ++q) s += part[(lr * slice_waves + q) * MT + m];
+    if constexpr (XM == 6) {
+      store_y<true>(y + (int64_t)m * N + row0 + lr, s);
+      continue;
+    }
     f16 yv = f32_to_f16_rne(s);
     if constexpr (RES) {
       const f16 rv = e == (int)threadIdx.x ? rpre
@@ -737,6 +810,11 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
     if (xf.mode == 2) PMI_GEMV_LAUNCH(2, true);
     else if (xf.mode == 3) PMI_GEMV_LAUNCH(3, true);
     else PMI_GEMV_LAUNCH(5, true);
+  } else if (xf.mode == 6) {
+    // bf16 activations: plain rows (act_order is gathered by the caller first)
+    if (perm) return hipErrorInvalidValue;
+    if (zero_u8) PMI_GEMV_LAUNCH(6, true);
+    else PMI_GEMV_LAUNCH(6, false);
   } else if (perm_lds) {
     if (zero_u8) PMI_GEMV_LAUNCH(4, true);
     else PMI_GEMV_LAUNCH(4, false);
@@ -916,7 +994,9 @@ hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, con
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream, const GemvXform* xform) {
   const GemvXform xf = xform ? *xform : GemvXform{};
-  const GemvConfig c = gemv_config(M, N, K, perm || xf.mode != 4 ? xf.mode : 0);
+  // bf16 activations (mode 6) take the plain tuning
+  const int tune_mode = xf.mode == 6 ? 0 : (perm || xf.mode != 4 ? xf.mode : 0);
+  const GemvConfig c = gemv_config(M, N, K, tune_mode);
   const int n = (int)N, k = (int)K, g = (int)gs;
   switch (M) {
     case 1: return launch_mt<1>(c, x, w, scales, zeros, zero_u8, perm, y, n, k, g, xf, stream);

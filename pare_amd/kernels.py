@@ -141,11 +141,41 @@ def matmul_w4a16(
     Raises RuntimeError when x is not on a HIP device or the library is
     missing; AssertionError on layout violations, like the reference.
     """
-    L = _lib.lib()
     if not x.is_cuda:
         raise RuntimeError("matmul_w4a16 requires HIP (cuda) tensors.")
     assert x.is_contiguous(), "x must be contiguous"
     assert x.dtype == torch.float16, f"x must be float16, got {x.dtype}"
+    return _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out)
+
+
+def matmul_w4a16_bf16(
+    x: torch.Tensor,
+    packed_weight: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    group_size: int,
+    *,
+    perm: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Y[M,N] = X[M,K] @ dequant(W)^T with bf16 X and Y (native bf16 activations).
+
+    An extension without a reference counterpart: the reference casts bf16
+    activations to fp16 before its kernel (pare/layers/linear.py:154-156),
+    which ``matmul_w4a16`` keeps. Here the bf16 values are used as they are
+    (fp32 accumulation, y rounded to bf16), on the GEMV, four activation rows
+    per launch. Other arguments as for ``matmul_w4a16``."""
+    if not x.is_cuda:
+        raise RuntimeError("matmul_w4a16_bf16 requires HIP (cuda) tensors.")
+    assert x.is_contiguous(), "x must be contiguous"
+    assert x.dtype == torch.bfloat16, f"x must be bfloat16, got {x.dtype}"
+    return _matmul(x, packed_weight, scales, zeros, group_size, perm, None, None, out)
+
+
+def _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out):
+    """The shared argument checks and the pmi_matmul_w4a16 call (x fp16 or
+    bf16, y of the same dtype)."""
+    L = _lib.lib()
     assert x.dim() == 2, f"x must be 2-D [M, K], got shape {tuple(x.shape)}"
     M, K = x.shape
     N, K_half = packed_weight.shape
@@ -182,21 +212,22 @@ def matmul_w4a16(
         assert w_tiled.numel() == L.pmi_tiled_bytes(N, K), \
             f"w_tiled must hold pmi_tiled_bytes(N, K)={L.pmi_tiled_bytes(N, K)} bytes"
         w_tiled = _aligned16(w_tiled)
+    code = _lib.PMI_BF16 if x.dtype == torch.bfloat16 else _lib.PMI_F16
     if out is None:
-        out = torch.empty(M, N, device=dev, dtype=torch.float16)
+        out = torch.empty(M, N, device=dev, dtype=x.dtype)
     else:
-        assert out.dtype == torch.float16 and tuple(out.shape) == (M, N) and out.is_contiguous(), \
-            "out must be a contiguous [M, N] float16 tensor"
+        assert out.dtype == x.dtype and tuple(out.shape) == (M, N) and out.is_contiguous(), \
+            f"out must be a contiguous [M, N] {x.dtype} tensor"
     with _DeviceGuard(dev):
         stream = _stream_handle(dev)
         nbytes = L.pmi_matmul_workspace_bytes(M, N, K, group_size, int(perm is not None))
         ws = _workspace(dev, stream, nbytes)
         _lib.check(L.pmi_matmul_w4a16(
-            xa.data_ptr(), _lib.PMI_F16, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
+            xa.data_ptr(), code, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
             perm.data_ptr() if perm is not None else None,
             s_gm.data_ptr() if s_gm is not None else None,
             z_gm.data_ptr() if z_gm is not None else None,
-            w_tiled.data_ptr() if w_tiled is not None else None, out.data_ptr(), _lib.PMI_F16,
+            w_tiled.data_ptr() if w_tiled is not None else None, out.data_ptr(), code,
             M, N, K, group_size, ws.data_ptr() if ws is not None else None,
             ws.numel() if ws is not None else 0, stream), "pmi_matmul_w4a16")
     return out

@@ -21,7 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .config import QuantConfig, is_int4, kernel_group_size
-from .kernels import kernel_choice, matmul_w4a16
+from .kernels import kernel_choice, matmul_w4a16, matmul_w4a16_bf16
 from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
                    tile_w4a16, tiled_supported,
                    zeros_to_u8)
@@ -40,6 +40,9 @@ class QuantizedLinear(nn.Module):
         self.in_features = in_features
         self.out_features = out_features
         self.use_kernel = use_kernel
+        # opt-in extension: bf16 inputs on the kernel path stay bf16 instead
+        # of the reference's cast to fp16 (pare/layers/linear.py:154-156)
+        self.native_bf16 = False
         self.quantize_inputs = False
         self.register_buffer("packed_weight", packed_weight)
         self.register_buffer("q_weight", None)
@@ -166,9 +169,18 @@ class QuantizedLinear(nn.Module):
         self._build_kernel_cache(w_kernel.contiguous())
 
     def _forward_kernel(self, x: torch.Tensor) -> torch.Tensor:
-        """pare/layers/linear.py:140-159 with the HIP kernels."""
+        """pare/layers/linear.py:140-159 with the HIP kernels. bf16 inputs are
+        cast to fp16 as the reference does (linear.py:154-156), unless
+        ``native_bf16`` is set on the module: then they run as bf16
+        (``matmul_w4a16_bf16``)."""
         w_k, zero_u8, perm, sz_gm = self._kernel_buffers()
         orig_shape = x.shape
+        if x.dtype == torch.bfloat16 and getattr(self, "native_bf16", False):
+            y = matmul_w4a16_bf16(x.reshape(-1, self.in_features).contiguous(), w_k, self.scale,
+                                  zero_u8, self._group_size(), perm=perm)
+            if self.bias is not None:
+                y = y + self.bias
+            return y.reshape(*orig_shape[:-1], self.out_features)
         x_2d = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
         w_t = self._tiled_buffer(w_k, x_2d.shape[0], perm)
         y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm, sz_gm=sz_gm,

@@ -710,3 +710,97 @@ def test_llama_decode_layers_full_size(N, K):
     """Llama-3.1-8B decode layers at M=1 (and the M=64 crossover side)."""
     for M in (1, 64):
         _matmul_case(M, N, K, 128, 10 + N // 1024 + M)
+
+
+# ---- native bf16 activations (extension: the reference casts to fp16) -------------
+
+def _bf16_ref(x: torch.Tensor, w_hat: np.ndarray) -> np.ndarray:
+    """The oracle in bf16: the dequantised weight rounded to bf16 (nearest
+    even), then x @ W^T accumulated in fp32."""
+    wb = torch.from_numpy(np.ascontiguousarray(w_hat, dtype=np.float32)).bfloat16().float()
+    return (x.float().cpu() @ wb.T).numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 1), (1024, 4096, 1), (14336, 4096, 1),
+                                   (4096, 14336, 1), (4096, 4096, 3), (6144, 4096, 2),
+                                   (1024, 4096, 7)])
+def test_bf16_matmul_against_oracle(N, K, M):
+    """matmul_w4a16_bf16 on the C1/C2 shapes (and 2, 3 and 7 rows); y is bf16.
+
+    Against the fp32-accumulated oracle at rtol = atol = 1e-2. Against the
+    bf16 oracle (weights rounded to bf16 first, as the reference's dequant
+    path does for bf16 inputs, pare/layers/linear.py:129,138) at the same
+    rtol/atol plus that oracle's own rounding bound, sum_k |x_k| |w_k| 2^-9:
+    the kernel applies the weights at fp32 precision, so on long rows (K =
+    14336) the two differ by up to ~0.02 from the oracle's rounding alone."""
+    gs = 128
+    g = torch.Generator().manual_seed(N + K + M)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    packed, s, z = O.rtn_quantize(w, gs)
+    wk = P.repack_int4_for_kernel(torch.from_numpy(packed).to(DEV), gs)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    y = P.matmul_w4a16_bf16(x.to(DEV), wk, torch.from_numpy(s).to(DEV),
+                            P.zeros_to_u8(torch.from_numpy(z).to(DEV)), gs)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (M, N)
+    w_hat = O.dequantize_packed(packed, s, z)
+    got = y.float().cpu().numpy()
+    xf = x.float().numpy()
+    round_bound = (np.abs(xf) @ np.abs(w_hat).T) * 2.0 ** -9
+    for ref, extra, what in ((O.linear_fp32(xf, w_hat), 0.0, "fp32"),
+                             (_bf16_ref(x, w_hat), round_bound, "bf16 oracle")):
+        err = np.abs(got - ref)
+        print(f"[parity] bf16 M={M} N={N} K={K} vs {what}: max_abs={err.max():.3e}", flush=True)
+        assert (err <= 1e-2 + 1e-2 * np.abs(ref) + extra).all(), f"{what}: max_abs={err.max():.4e}"
+
+
+@pytest.mark.gpu
+def test_bf16_one_hot_rows_give_the_dequantised_weight():
+    """With one-hot activation rows each output is one weight: s (q - z) formed
+    in fp32 and rounded to bf16, i.e. the reference's dequantisation
+    (pare/core/functional.py:91) cast to bf16, bit for bit."""
+    N, K, gs = 256, 1024, 128
+    g = torch.Generator().manual_seed(5)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    packed, s, z = O.rtn_quantize(w, gs)
+    wk = P.repack_int4_for_kernel(torch.from_numpy(packed).to(DEV), gs)
+    cols = [0, 1, 63, 64, 65, 127, 128, 511, 777, 1023]
+    x = torch.zeros(len(cols), K, dtype=torch.bfloat16)
+    x[torch.arange(len(cols)), torch.tensor(cols)] = 1.0
+    y = P.matmul_w4a16_bf16(x.to(DEV), wk, torch.from_numpy(s).to(DEV),
+                            P.zeros_to_u8(torch.from_numpy(z).to(DEV)), gs)
+    ref = torch.from_numpy(O.dequantize_packed(packed, s, z)[:, cols].T.copy()).bfloat16()
+    assert torch.equal(y.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_bf16_act_order_and_module_flag():
+    """act_order rows (X[:, perm] gathered into the workspace first) and the
+    module: default casts bf16 to fp16 as the reference does; native_bf16
+    keeps bf16; both within the bar of the oracle."""
+    N, K, gs = 2048, 4096, 128
+    g0 = torch.Generator().manual_seed(17)
+    w = (torch.randn(N, K, generator=g0) * 0.02).numpy().astype(np.float32)
+    packed, s, z, g_idx = O.rtn_quantize_act_order(w, np.random.default_rng(3).permutation(K), gs)
+    perm = P.perm_from_g_idx(torch.from_numpy(g_idx).to(DEV), gs)
+    wk = P.repack_int4_for_kernel(torch.from_numpy(packed).to(DEV), gs, perm=perm)
+    x = torch.randn(2, K, generator=g0).bfloat16()
+    y = P.matmul_w4a16_bf16(x.to(DEV), wk, torch.from_numpy(s).to(DEV),
+                            P.zeros_to_u8(torch.from_numpy(z).to(DEV)), gs, perm=perm)
+    w_hat = O.dequantize_gidx(O.unpack_int4(packed), s, z, g_idx)
+    ref = O.linear_fp32(x.float().numpy(), w_hat)
+    err = np.abs(y.float().cpu().numpy() - ref)
+    assert (err <= 1e-2 + 1e-2 * np.abs(ref)).all(), f"act_order bf16 max_abs={err.max():.4e}"
+
+    lin = torch.nn.Linear(1024, 512, bias=True).to(torch.bfloat16)
+    ql = P.QuantizedLinear.from_linear(lin.to(DEV), P.QuantConfig(bits=4, group_size=gs))
+    ql.use_kernel = True
+    xb = torch.randn(3, 5, 1024, generator=g0).bfloat16().to(DEV)
+    assert ql.native_bf16 is False
+    y16 = ql(xb)
+    ql.native_bf16 = True
+    ynat = ql(xb)
+    assert y16.dtype == ynat.dtype == torch.bfloat16 and ynat.shape == (3, 5, 512)
+    ref = xb.float() @ ql.dequantize(torch.float32).T + ql.bias.float()
+    for yy in (y16, ynat):
+        assert torch.allclose(yy.float(), ref, rtol=2e-2, atol=2e-2)
