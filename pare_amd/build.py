@@ -1,6 +1,8 @@
 """Builds libpare_amd.so in-tree with hipcc for gfx950.
 
-Usage: ``python -m pare_amd.build`` (or ``pare_amd.build.build()``).
+Usage: ``python -m pare_amd.build`` (or ``pare_amd.build.build()``);
+``python -m pare_amd.build sanitized`` builds the host-sanitized C ABI for
+CPU tests (``build_sanitized()``).
 The library is written next to this file so it travels with the source tree.
 """
 
@@ -88,5 +90,51 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     return LIB_PATH
 
 
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer for the C ABI's
+# argument validation (capi.hip): every -fsanitize goes to the host pass only
+# (-Xarch_host), the device code is built exactly as in build().
+SANITIZE_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+SANITIZED_DIR = REPO_DIR / "_build" / "sanitized"
+
+
+def asan_runtime() -> Path:
+    """The clang AddressSanitizer runtime of the ROCm toolchain (to LD_PRELOAD
+    into an uninstrumented python that loads the sanitized library)."""
+    for cand in sorted(Path("/opt/rocm/llvm/lib/clang").glob("*/lib/linux/libclang_rt.asan-x86_64.so")):
+        return cand
+    raise RuntimeError("libclang_rt.asan-x86_64.so not found under /opt/rocm/llvm/lib/clang")
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    """Builds ``_build/sanitized/libpare_amd.so``: capi.hip (the C ABI and its
+    host-side validation) with ASan and UBSan in the host pass, linked with the
+    other sources' objects from build() (compiled first if missing). For CPU
+    tests of the C ABI; the GPU box never loads it."""
+    hipcc = _hipcc()
+    obj_dir = REPO_DIR / "_build"
+    SANITIZED_DIR.mkdir(parents=True, exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    inc = f"-I{REPO_DIR / 'include'}"
+    objs = []
+    for src in SOURCES:
+        if src == "capi.hip":
+            obj = SANITIZED_DIR / "capi.o"
+            _run([hipcc, *flags, *SANITIZE_FLAGS, inc, "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        else:
+            obj = obj_dir / (Path(src).stem + ".o")
+            if not obj.exists():
+                obj_dir.mkdir(exist_ok=True)
+                _run([hipcc, *flags, inc, "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        objs.append(str(obj))
+    out = SANITIZED_DIR / LIB_NAME
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+          "-Xarch_host", "-fsanitize=undefined", *objs, "-o", str(out)], verbose)
+    return out
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if len(sys.argv) > 1 and sys.argv[1] == "sanitized":
+        print(build_sanitized(verbose=True))
+    else:
+        print(build(verbose=True))
