@@ -431,14 +431,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only",
                     choices=["gate_up_m1", "gate_m64", "gate", "sweep", "narrow", "read_floor", "copy",
-                             "e2e_bs1", "e2e_bs4"],
+                             "e2e_bs1", "e2e_bs4", "prefill"],
                     default=None,
                     help="run only one kernel loop (for rocprofv3 counter passes): gate_up_m1 "
                          "the fused gate/up GEMV; gate the gate_proj launches at --m rows "
                          "(gate_m64: --m 64); narrow the tiled GEMM on k/v at 16 rows (K split), "
                          "q/o at 64 and k/v at 128 rows (16-row activation blocks); read_floor "
                          "the plain read of the gate/up weights; "
-                         "e2e_bs1 / e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens")
+                         "e2e_bs1 / e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens; "
+                         "prefill: the reference's 4096x4096 layer at M = 2048 (the big-tile GEMM), "
+                         "8 weight copies, graph replays")
     ap.add_argument("--m", type=int, default=64, help="activation rows of --kernel-only gate")
     ap.add_argument("--graph", action="store_true",
                     help="--kernel-only gate_up_m1 / gate / gate_m64 / read_floor: capture one pass "
@@ -470,6 +472,38 @@ def main():
         model = QuantizedDecoder(DecoderConfig(), dev, seed=0)
         r = decoder_throughput(model, batch=batch, prompt_len=512, n_generate=32)
         log(f"{args.kernel_only}: {r['decode_ms_per_step']} ms/step decode")
+        return
+
+    if args.kernel_only == "prefill":
+        # the reference harness's "BS=16" shape (x [16, 128, 4096]): 4096x4096
+        # INT4 g128 at M = 2048 over 8 weight copies, as a module runs it (the
+        # tiled copy built on its first forward), graph-captured and replayed
+        # (--graph is implied), timed with events on the launch stream
+        import torch.nn as nn
+
+        mods = []
+        for c in range(8):
+            lin = nn.Linear(4096, 4096, bias=False)
+            nn.init.normal_(lin.weight, std=0.02, generator=torch.Generator().manual_seed(c))
+            ql = P.QuantizedLinear.from_linear(lin.to(dev), P.QuantConfig(bits=4, group_size=GS))
+            ql.use_kernel = True
+            mods.append(ql)
+        x = torch.randn(2048, 4096, generator=torch.Generator(device=dev).manual_seed(1), device=dev).half()
+        with torch.cuda.stream(stream):
+            for m in mods:
+                m(x)
+        torch.cuda.synchronize()
+        gp = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gp, stream=stream):
+            for _ in range(2):
+                for m in mods:
+                    m(x)
+        gp.replay()
+        us = time_graph(gp, args.steps, stream) * 1e3 / 16
+        log(f"prefill (M=2048, 4096x4096): kernel "
+            f"{P.kernel_choice(2048, 4096, 4096, GS, tiled=mods[0]._packed_weight_tiled is not None)}, "
+            f"{us:.3f} us per launch over {args.steps} timed replays of 16 launches, "
+            f"{2 * 2048 * 4096 * 4096 / (us * 1e-6) / 1e12:.1f} TFLOP/s")
         return
 
     if args.kernel_only == "copy":
