@@ -506,6 +506,9 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
       const int c = (int)threadIdx.x + i * (int)blockDim.x;
       xst[i] = c < n_xch ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
     }
+    // issued ahead of the weight batches: a staging load scheduled after them
+    // would make its LDS write wait for every batch in flight
+    __builtin_amdgcn_sched_barrier(0);
   }
   // XM 5: the producing launch's partials of sum(h^2), lane l holding
   // l, l + 64, ... (the host checks 1 <= n_stats <= 64 kSt). The loads are
@@ -715,19 +718,28 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     stage_x();
     setup_x();
     // Steady state, unrolled by D so every ring slot is a fixed register set.
-    // Each step issues its load unconditionally (past the last batch it
-    // re-reads the last row), so the wait before a reduction is always for
-    // exactly the D - 1 younger batches.
-    for (int i = 0; i < n_batches; i += D) {
+    // Step b issues the loads of batch b + D - 1 unconditionally (past the
+    // last batch it re-reads the last row), so the wait before a reduction is
+    // always for exactly the D - 1 younger batches. Whole rounds of D steps
+    // first, with no exit inside a round: an exit path into the loop head made
+    // the compiler wait for all but one batch at the first step of every
+    // round. The last n_batches % D steps only reduce: every batch they would
+    // load lies past the end.
+    const int n_full = n_batches - n_batches % D;
+    int i = 0;
+    for (; i < n_full; i += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        if (i + d >= n_batches) break;
         load_batch<U, SPW, ZU8>(ring[(d + D - 1) % D], rs, my_row0 + (i + d + D - 1) * stride,
                                 row_last, row_bytes, G, boff, grp);
         __builtin_amdgcn_sched_barrier(0);
         finish(ring[d], i + d);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (i + d < n_batches) finish(ring[d], i + d);
   }
   if (slice_waves == 1) return;
   __syncthreads();
