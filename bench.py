@@ -758,6 +758,28 @@ def main():
         del gs_
     detail["gate_sweep"] = sweep
 
+    # --- native bf16 activations at 16 rows on gate_proj (the tiled GEMM's
+    # bf16 variant; the extension, not the reference's fp16 cast) ------------
+    xb16 = torch.randn(16, 4096, generator=g, device=dev).to(torch.bfloat16)
+    yb16 = torch.empty(16, 14336, dtype=torch.bfloat16, device=dev)
+
+    def gate_bf16(s):
+        for i in range(copies):
+            b = single[i % n_layers][4 + (i // n_layers) % 2]
+            s_gm, z_gm = b.gm()
+            rc = L.pmi_matmul_w4a16(xb16.data_ptr(), _lib.PMI_BF16, b.w.data_ptr(), b.s.data_ptr(),
+                                    b.z.data_ptr(), _lib.PMI_U8, None, s_gm.data_ptr(), z_gm.data_ptr(),
+                                    b.tiled().data_ptr(), yb16.data_ptr(), _lib.PMI_BF16, 16, b.N, b.K, GS,
+                                    WORKSPACE[0].data_ptr(), WORKSPACE[0].numel(), s)
+            assert rc == 0, _lib.last_error()
+    gbm = capture(gate_bf16, stream)
+    gbm.replay()
+    b16_us = time_graph(gbm, 5, stream) * 1e3 / copies
+    detail["gate_m16_bf16"] = {"us": round(b16_us, 2), "f16_us": sweep[16]["us"],
+                               "kernel": "tgemm (bf16)"}
+    log(f"  gate M=16 bf16: {b16_us:.2f} us (fp16 {sweep[16]['us']} us)")
+    del gbm
+
     # --- achievable peaks and the reference's own per-layer shapes ----------
     detail["measured_peaks"] = measured_peaks(L, dev, stream, [f[2] for f in fused])
     log(f"  measured peaks: {detail['measured_peaks']}")

@@ -148,8 +148,10 @@ PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N,
  * x_dtype and y_dtype: both PMI_F16, or both PMI_BF16 (native bf16
  * activations: an extension with no reference counterpart, where the
  * reference casts bf16 activations to fp16, pare/layers/linear.py:154-156;
- * it runs on the GEMV, four activation rows per launch, y rounded to bf16,
- * and with perm it needs the workspace for the gather of X[:, perm]);
+ * y rounded to bf16; with w_tiled and no perm, the rows an fp16 call would
+ * run on the tiled GEMM's 16-row blocks take its bf16 variant (one K range,
+ * group_size % 128 == 0), the rest run on the GEMV, four activation rows per
+ * launch, and with perm it needs the workspace for the gather of X[:, perm]);
  * zeros: PMI_F32 or PMI_U8 [N,G]; perm (nullable, int32 [K]): act_order
  * gather, X is read as X[:, perm[j]] for weight column j (w must then be
  * repacked with the same perm); y: fp16 [M,N].

@@ -552,12 +552,24 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   const int zu8 = zero_dtype == PMI_U8;
   const int forced = g_kernel_override.load();
   if (bf) {
-    // bf16 activations (the native bf16 extension) run on the GEMV, four
-    // activation rows per launch; act_order rows are gathered into the
-    // workspace first (2-byte elements, as for fp16)
-    if (forced && forced != 1)
-      return fail(PMI_ERR_UNSUPPORTED, "%s: bf16 activations run on the GEMV only (kernel %d forced)",
-                  fn, forced);
+    // bf16 activations (the native bf16 extension): with the tiled copy, the
+    // rows an fp16 call would run on the tiled GEMM's 16-row blocks (no
+    // act_order) take its bf16 variant; the rest run on the GEMV, four
+    // activation rows per launch, act_order rows gathered into the workspace
+    // first (2-byte elements, as for fp16)
+    if (forced && forced != 1 && forced != 5)
+      return fail(PMI_ERR_UNSUPPORTED, "%s: bf16 activations run on the GEMV or the tiled GEMM only "
+                  "(kernel %d forced)", fn, forced);
+    const bool bf_tiled = w_tiled && scales_gm && zeros_gm && N % 4 == 0 && !perm && aligned(y, 8) &&
+                          pmi::tgemm_bf16_supported(M, N, K, group_size);
+    if (forced == 5 && !bf_tiled)
+      return fail(PMI_ERR_UNSUPPORTED, "%s: the tiled GEMM's bf16 variant needs w_tiled, scales_gm and "
+                  "zeros_gm, no perm, y 8-byte aligned, group_size %% 128 == 0 and 16-row blocks", fn);
+    if (bf_tiled && (forced == 5 || (!forced && pmi_matmul_kernel_choice(M, N, K, group_size,
+                                                                         PMI_CHOICE_TILED) == 5)))
+      return from_hip(pmi::launch_tgemm(x, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N, K, group_size,
+                                        nullptr, 0, 0, s, true),
+                      fn);
     const uint16_t* xp = (const uint16_t*)x;
     if (perm) {
       if (workspace_bytes < pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K))

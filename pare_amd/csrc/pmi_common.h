@@ -167,6 +167,17 @@ PMI_DEV f16x8 b_operand(uint32_t t0, uint32_t t1, f16x2 nz) {
   return __builtin_bit_cast(f16x8, r);
 }
 
+// The same 8 nibbles as bf16 128 + q, exact: v_perm_b32 under a 0x43 byte
+// (bf16 has no packed subtract on gfx950; the zero point is taken off by a
+// separate MFMA whose operand is -(128 + z)).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+PMI_DEV bf16x8 b_operand_bf16(uint32_t t0, uint32_t t1) {
+  const uint32_t K = 0x43434343u;
+  const u32x4 r = {__builtin_amdgcn_perm(K, t0, 0x04010400u), __builtin_amdgcn_perm(K, t0, 0x04030402u),
+                   __builtin_amdgcn_perm(K, t1, 0x04010400u), __builtin_amdgcn_perm(K, t1, 0x04030402u)};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 // (scale, zero) of an INT4 group from its min and max, qmin = 0, qmax = 15.
 // sym 0: asymmetric (pare/core/scale.py:83-91); 1: the reference's symmetric
 // rule on the unsigned grid (scale.py:73-82: zero 0, so negative weights clamp

@@ -197,13 +197,23 @@ __device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int s
 // than one 64-row panel per CU), the last ones clamped and not stored.
 // SPLIT: a K range of a split weight workgroup (a.splits > 1); a variant of its
 // own, so that unsplit launches carry none of its index arithmetic.
-template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false, bool NORM = false>
+// BF: bf16 activations and output (the native bf16 extension), up to 16 rows
+// per activation block, one K range, gs % 128 == 0. gfx950 has no packed bf16
+// subtract, so B is the bf16 128 + q, exact (v_perm_b32 under a 0x43 byte),
+// and each k-step adds a second MFMA whose B operand is -(128 + z) in every
+// element: its products x (-(128 + z)) are exact in fp32, so the group's sum
+// is sum x (q - z) up to the fp32 rounding of the accumulation; the fold and
+// the combine are those of fp16, and y is rounded to bf16 (nearest even).
+template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false, bool NORM = false,
+          bool BF = false>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
   static_assert(!NORM || (MT == 1 && GPU == 1 && !GATHER && !RNG && !SPLIT),
                 "the fused norm is built for up to 4 rows, gs % 128 == 0, one K range");
   static_assert(!RNG || (MT == 1 && GPU == 1), "tile ranges are built for up to 16 rows, gs >= 128");
   static_assert(!SPLIT || (MT == 1 && !RNG), "the K split is built for up to 16 rows");
+  static_assert(!BF || (MT == 1 && GPU == 1 && !GATHER && !RNG && !SPLIT && !NORM),
+                "bf16 activations are built for 16-row blocks, gs % 128 == 0, one K range");
   using UnitT = Unit<MT, NTW, GPU, RNG>;
   constexpr bool RING = MT > 1;
   // MT = 4: the ring holds half units (64 columns, k-steps 0-1 or 2-3), two
@@ -472,11 +482,24 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
           const uint32_t w0 = un.w[j][2 * half], w1 = un.w[j][2 * half + 1];
           const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
           const uint32_t t1 = (run ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
-          const f16x8 B = b_operand(t0, t1, nz);
+          if constexpr (BF) {
+            const bf16x8 Bq = b_operand_bf16(t0, t1);
+            const uint32_t nzb = (0xC300u | zq) * 0x00010001u;  // bf16 -(128 + z), twice
+            const bf16x8 Bz = __builtin_bit_cast(bf16x8, u32x4{nzb, nzb, nzb, nzb});
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B, t % TPG == 0 ? zero4 : cg[mt][j],
-                                                               0, 0, 0);
+            for (int mt = 0; mt < MT; ++mt) {
+              const bf16x8 Ab = __builtin_bit_cast(bf16x8, A[mt]);
+              cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ab, Bq, t % TPG == 0 ? zero4 : cg[mt][j], 0,
+                                                                  0, 0);
+              cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ab, Bz, cg[mt][j], 0, 0, 0);
+            }
+          } else {
+            const f16x8 B = b_operand(t0, t1, nz);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              cg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mt], B, t % TPG == 0 ? zero4 : cg[mt][j],
+                                                                 0, 0, 0);
+          }
         }
         if (t % TPG == TPG - 1) {
 #pragma unroll
@@ -693,7 +716,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       }
       uint16_t v[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < NTW && j < 4; ++j) v[j] = __builtin_bit_cast(uint16_t, f32_to_f16_rne(sum[j][i]));
+      for (int j = 0; j < NTW && j < 4; ++j)
+        v[j] = BF ? f32_to_bf16_rne(sum[j][i]) : __builtin_bit_cast(uint16_t, f32_to_f16_rne(sum[j][i]));
       if constexpr (NTW == 4) {
         if (a.glu) {
           // columns 32 p + 2 n and + 1 of the activation, each formed as
@@ -906,6 +930,14 @@ TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gathe
   return c;
 }
 
+// The bf16 variant: the configuration the fp16 call would take, when it is
+// one unsplit K range of 16-row blocks without tile ranges.
+bool tgemm_bf16_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
+  if (!tgemm_supported(M, N, K, gs) || gs % 128 != 0) return false;
+  const TgemmConfig c = tgemm_config(M, N, K, gs, false);
+  return c.mt == 1 && !c.rng;
+}
+
 bool tgemm_gather_supported(int64_t M, int64_t K) {
   return M >= 1 && M <= 16 && K <= 4 * 64 * kXGPermIt * 4 && M * (2 * K + 16) + 4 * K <= kXGLds;
 }
@@ -913,9 +945,15 @@ bool tgemm_gather_supported(int64_t M, int64_t K) {
 hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
                         const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
                         int64_t N, int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
-                        size_t part_offset, hipStream_t stream) {
+                        size_t part_offset, hipStream_t stream, bool bf16) {
   if (perm && !tgemm_gather_supported(M, K)) return hipErrorInvalidValue;
+  if (bf16 && (perm || !tgemm_bf16_supported(M, N, K, gs))) return hipErrorInvalidValue;
   TgemmConfig c = tgemm_config(M, N, K, gs, perm != nullptr);
+  if (bf16) {
+    // one K range (no workspace): a split configuration runs unsplit
+    c.splits = 1;
+    c.grid = c.grid_m == 1 ? c.n_wg : (int)((c.n_wg + 7) / 8 * 8 * c.grid_m);
+  }
   if (c.splits > 1 && (!workspace || ws_bytes < part_offset + c.ws_split)) {
     c.splits = 1;
     c.grid = c.n_wg;
@@ -938,6 +976,17 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   a.counters = (int*)workspace;
   a.part = c.splits > 1 ? (float*)((uint8_t*)workspace + part_offset) : nullptr;
   a.glu = 0;
+  if (bf16) {
+    const dim3 block(kKW * 64);
+#define PMI_TG_BF(NTW_)                                                                               \
+  hipLaunchKernelGGL((w4a16_tgemm_kernel<1, NTW_, 1, false, false, false, false, true>), dim3(c.grid), \
+                     block, 0, stream, a)
+    if (c.ntw == 4) PMI_TG_BF(4);
+    else if (c.ntw == 2) PMI_TG_BF(2);
+    else PMI_TG_BF(1);
+#undef PMI_TG_BF
+    return hipGetLastError();
+  }
   if (c.mt == 1) return launch_mt<1>(c, a, stream);
   if (c.mt == 2) return launch_mt<2>(c, a, stream);
   return launch_mt<4>(c, a, stream);

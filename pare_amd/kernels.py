@@ -156,6 +156,8 @@ def matmul_w4a16_bf16(
     group_size: int,
     *,
     perm: torch.Tensor | None = None,
+    sz_gm: tuple[torch.Tensor, torch.Tensor] | None = None,
+    w_tiled: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Y[M,N] = X[M,K] @ dequant(W)^T with bf16 X and Y (native bf16 activations).
@@ -163,13 +165,15 @@ def matmul_w4a16_bf16(
     An extension without a reference counterpart: the reference casts bf16
     activations to fp16 before its kernel (pare/layers/linear.py:154-156),
     which ``matmul_w4a16`` keeps. Here the bf16 values are used as they are
-    (fp32 accumulation, y rounded to bf16), on the GEMV, four activation rows
-    per launch. Other arguments as for ``matmul_w4a16``."""
+    (fp32 accumulation, y rounded to bf16): with ``w_tiled`` and ``sz_gm`` and
+    no ``perm``, the row counts an fp16 call runs on the tiled GEMM's 16-row
+    blocks take its bf16 variant; the rest run on the GEMV, four activation
+    rows per launch. Other arguments as for ``matmul_w4a16``."""
     if not x.is_cuda:
         raise RuntimeError("matmul_w4a16_bf16 requires HIP (cuda) tensors.")
     assert x.is_contiguous(), "x must be contiguous"
     assert x.dtype == torch.bfloat16, f"x must be bfloat16, got {x.dtype}"
-    return _matmul(x, packed_weight, scales, zeros, group_size, perm, None, None, out)
+    return _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out)
 
 
 def _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out):

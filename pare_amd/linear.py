@@ -176,8 +176,10 @@ class QuantizedLinear(nn.Module):
         w_k, zero_u8, perm, sz_gm = self._kernel_buffers()
         orig_shape = x.shape
         if x.dtype == torch.bfloat16 and getattr(self, "native_bf16", False):
-            y = matmul_w4a16_bf16(x.reshape(-1, self.in_features).contiguous(), w_k, self.scale,
-                                  zero_u8, self._group_size(), perm=perm)
+            xb = x.reshape(-1, self.in_features).contiguous()
+            w_t = None if perm is not None else self._tiled_buffer(w_k, xb.shape[0])
+            y = matmul_w4a16_bf16(xb, w_k, self.scale, zero_u8, self._group_size(), perm=perm,
+                                  sz_gm=sz_gm, w_tiled=w_t)
             if self.bias is not None:
                 y = y + self.bias
             return y.reshape(*orig_shape[:-1], self.out_features)

@@ -804,3 +804,84 @@ def test_bf16_act_order_and_module_flag():
     ref = xb.float() @ ql.dequantize(torch.float32).T + ql.bias.float()
     for yy in (y16, ynat):
         assert torch.allclose(yy.float(), ref, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,M", [(4096, 4096, 2), (4096, 4096, 16), (14336, 4096, 4),
+                                   (14336, 4096, 16), (1024, 4096, 8), (4096, 14336, 16),
+                                   (1024, 4096, 64), (6144, 4096, 5)])
+def test_bf16_tiled_gemm_against_oracle(N, K, M):
+    """The tiled GEMM's bf16 variant (16-row blocks, one K range; forced), with
+    the same bar as the GEMV's: the fp32-accumulated oracle at rtol = atol =
+    1e-2, and the bf16 oracle plus its own weight-rounding bound. Two launches
+    are bit-identical, and the automatic dispatch picks the same kernel where
+    an fp16 call would run on the tiled GEMM."""
+    gs = 128
+    g = torch.Generator().manual_seed(N + 3 * K + M)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    packed, s, z = O.rtn_quantize(w, gs)
+    wk = P.repack_int4_for_kernel(torch.from_numpy(packed).to(DEV), gs)
+    sd, zd = torch.from_numpy(s).to(DEV), P.zeros_to_u8(torch.from_numpy(z).to(DEV))
+    sz = P.sz_group_major(sd, zd)
+    wt = P.tile_w4a16(wk, gs)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    xd = x.to(DEV)
+    with force_kernel("tgemm"):
+        y = P.matmul_w4a16_bf16(xd, wk, sd, zd, gs, sz_gm=sz, w_tiled=wt)
+        y2 = P.matmul_w4a16_bf16(xd, wk, sd, zd, gs, sz_gm=sz, w_tiled=wt)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (M, N)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    w_hat = O.dequantize_packed(packed, s, z)
+    got = y.float().cpu().numpy()
+    xf = x.float().numpy()
+    round_bound = (np.abs(xf) @ np.abs(w_hat).T) * 2.0 ** -9
+    for ref, extra, what in ((O.linear_fp32(xf, w_hat), 0.0, "fp32"),
+                             (_bf16_ref(x, w_hat), round_bound, "bf16 oracle")):
+        err = np.abs(got - ref)
+        print(f"[parity] bf16 tiled M={M} N={N} K={K} vs {what}: max_abs={err.max():.3e}", flush=True)
+        assert (err <= 1e-2 + 1e-2 * np.abs(ref) + extra).all(), f"{what}: max_abs={err.max():.4e}"
+    if P.kernel_choice(M, N, K, gs, tiled=True) == "tgemm":
+        ya = P.matmul_w4a16_bf16(xd, wk, sd, zd, gs, sz_gm=sz, w_tiled=wt)
+        assert torch.equal(ya.view(torch.int16), y.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_bf16_tiled_gemm_one_hot_rows_and_unsupported_forcing():
+    """One-hot rows through the tiled bf16 variant give the reference
+    dequantisation cast to bf16, bit for bit (the -(128 + z) correction MFMA
+    is exact); forcing it with a permutation raises."""
+    N, K, gs = 256, 2048, 128
+    g = torch.Generator().manual_seed(9)
+    w = (torch.randn(N, K, generator=g) * 0.02).numpy()
+    packed, s, z = O.rtn_quantize(w, gs)
+    wk = P.repack_int4_for_kernel(torch.from_numpy(packed).to(DEV), gs)
+    sd, zd = torch.from_numpy(s).to(DEV), P.zeros_to_u8(torch.from_numpy(z).to(DEV))
+    sz = P.sz_group_major(sd, zd)
+    wt = P.tile_w4a16(wk, gs)
+    cols = [0, 1, 31, 32, 63, 64, 127, 128, 1000, 2047]
+    x = torch.zeros(len(cols), K, dtype=torch.bfloat16)
+    x[torch.arange(len(cols)), torch.tensor(cols)] = 1.0
+    with force_kernel("tgemm"):
+        y = P.matmul_w4a16_bf16(x.to(DEV), wk, sd, zd, gs, sz_gm=sz, w_tiled=wt)
+    ref = torch.from_numpy(O.dequantize_packed(packed, s, z)[:, cols].T.copy()).bfloat16()
+    assert torch.equal(y.cpu().view(torch.int16), ref.view(torch.int16))
+    perm = torch.arange(K, dtype=torch.int32, device=DEV)
+    with force_kernel("tgemm"), pytest.raises(RuntimeError, match="bf16 variant"):
+        P.matmul_w4a16_bf16(x.to(DEV), wk, sd, zd, gs, perm=perm, sz_gm=sz, w_tiled=wt)
+
+
+@pytest.mark.gpu
+def test_bf16_module_builds_the_tiled_copy():
+    """A native-bf16 module at 8 rows builds its tiled copy and runs the bf16
+    variant; the result equals the functional call with the same buffers."""
+    lin = torch.nn.Linear(4096, 4096, bias=False)
+    ql = P.QuantizedLinear.from_linear(lin.to(DEV), P.QuantConfig(bits=4, group_size=128))
+    ql.use_kernel = True
+    ql.native_bf16 = True
+    x = torch.randn(8, 4096, generator=torch.Generator().manual_seed(2)).bfloat16().to(DEV)
+    y = ql(x)
+    assert ql._packed_weight_tiled is not None
+    w_k, zero_u8, perm, sz_gm = ql._kernel_buffers()
+    ref = P.matmul_w4a16_bf16(x, w_k, ql.scale, zero_u8, 128, sz_gm=sz_gm,
+                              w_tiled=ql._packed_weight_tiled)
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
