@@ -370,8 +370,58 @@ def test_c5_full_decoder_prefill_matches_dequant_path(full_decoder):
     agree = (a.argmax(-1) == b.argmax(-1)).float().mean().item()
     print(f"[baseline] C5 32-layer prefill kernel vs dequant path: max_abs={err:.3e} "
           f"(max |logit| {scale:.3e}), argmax agreement {agree:.3f}", flush=True)
-    assert err <= 1e-2 + 2e-2 * scale
-    assert agree >= 0.9
+    # measured 6.1e-2 against max |logit| 7.0 (seeded, deterministic)
+    assert err <= 1e-2 + 1e-2 * scale
+    assert agree >= 0.95
+
+
+def _teacher_forced_logits(model, prompt, cont):
+    """Prefill `prompt`, then decode the tokens of `cont` one step at a time
+    (teacher forcing, so both paths see the same inputs at every step);
+    returns the fp32 logits of every decode step [B, T, vocab]."""
+    B, P = prompt.shape
+    T = cont.shape[1]
+    L = P + T
+    cos, sin = model.rope_tables(L)
+    cache = model.new_cache(B, L)
+    ar = torch.arange(L, device=DEV)
+    model.forward_tokens(prompt, cos, sin, cache, torch.arange(P, device=DEV), None, True, True)
+    out = []
+    for t in range(T):
+        p = torch.full((1,), P + t, dtype=torch.long, device=DEV)
+        out.append(model.forward_tokens(cont[:, t:t + 1].contiguous(), cos, sin, cache, p, ar <= p,
+                                        False)[:, -1].float())
+    return torch.stack(out, 1)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_c5_full_decoder_fused_decode_matches_torch_ops(full_decoder, batch):
+    """The full-size decode path against the same 32-layer model on plain
+    PyTorch ops (fused_ops=False: torch RMSNorm, RoPE, SDPA attention, SiLU and
+    residual adds around the same INT4 linears). At batch 1 the fused path is
+    the five-launch layer (prenormed q/k/v and gate/up GEMVs, residual o and
+    down epilogues, split attention with fused RoPE); at batch 4 the tiled
+    GEMM's norm prologue and SiLU epilogue. Teacher-forced logits of 12 decode
+    steps after a 40-token prompt."""
+    model = full_decoder
+    g = torch.Generator(device=DEV).manual_seed(30 + batch)
+    prompt = torch.randint(0, model.cfg.vocab, (batch, 40), generator=g, device=DEV)
+    cont = torch.randint(0, model.cfg.vocab, (batch, 12), generator=g, device=DEV)
+    with torch.no_grad():
+        a = _teacher_forced_logits(model, prompt, cont)
+        model.fused_ops = False
+        try:
+            b = _teacher_forced_logits(model, prompt, cont)
+        finally:
+            model.fused_ops = True
+    err = (a - b).abs().max().item()
+    scale = b.abs().max().item()
+    agree = (a.argmax(-1) == b.argmax(-1)).float().mean().item()
+    print(f"[baseline] C5 batch={batch} fused decode vs torch ops: max_abs={err:.3e} "
+          f"(max |logit| {scale:.3e}), argmax agreement {agree:.3f}", flush=True)
+    # measured 3.9e-2 / 4.5e-2 against max |logit| 6.2 / 6.5 at batch 1 / 4
+    assert err <= 1e-2 + 1e-2 * scale
+    assert agree >= 0.95
 
 
 @pytest.mark.parametrize("batch", [1, 4])
