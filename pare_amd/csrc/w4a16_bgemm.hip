@@ -24,9 +24,11 @@
 //
 // Operands. Each unit's activation rows (128 x 256 bytes), the band's four
 // 4 KiB weight blocks and its scales and zero points go global -> registers
-// -> LDS, double-buffered: every wave loads one eighth of unit s + 2 into
-// registers while it computes unit s, and writes unit s + 1 to the other LDS
-// slot after computing s; one barrier per unit. In a slot, the 16-byte chunk
+// -> LDS, double-buffered in LDS: every wave writes its eighth of unit s + 1 to
+// the other slot after computing unit s, then loads the codes of unit s + 2
+// and the activations of unit s + 3 (two register stages for the
+// activations, whose loads otherwise stalled the slot writes; 79 against 81
+// us at 4096 x 4096, M = 2048); one barrier per unit. In a slot, the 16-byte chunk
 // c of activation row r sits at chunk c ^ (r % 16), so the 16 rows an
 // A-operand read touches at one column fall in 16 different bank groups.
 //
@@ -110,15 +112,26 @@ __global__ __launch_bounds__(kBWaves * 64, 1) void w4a16_bgemm_kernel(BgemmArgs 
     vwp[i] = (band * 4 + pc / 4) * U * 4096 + (pc % 4) * 1024 + 16 * l;
   }
   const int vsz = wv == 0 ? (256 * band + 4 * l) * 4 : 256 * band + 4 * l;
-  struct Stage {
-    u32x4 x[4], w[2], sz;
+  // The activation rows are staged two units ahead, in two register stages;
+  // the codes, scales and zero points one unit ahead.
+  struct XStage {
+    u32x4 x[4];
   };
-  auto stage_load = [&](Stage& st, int u) {
+  struct WStage {
+    u32x4 w[2], sz;
+  };
+  auto clamp_unit = [&](int u) {
     u = u < U ? u : U - 1;  // past K: re-read the last unit (never used)
-    const int uu = __builtin_amdgcn_readfirstlane(u);
+    return __builtin_amdgcn_readfirstlane(u);
+  };
+  auto load_x = [&](XStage& st, int u) {
+    const int uu = clamp_unit(u);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       st.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, vx[i], uu * 256, 0));
+  };
+  auto load_w = [&](WStage& st, int u) {
+    const int uu = clamp_unit(u);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       st.w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vwp[i], uu * 4096, 0));
@@ -128,13 +141,13 @@ __global__ __launch_bounds__(kBWaves * 64, 1) void w4a16_bgemm_kernel(BgemmArgs 
     else if (wv == 1)
       st.sz = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rz, vsz, g * N, 0), 0u, 0u, 0u};
   };
-  auto stage_write = [&](const Stage& st, uint8_t* base) {
+  auto stage_write = [&](const XStage& xs, const WStage& ws, uint8_t* base) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + (4 * wv + i) * 1024 + 16 * l) = st.x[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + (4 * wv + i) * 1024 + 16 * l) = xs.x[i];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(base + kBWo + (2 * wv + i) * 1024 + 16 * l) = st.w[i];
-    if (wv == 0) *reinterpret_cast<u32x4*>(base + kBSo + 16 * l) = st.sz;
-    else if (wv == 1) *reinterpret_cast<uint32_t*>(base + kBZo + 4 * l) = st.sz[0];
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(base + kBWo + (2 * wv + i) * 1024 + 16 * l) = ws.w[i];
+    if (wv == 0) *reinterpret_cast<u32x4*>(base + kBSo + 16 * l) = ws.sz;
+    else if (wv == 1) *reinterpret_cast<uint32_t*>(base + kBZo + 4 * l) = ws.sz[0];
   };
 
   // ---- compute: tiles 2 jh, 2 jh + 1 of panel pw, all 128 activation rows
@@ -163,20 +176,23 @@ __global__ __launch_bounds__(kBWaves * 64, 1) void w4a16_bgemm_kernel(BgemmArgs 
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int run = t >> 1, half = t & 1;
-      f16x8 A[kBMT];
-#pragma unroll
-      for (int i = 0; i < kBMT; ++i)
-        A[i] = *reinterpret_cast<const f16x8*>(base + (16 * i + ln) * 256 + (((4 * t + h) ^ ln) << 4));
+      // the step's two B operands, then each activation tile read once for both
+      f16x8 B[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const uint32_t w0 = w[j][2 * half], w1 = w[j][2 * half + 1];
         const uint32_t t0 = (run ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
         const uint32_t t1 = (run ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
-        const f16x8 B = b_operand(t0, t1, nz[j]);
-#pragma unroll
-        for (int i = 0; i < kBMT; ++i)
-          cg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B, t == 0 ? zero4 : cg[i][j], 0, 0, 0);
+        B[j] = b_operand(t0, t1, nz[j]);
       }
+#pragma unroll
+      for (int i = 0; i < kBMT; ++i) {
+        const f16x8 A = *reinterpret_cast<const f16x8*>(base + (16 * i + ln) * 256 + (((4 * t + h) ^ ln) << 4));
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          cg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], t == 0 ? zero4 : cg[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -186,26 +202,44 @@ __global__ __launch_bounds__(kBWaves * 64, 1) void w4a16_bgemm_kernel(BgemmArgs 
         for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(sc[j], cg[i][j][e], acc[i][j][e]);
   };
 
-  Stage st;
-  stage_load(st, 0);
-  stage_write(st, lds);
-  stage_load(st, 1);
+  // Unit u: activations in xs[u % 2] (loaded during unit u - 2), codes in ws
+  // (loaded during unit u - 1). Issue order within a step is codes, then
+  // activations, so the wait for the codes leaves the younger activations in
+  // flight.
+  XStage xs[2];
+  WStage ws;
+  load_x(xs[0], 0);
+  load_w(ws, 0);
+  stage_write(xs[0], ws, lds);
+  load_x(xs[1], 1);
+  load_w(ws, 1);
+  load_x(xs[0], 2);
   wait_lgkm0();
   barrier_only();
-  for (int s = 0; s < U; ++s) {
-    uint8_t* cur = lds + (s & 1) * kBSlot;
-    compute(cur);
-    if (s + 1 < U) {
-      // unit s + 1 (loaded during unit s) to the other slot, whose unit s - 1
-      // every wave finished before the last barrier; then fetch unit s + 2
-      stage_write(st, lds + ((s + 1) & 1) * kBSlot);
-      stage_load(st, s + 2);
-    }
+  // step s: compute unit s, write unit s + 1 to the other slot (whose unit
+  // s - 1 every wave finished before the last barrier), fetch the codes of
+  // s + 2 and the activations of s + 3
+  auto step = [&](int s, XStage& x1) {
+    compute(lds + (s & 1) * kBSlot);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_write(x1, ws, lds + ((s + 1) & 1) * kBSlot);
+    load_w(ws, s + 2);
+    load_x(x1, s + 3);
     // the slot writes have landed before any wave passes (LDS operations
     // complete in order per wave; the barrier makes them visible)
     wait_lgkm0();
     barrier_only();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // whole pairs of steps with no exit inside, then the last two units (U is
+  // even and at least 12: K % 512 == 0, K >= 1536)
+  int s = 0;
+  for (; s < U - 2; s += 2) {
+    step(s, xs[1]);
+    step(s + 1, xs[0]);
   }
+  step(U - 2, xs[1]);
+  compute(lds + ((U - 1) & 1) * kBSlot);
   if (p >= a.n_panels || row0 >= N) return;
 
   // lane (n, h): activation rows m0 + 16 i + 4 h + e, weight rows row0 + j
