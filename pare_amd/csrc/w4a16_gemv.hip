@@ -228,6 +228,16 @@ struct Rsrc {
   __amdgpu_buffer_rsrc_t w, s, z;
 };
 
+// A launch's geometry as the kernel reads it (GemvConfig plus the quotients
+// and reciprocals the host works out, gemv_geom).
+struct GemvGeom {
+  int n_slices, slice_waves, row_waves, rows_per_wg;
+  int groups;          // K / gs
+  int n_batches;       // ceil(rows_per_wg / (row_waves * U))
+  uint32_t sw_magic;   // ceil(2^16 / slice_waves): wave / slice_waves, wave < 16
+  uint32_t hgs_magic;  // ceil(2^32 / (gs / 2)): b / (gs / 2) for b * (gs / 2) < 2^32
+};
+
 // Raw buffer resource over `bytes` bytes (untyped dword access).
 PMI_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -415,30 +425,39 @@ PMI_DEV void store_y(f16* p, float v) {
 // Epilogue (xf.res, one activation row, slice_waves > 1): y = h = y + res
 // rounded as add_rmsnorm_kernel forms h, and xf.stats[blockIdx.x] = the sum of
 // h^2 over the workgroup's rows (fixed order), for a mode-5 launch to read.
+//
+// The launch geometry comes with the divisions a wave would otherwise do
+// before its first load worked out on the host (an integer division is ~25
+// dependent instructions, and the first weight batch waited for three of
+// them): wave / slice_waves = (wave * sw_magic) >> 16 and a lane's byte
+// offset b / (gs / 2) = umulhi(b, hgs_magic), both exact in the ranges the
+// host checks (gemv_geom).
 template <int MT, int U, int D, int SPW, int XM, bool ZU8, bool RES = false>
 __global__ void __launch_bounds__(kMaxWaves * 64)
 w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                   const float* __restrict__ scales, const void* __restrict__ zeros,
                   const int32_t* __restrict__ perm, f16* __restrict__ y, int N, int K, int gs,
-                  int n_slices, int slice_waves, int row_waves, int rows_per_wg, GemvXform xf) {
+                  GemvGeom gg, GemvXform xf) {
   extern __shared__ float part[];  // [rows_per_wg][slice_waves][MT] when slice_waves > 1
   __shared__ float nrm[XM == 3 ? kMaxWaves * 4 : 1];  // per-wave sums of h^2 (XM 3)
   __shared__ float hred[RES ? kMaxWaves : 1];          // per-wave sums of h^2 (RES)
   constexpr int VP = Pow2Ceil<U * MT>::value;
   constexpr int LOGV = Log2<VP>::value;
 
+  const int n_slices = gg.n_slices, slice_waves = gg.slice_waves;
+  const int row_waves = gg.row_waves, rows_per_wg = gg.rows_per_wg;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ws = wave % slice_waves;
-  const int wr = wave / slice_waves;
+  const int wr = (int)(((uint32_t)wave * gg.sw_magic) >> 16);
+  const int ws = wave - wr * slice_waves;
   const int row_chunks = K >> 5;
   const int hgs = gs >> 1;  // bytes per group tile
-  const int G = K / gs;
+  const int G = gg.groups;
   const int row_bytes = K >> 1;
   const int row0 = blockIdx.x * rows_per_wg;
   const int row_lim = min(N, row0 + rows_per_wg);
   const int stride = row_waves * U;
-  const int n_batches = (rows_per_wg + stride - 1) / stride;
+  const int n_batches = gg.n_batches;
 
   Rsrc rs;
   rs.w = make_rsrc(w, (uint32_t)N * (uint32_t)row_bytes);
@@ -464,7 +483,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     const int chunk = s * kSliceChunks + lane;
     act[sp] = s < n_slices && chunk < row_chunks;
     const int b = act[sp] ? chunk << 4 : 0;
-    const int t = b / hgs;
+    const int t = (int)__umulhi((uint32_t)b, gg.hgs_magic);  // b / hgs
     const int j = b - t * hgs;
     boff[sp] = b;
     grp[sp] = t;
@@ -783,11 +802,33 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   }
 }
 
+// The kernel's geometry for a launch of U rows per batch; false when a
+// quotient would leave the range in which its reciprocal is exact (rows of
+// 2^17 columns or more).
+bool gemv_geom(const GemvConfig& c, int U, int K, int gs, GemvGeom& g) {
+  const uint32_t hgs = (uint32_t)gs / 2u;
+  if (c.slice_waves < 1 || c.slice_waves > kMaxWaves || hgs < 1 ||
+      (uint64_t)(K / 2) * hgs >= (1ull << 32))
+    return false;
+  const int stride = c.row_waves * U;
+  g.n_slices = c.n_slices;
+  g.slice_waves = c.slice_waves;
+  g.row_waves = c.row_waves;
+  g.rows_per_wg = c.rows_per_wg;
+  g.groups = K / gs;
+  g.n_batches = (c.rows_per_wg + stride - 1) / stride;
+  g.sw_magic = (65536u + (uint32_t)c.slice_waves - 1u) / (uint32_t)c.slice_waves;
+  g.hgs_magic = (uint32_t)(((1ull << 32) + hgs - 1) / hgs);
+  return true;
+}
+
 template <int MT, int U, int D, int SPW>
 hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, const float* scales,
                       const void* zeros, int zero_u8, const int32_t* perm, void* y, int N, int K,
                       int gs, const GemvXform& xf, hipStream_t stream) {
   const dim3 block(64 * c.slice_waves * c.row_waves);
+  GemvGeom gg;
+  if (!gemv_geom(c, U, K, gs, gg)) return hipErrorInvalidValue;
   // XM 4 (xf.mode 4): the activation rows staged in LDS after the partials
   const bool perm_lds = perm && xf.mode == 4;
   if (perm_lds && !gemv_perm_lds_fits(MT, K, (int)block.x)) return hipErrorInvalidValue;
@@ -795,8 +836,7 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
                               : (size_t)c.lds_bytes;
 #define PMI_GEMV_LAUNCH(XM, Z)                                                                  \
   hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
-                     (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, c.n_slices,       \
-                     c.slice_waves, c.row_waves, c.rows_per_wg, xf)
+                     (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, gg, xf)
   if (xf.res) {
     // the residual epilogue: one activation row, plain or SiLU(gate) * up
     // activations, u8 zero points, no permutation
@@ -806,11 +846,11 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
       if (xf.mode == 2)
         hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, 2, true, true>), dim3(c.grid), block,
                            lds, stream, (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs,
-                           c.n_slices, c.slice_waves, c.row_waves, c.rows_per_wg, xf);
+                           gg, xf);
       else
         hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, 0, true, true>), dim3(c.grid), block,
                            lds, stream, (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs,
-                           c.n_slices, c.slice_waves, c.row_waves, c.rows_per_wg, xf);
+                           gg, xf);
       return hipGetLastError();
     } else {
       return hipErrorInvalidValue;

@@ -121,11 +121,13 @@ def _gemv_kernels(asm: str) -> dict[tuple, str]:
     keyed by (MT, U, D, SPW, XM, ZU8, mangled name). XM: 0 plain activations,
     1 act_order gather from global memory, 2 silu(gate) * up, 3 residual add +
     RMSNorm, 4 act_order gather from activations staged in LDS, 5 RMSNorm with
-    sum(x^2) from a residual launch's partials."""
+    sum(x^2) from a residual launch's partials. The body runs to the function's
+    end label, not its first s_endpgm: the early return of one-slice launches
+    can be laid out ahead of the streaming loop."""
     out = {}
     pat = r"^(_ZN\S*w4a16_gemv_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d)ELb(\d)E\S*):"
     for m in re.finditer(pat, asm, re.M):
-        end = asm.find("s_endpgm", m.end())
+        end = asm.find(".Lfunc_end", m.end())
         key = tuple(int(m.group(i)) for i in range(2, 8)) + (m.group(1),)
         out[key] = asm[m.end():end]
     return out
