@@ -111,7 +111,34 @@ struct TgemmArgs {
   const f16* nw;
   f16* h_out;
   float eps;
+  // Quotients and reciprocal constants the host works out (derive_args), so
+  // that no wave divides before its first load (an integer division is a
+  // ~25-instruction dependent chain): n / d = umulhi(n, ceil(2^32 / d)) for
+  // d >= 2 and n d < 2^32, and n / d = (n ceil(2^16 / d)) >> 16 for n d < 2^16.
+  int groups;           // K / gs
+  uint32_t upg_magic;   // units per group (gs >= 128: gs / 128, else 1), 16-bit form
+  uint32_t span_magic;  // grid_m > 1: 8 grid_m, 32-bit form
+  uint32_t split_magic; // splits > 1: splits, 32-bit form
 };
+
+// Fills the derived fields of `a`; false when a quotient would leave the range
+// in which its constant is exact.
+inline bool derive_args(TgemmArgs& a) {
+  const uint32_t upg = a.gs >= 128 ? (uint32_t)a.gs / 128u : 1u;
+  const uint64_t units = (uint64_t)a.K / 128u;
+  const uint64_t grid = (uint64_t)(a.n_wg + 8) * (uint64_t)(a.grid_m > 0 ? a.grid_m : 1) *
+                        (uint64_t)(a.splits > 0 ? a.splits : 1);
+  const uint64_t span = 8ull * (uint64_t)(a.grid_m > 0 ? a.grid_m : 1);
+  if (a.gs <= 0 || units * upg >= (1ull << 16) || grid * span >= (1ull << 32) ||
+      grid * (uint64_t)(a.splits > 0 ? a.splits : 1) >= (1ull << 32) ||
+      (units / kKW) * (uint64_t)(a.splits > 0 ? a.splits : 1) >= (1ull << 32))
+    return false;
+  a.groups = a.K / a.gs;
+  a.upg_magic = (65536u + upg - 1u) / upg;
+  a.span_magic = span >= 2 ? (uint32_t)(((1ull << 32) + span - 1) / span) : 0u;
+  a.split_magic = a.splits >= 2 ? (uint32_t)(((1ull << 32) + (uint64_t)a.splits - 1) / (uint64_t)a.splits) : 0u;
+  return true;
+}
 
 // One unit of a compute wave: activations (MT = 1), weights, and for each of
 // the GPU groups of the unit the NTW scales and zero points of the lane's rows
@@ -242,6 +269,13 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   uint8_t* const lds = GATHER || NORM ? lds_d : lds_s;
   __shared__ float npart[NORM ? 4 * kKW : 1];  // NORM: per-row, per-wave sums of h^2
 
+  // The arguments the prologue reads, pinned in SGPRs at entry so that they
+  // arrive in one round trip: left to itself the compiler loads each group
+  // where it is first used, and every group behind a branch waited for its
+  // own trip to the kernel-argument memory before the first weight load.
+  asm volatile("" ::"s"(a.M), "s"(a.N), "s"(a.K), "s"(a.n_wg), "s"(a.grid_m), "s"(a.splits),
+               "s"(a.groups), "s"(a.upg_magic), "s"(a.span_magic), "s"(a.split_magic), "s"(a.x),
+               "s"(a.wt), "s"(a.s_gm), "s"(a.z_gm));
   const int tid = threadIdx.x, l = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // (weight workgroup, activation block). Workgroups are dealt to the 8 XCDs
@@ -252,11 +286,11 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   if constexpr (SPLIT) {
     // K split (one activation block): the splits of a weight workgroup are
     // consecutive blocks
-    wg = blockIdx.x / a.splits;
+    wg = (int)__umulhi(blockIdx.x, a.split_magic);  // blockIdx.x / splits
     sp = blockIdx.x - wg * a.splits;
   } else if (a.grid_m > 1) {
     const int span = 8 * a.grid_m;
-    const int q = blockIdx.x / span, r = blockIdx.x % span;
+    const int q = (int)__umulhi(blockIdx.x, a.span_magic), r = blockIdx.x - q * span;
     wg = 8 * q + (r & 7);
     mb = r >> 3;
   }
@@ -269,8 +303,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   // steps of this workgroup: the unit quads q_lo .. q_lo + steps - 1 (all of
   // them unsplit; split sp takes quads Q sp / splits .. Q (sp + 1) / splits - 1)
   const int Q = U / kKW;
-  const int q_lo = SPLIT ? sp * Q / a.splits : 0;
-  const int steps = SPLIT ? (sp + 1) * Q / a.splits - q_lo : Q;
+  const int q_lo = SPLIT ? (int)__umulhi((uint32_t)(sp * Q), a.split_magic) : 0;
+  const int steps = SPLIT ? (int)__umulhi((uint32_t)((sp + 1) * Q), a.split_magic) - q_lo : Q;
   const int ln = l & 15, h = l >> 4;
   const int row0 = 64 * panel + 4 * ln + jb;  // first of the lane's NTW rows
   // RNG: tile j of the range (clamped to the last tile), its lane row and the
@@ -332,15 +366,13 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
   } else {
     // ---- compute wave kw: units u = 4 s + kw
     const int kw = wv;
-    const int G = K / a.gs;
+    const int G = a.groups;
     const int rowc = row0 < N ? row0 : N - 4 + jb;  // clamped for the scale/zero loads
     const __amdgpu_buffer_rsrc_t rw = rsrc(a.wt, (int64_t)((N + 63) / 64) * 64 * (K >> 1));
     const __amdgpu_buffer_rsrc_t rs = rsrc(a.s_gm, (int64_t)G * N * 4);
     const __amdgpu_buffer_rsrc_t rz = rsrc(a.z_gm, (int64_t)G * N);
     const int vw = panel * U * 4096 + 1024 * jb + 16 * l;
     const int vs = rowc * 4, vz = rowc;
-    // groups per unit (GPU > 1: gs 32 or 64) or units per group (gs >= 128)
-    const int upg = a.gs >= 128 ? a.gs >> 7 : 1;
     __amdgpu_buffer_rsrc_t rxd;
     int vxd = 0;
     const int xstride = 2 * K + 16;   // GATHER: LDS bytes per activation row
@@ -422,7 +454,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       }
       if constexpr (NORM) un.xo = uu * 256;
       if constexpr (RNG) {
-        const int g = uu / upg;
+        const int g = (int)(((uint32_t)uu * a.upg_magic) >> 16);  // uu / upg
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
           un.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -438,7 +470,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
         un.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw + 1024 * j, uu * 4096, 2));
 #pragma unroll
       for (int gp = 0; gp < GPU; ++gp) {
-        const int g = GPU > 1 ? uu * GPU + gp : uu / upg;
+        const int g = GPU > 1 ? uu * GPU + gp : (int)(((uint32_t)uu * a.upg_magic) >> 16);
         // the vector result is converted as a whole: hipcc 7.2 mis-reads the
         // lanes of a u32x4 bit-cast element by element to float
         if constexpr (NTW == 4) {
@@ -823,10 +855,15 @@ hipError_t launch_mt(const TgemmConfig& c, const TgemmArgs& a, hipStream_t strea
 bool tgemm_supported(int64_t M, int64_t N, int64_t K, int64_t gs) {
   // K % 512 == 0: every compute wave gets the same number of units, at least
   // the ring depth of them (K >= 1536)
+  // The last two bounds keep the host's reciprocal constants exact
+  // (derive_args): units times units per group, workgroups times the span
+  // of one weight workgroup's activation blocks.
+  const int64_t wgs = ((N + 63) / 64 * 4 + 8) * ((M + 15) / 16);
   return M >= 1 && N % 4 == 0 && K % 512 == 0 && K >= 1536 &&
          (gs == 32 || gs == 64 || gs % 128 == 0) &&
          K % gs == 0 && (int64_t)M * K * 2 < (1ll << 31) && ((N + 63) / 64) * 64 * (K / 2) < (1ll << 31) &&
-         ((N + 63) / 64 * 4 + 8) * ((M + 15) / 16) < (1ll << 31);  // workgroups
+         wgs < (1ll << 31) && (K / 128) * (gs >= 128 ? gs / 128 : 1) < (1ll << 16) &&
+         wgs * 8 * ((M + 15) / 16) < (1ll << 32);
 }
 
 TgemmConfig tgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs, bool gather) {
@@ -976,6 +1013,7 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   a.counters = (int*)workspace;
   a.part = c.splits > 1 ? (float*)((uint8_t*)workspace + part_offset) : nullptr;
   a.glu = 0;
+  if (!derive_args(a)) return hipErrorInvalidValue;
   if (bf16) {
     const dim3 block(kKW * 64);
 #define PMI_TG_BF(NTW_)                                                                               \
@@ -1022,6 +1060,7 @@ hipError_t launch_tgemm_glu(const void* x, const uint8_t* w_tiled, const float* 
   a.counters = nullptr;
   a.part = nullptr;
   a.glu = 1;
+  if (!derive_args(a)) return hipErrorInvalidValue;
   return launch_mt<1>(c, a, stream);
 }
 
@@ -1064,6 +1103,7 @@ hipError_t launch_tgemm_norm(const void* x, const void* r, const void* norm_w, f
   a.nw = (const f16*)norm_w;
   a.h_out = (f16*)h_out;
   a.eps = eps;
+  if (!derive_args(a)) return hipErrorInvalidValue;
   if (c.ntw == 4) return launch_norm_variant<4>(c, a, stream);
   if (c.ntw == 2) return launch_norm_variant<2>(c, a, stream);
   return launch_norm_variant<1>(c, a, stream);
