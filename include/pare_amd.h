@@ -496,7 +496,8 @@ PMI_API int pmi_silu_mul_f16(const void* gate_up, void* out, int64_t rows, int64
 
 /* ---- Measurement hook ------------------------------------------------------
  * Reads `bytes` (a multiple of 16) of device memory at `buf` once, with at most
- * `grid` workgroups each streaming one contiguous range in 16-byte loads, and
+ * `grid` workgroups of 8 waves (the GEMV's workgroup shape) each streaming one
+ * contiguous range in 16-byte loads, and
  * computes nothing from it: the read floor that a kernel reading the same bytes
  * on the same grid can reach. sink: device uint32 [grid] (never written in
  * practice; it keeps the loads live). No reference counterpart. */

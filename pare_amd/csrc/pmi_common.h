@@ -100,6 +100,19 @@ PMI_DEV int perm_col(const int32_t* __restrict__ perm, int k, int K) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// Division by a launch constant d >= 1 without a division sequence in the
+// kernel (one is ~25 dependent instructions): the host passes
+// m = udiv_magic(d) = ceil(2^32 / d) (0 for d = 1), and umulhi(n, m) is
+// floor(n / d) or one more; one compare corrects it. Exact for n < 2^31.
+inline uint32_t udiv_magic(uint32_t d) {
+  return d <= 1 ? 0u : (uint32_t)(((1ull << 32) + d - 1) / d);
+}
+PMI_DEV uint32_t udiv(uint32_t n, uint32_t d, uint32_t m) {
+  if (m == 0) return n;
+  const uint32_t q = __umulhi(n, m);
+  return q * d > n ? q - 1 : q;
+}
+
 // Raw buffer resource over `bytes` bytes (untyped dword access, no swizzle).
 PMI_DEV __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);

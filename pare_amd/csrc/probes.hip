@@ -7,26 +7,32 @@
 namespace pmi {
 namespace {
 
-// Workgroup b reads bytes [b * span, (b + 1) * span) of the buffer (span a
-// multiple of 16 KiB, the last workgroup's range clamped to the end) with
-// 16-byte loads, 64 lanes x 16 B = 1 KiB per wave load, four loads in flight
-// per lane, the way the GEMV streams a workgroup's rows. The XOR of what it
-// read is stored only when it equals a constant no data here produces, which
-// keeps the loads live at no cost.
-__global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict__ p, int64_t n16,
-                                                         int64_t span16, uint32_t* __restrict__ sink) {
+// Workgroup b (8 waves, the GEMV's workgroup shape, so that a grid of one
+// workgroup per CU runs at the GEMV's occupancy) reads bytes
+// [b * span, (b + 1) * span) of the buffer (span a multiple of 32 KiB, the
+// last workgroup's range clamped to the end) with 16-byte loads, 64 lanes x
+// 16 B = 1 KiB per wave load, four loads in flight per lane, the way the GEMV
+// streams a workgroup's rows. The XOR of what it read is stored only when it
+// equals a constant no data here produces, which keeps the loads live at no
+// cost.
+constexpr int kProbeThreads = 512;
+
+__global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const u32x4* __restrict__ p,
+                                                                   int64_t n16, int64_t span16,
+                                                                   uint32_t* __restrict__ sink) {
   const int64_t b0 = (int64_t)blockIdx.x * span16;
   const int64_t b1 = b0 + span16 < n16 ? b0 + span16 : n16;
   u32x4 acc = {0u, 0u, 0u, 0u};
   int64_t i = b0 + threadIdx.x;
-  for (; i + 3 * 256 < b1; i += 4 * 256) {
+  constexpr int T = kProbeThreads;
+  for (; i + 3 * T < b1; i += 4 * T) {
     const u32x4 a = __builtin_nontemporal_load(p + i);
-    const u32x4 b = __builtin_nontemporal_load(p + i + 256);
-    const u32x4 c = __builtin_nontemporal_load(p + i + 512);
-    const u32x4 d = __builtin_nontemporal_load(p + i + 768);
+    const u32x4 b = __builtin_nontemporal_load(p + i + T);
+    const u32x4 c = __builtin_nontemporal_load(p + i + 2 * T);
+    const u32x4 d = __builtin_nontemporal_load(p + i + 3 * T);
     acc ^= a ^ b ^ c ^ d;
   }
-  for (; i < b1; i += 256) acc ^= p[i];
+  for (; i < b1; i += T) acc ^= p[i];
   const uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
   if (v == 0x9E3779B9u) sink[blockIdx.x] = v;
 }
@@ -36,10 +42,10 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict
 hipError_t launch_read_probe(const void* buf, int64_t bytes, int64_t grid, uint32_t* sink,
                              hipStream_t stream) {
   const int64_t n16 = bytes / 16;
-  // per-workgroup span rounded up to 16 KiB (1024 chunks of 16 bytes)
-  const int64_t span16 = ((n16 + grid - 1) / grid + 1023) / 1024 * 1024;
+  // per-workgroup span rounded up to 32 KiB (2048 chunks of 16 bytes)
+  const int64_t span16 = ((n16 + grid - 1) / grid + 2047) / 2048 * 2048;
   const int64_t blocks = (n16 + span16 - 1) / span16;
-  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(kProbeThreads), 0, stream,
                      (const u32x4*)buf, n16, span16, sink);
   return hipGetLastError();
 }

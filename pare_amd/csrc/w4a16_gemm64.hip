@@ -76,6 +76,9 @@ struct Gemm64Args {
   float* part;    // split-K partial tiles (splits > 1)
   int* counters;  // one per (n block, m block), zero between calls
   int M, N, K, n_blocks, grid_m, splits;
+  // udiv_magic of splits, 8 grid_m and n_blocks % 8 (the divisors of the
+  // workgroup numbering), so that no wave divides before its first load
+  uint32_t split_m, span_m, rem_m;
 };
 
 // One weight stage of a compute lane: 32 bytes of its row, the row's scale
@@ -102,23 +105,28 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm64_kernel(Gemm64Args a)
   // consecutive; workgroups are dealt to the 8 XCDs round-robin by index, so
   // the m blocks of one n block, numbered 8 tiles apart, share an XCD and its
   // L2 (a placement preference only).
+  // The arguments the prologue reads, pinned in SGPRs at entry so that they
+  // arrive in one round trip to the kernel-argument memory.
+  asm volatile("" ::"s"(a.M), "s"(a.N), "s"(a.K), "s"(a.n_blocks), "s"(a.grid_m), "s"(a.splits),
+               "s"(a.split_m), "s"(a.span_m), "s"(a.rem_m), "s"(a.x), "s"(a.w));
   const int bid = blockIdx.x;
-  const int sp = bid % a.splits;
-  const int tl = bid / a.splits;
+  const int tl = (int)udiv(bid, a.splits, a.split_m);
+  const int sp = bid - tl * a.splits;
   int nb, mb;
   {
-    const int gm = a.grid_m, full = (a.n_blocks / 8) * 8;
+    const int gm = a.grid_m, full = a.n_blocks & ~7;
     if (gm == 1) {
       nb = tl;
       mb = 0;
     } else if (tl < full * gm) {
-      const int r = tl % (8 * gm);
-      nb = (tl / (8 * gm)) * 8 + (r & 7);
+      const int q = (int)udiv(tl, 8 * gm, a.span_m), r = tl - q * 8 * gm;
+      nb = q * 8 + (r & 7);
       mb = r >> 3;
     } else {
       const int rem = a.n_blocks - full, r = tl - full * gm;
-      nb = full + r % rem;
-      mb = r / rem;
+      const int q = (int)udiv(r, rem, a.rem_m);
+      nb = full + (r - q * rem);
+      mb = q;
     }
   }
   const int M = a.M, N = a.N, K = a.K;
@@ -126,8 +134,8 @@ __global__ __launch_bounds__(kThreads, 1) void w4a16_gemm64_kernel(Gemm64Args a)
   // groups [g_lo, g_hi) of this split, in K-wave pairs; K wave k takes
   // g_lo + k, g_lo + k + 2, ... (stage s of K wave k is group g_lo + 2s + k)
   const int pairs = (G + 1) >> 1;
-  const int g_lo = 2 * (int)((int64_t)sp * pairs / a.splits);
-  const int g_hi_raw = 2 * (int)((int64_t)(sp + 1) * pairs / a.splits);
+  const int g_lo = 2 * (int)udiv(sp * pairs, a.splits, a.split_m);
+  const int g_hi_raw = 2 * (int)udiv((sp + 1) * pairs, a.splits, a.split_m);
   const int g_hi = g_hi_raw < G ? g_hi_raw : G;
   const int S = (g_hi - g_lo + 1) >> 1;  // steps (stages of K wave 0)
   const int row_bytes = K >> 1;
@@ -451,6 +459,9 @@ hipError_t launch_gemm64(const void* x, const uint8_t* w, const float* scales, c
     c.grid = c.n_blocks * c.grid_m;
   }
   a.splits = c.splits;
+  a.split_m = udiv_magic((uint32_t)c.splits);
+  a.span_m = udiv_magic(8u * (uint32_t)c.grid_m);
+  a.rem_m = udiv_magic((uint32_t)(c.n_blocks % 8 ? c.n_blocks % 8 : 1));
   a.counters = (int*)workspace;
   a.part = c.splits > 1 ? (float*)((uint8_t*)workspace + part_offset) : nullptr;
   if (M <= 32) return launch_mt<1>(a, c.grid, zero_u8, stream);
