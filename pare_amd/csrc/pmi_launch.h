@@ -112,6 +112,12 @@ constexpr int kGemvLdsChunks = 8;  // 16-byte activation chunks staged per threa
 inline bool gemv_perm_lds_fits(int64_t mt, int64_t K, int64_t threads) {
   return K % 8 == 0 && mt * K * 2 <= 64 * 1024 && mt * K / 8 <= kGemvLdsChunks * threads;
 }
+// Plain activations staged in LDS (mode 7): one 16-byte chunk per thread at
+// most, so that a workgroup's start-up issues one load per wave for them.
+constexpr int kGemvXLdsChunks = 1;
+inline bool gemv_x_lds_fits(int64_t mt, int64_t K, int64_t threads) {
+  return K % 8 == 0 && mt * K * 2 <= 64 * 1024 && mt * K / 8 <= kGemvXLdsChunks * threads;
+}
 // Mode 4 fits every launch of an M-row GEMV (launched four rows at a time).
 bool gemv_perm_lds_ok(int64_t M, int64_t N, int64_t K);
 struct GemvXform {

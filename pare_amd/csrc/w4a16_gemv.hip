@@ -421,7 +421,10 @@ PMI_DEV void store_y(f16* p, float v) {
 // residual stream x whose sum of squares the launch that formed it left as
 // per-workgroup partials (xf.stats, xf.n_stats of them): every wave adds them
 // in the same fixed order, so no workgroup reduces the row or waits at a
-// barrier first; 6 bf16 x [M, K], y bf16 (the native bf16 extension).
+// barrier first; 6 bf16 x [M, K], y bf16 (the native bf16 extension);
+// 7 x [M, K] as 0, staged in LDS with one 16-byte load per thread and read
+// from there: a workgroup's start-up then puts 8 KiB (K = 4096) of activation
+// reads in front of its weight stream, not 8 waves x 4 KiB.
 // Epilogue (xf.res, one activation row, slice_waves > 1): y = h = y + res
 // rounded as add_rmsnorm_kernel forms h, and xf.stats[blockIdx.x] = the sum of
 // h^2 over the workgroup's rows (fixed order), for a mode-5 launch to read.
@@ -505,25 +508,34 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                           ub[sp][m]);
       } else if constexpr (XM == 4) {
         if (m == 0) load_perm(perm, k_lo, k_lo + hgs, K, pl[sp], ph[sp]);
-      } else {
+      } else if constexpr (XM != 7) {
         load_x_raw<XM == 1>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
       }
     }
   }
-  // XM 4: the MT activation rows ([MT, K], contiguous) in 16-byte chunks, at
-  // most kXCh per thread (the host checks MT * K / 8 <= kXCh * blockDim.x),
+  // XM 4, 7: the MT activation rows ([MT, K], contiguous) in 16-byte chunks,
+  // at most kXCh per thread (the host checks MT * K / 8 <= kXCh * blockDim.x),
   // loaded here and written to LDS after the first weight batch is issued.
-  constexpr int kXCh = XM == 4 ? kGemvLdsChunks : 1;
+  constexpr bool kXL = XM == 4 || XM == 7;
+  constexpr int kXCh = XM == 4 ? kGemvLdsChunks : XM == 7 ? kGemvXLdsChunks : 1;
   u32x4 xst[kXCh];
   const int n_xch = MT * K / 8;
   f16* lds_x = reinterpret_cast<f16*>(
       reinterpret_cast<uint8_t*>(part) +
       (((slice_waves > 1 ? rows_per_wg * slice_waves * MT * 4 : 0) + 15) & ~15));
-  if constexpr (XM == 4) {
+  if constexpr (kXL) {
 #pragma unroll
     for (int i = 0; i < kXCh; ++i) {
       const int c = (int)threadIdx.x + i * (int)blockDim.x;
-      xst[i] = c < n_xch ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
+      if constexpr (XM == 7) {
+        // one chunk per thread, loaded and written without a branch (threads
+        // past the rows re-read the last chunk and write it to a spare slot
+        // after the rows): in a branch the compiler sank the load below the
+        // weight batches and drained them before the write
+        xst[i] = reinterpret_cast<const u32x4*>(x)[c < n_xch ? c : n_xch - 1];
+      } else {
+        xst[i] = c < n_xch ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
+      }
     }
     // issued ahead of the weight batches: a staging load scheduled after them
     // would make its LDS write wait for every batch in flight
@@ -559,18 +571,31 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   uint32_t xp[SPW][MT][16];
   float sx[SPW][MT];
   // Pairs the activations with the nibble order and sums each lane's 32.
-  // XM 4: stage the activations in LDS, then gather this lane's columns
+  // XM 4: stage the activations in LDS, then gather this lane's columns;
+  // XM 7: stage them in LDS, then read this lane's two 16-column runs
   auto stage_x = [&]() {
-    if constexpr (XM == 4) {
+    if constexpr (kXL) {
 #pragma unroll
       for (int i = 0; i < kXCh; ++i) {
         const int c = (int)threadIdx.x + i * (int)blockDim.x;
-        if (c < n_xch) reinterpret_cast<u32x4*>(lds_x)[c] = xst[i];
+        if constexpr (XM == 7)
+          reinterpret_cast<u32x4*>(lds_x)[c < n_xch ? c : n_xch] = xst[i];
+        else if (c < n_xch)
+          reinterpret_cast<u32x4*>(lds_x)[c] = xst[i];
       }
       // own LDS writes done (lgkmcnt(0)), then a bare s_barrier (no vmcnt
       // wait: the weight batches stay in flight)
       __builtin_amdgcn_s_waitcnt(0xC07F);
       barrier_only();
+    }
+    if constexpr (XM == 7) {
+#pragma unroll
+      for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          load_x_raw<false>(lds_x + m * K, perm, klo[sp], klo[sp] + hgs, K, xa[sp][m], xb[sp][m]);
+    }
+    if constexpr (XM == 4) {
       const uint16_t* xs = reinterpret_cast<const uint16_t*>(lds_x);
 #pragma unroll
       for (int sp = 0; sp < SPW; ++sp)
@@ -802,6 +827,24 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   }
 }
 
+int env_int(const char* name, int dflt) {
+  const char* s = getenv(name);
+  return (s && *s) ? atoi(s) : dflt;
+}
+
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
 // The kernel's geometry for a launch of U rows per batch; false when a
 // quotient would leave the range in which its reciprocal is exact (rows of
 // 2^17 columns or more).
@@ -829,11 +872,23 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
   const dim3 block(64 * c.slice_waves * c.row_waves);
   GemvGeom gg;
   if (!gemv_geom(c, U, K, gs, gg)) return hipErrorInvalidValue;
-  // XM 4 (xf.mode 4): the activation rows staged in LDS after the partials
+  // XM 4 (xf.mode 4): the activation rows staged in LDS after the partials;
+  // plain activations (XM 7 for 0) likewise where several row waves would
+  // each load the same slices, the rows fit one chunk per thread, and either
+  // a ring or several workgroups per CU multiply those loads (A/B on MI355X,
+  // us: fused q/k/v, three workgroups per CU, 5.01 -> 4.75; gate 7.75 ->
+  // 7.67; fused gate/up 12.5 -> 12.45). One workgroup per CU with one batch
+  // per wave (q/o, k/v) lost 0.1-0.2 to the barrier and keeps its registers.
   const bool perm_lds = perm && xf.mode == 4;
   if (perm_lds && !gemv_perm_lds_fits(MT, K, (int)block.x)) return hipErrorInvalidValue;
-  const size_t lds = perm_lds ? (((size_t)c.lds_bytes + 15) & ~(size_t)15) + (size_t)MT * K * 2
-                              : (size_t)c.lds_bytes;
+  static const bool env_xlds = env_int("PMI_GEMV_XLDS", 1) != 0;  // benchmark sweeps only
+  const bool x_lds = env_xlds && !perm && xf.mode == 0 && c.row_waves > 1 &&
+                     (D > 1 || c.grid > device_cus()) && gemv_x_lds_fits(MT, K, (int)block.x);
+  // (XM 7 writes one spare 16-byte slot after the rows)
+  const size_t lds = perm_lds || x_lds
+                         ? (((size_t)c.lds_bytes + 15) & ~(size_t)15) + (size_t)MT * K * 2 +
+                               (x_lds ? 16 : 0)
+                         : (size_t)c.lds_bytes;
 #define PMI_GEMV_LAUNCH(XM, Z)                                                                  \
   hipLaunchKernelGGL((w4a16_gemv_kernel<MT, U, D, SPW, XM, Z>), dim3(c.grid), block, lds, stream, \
                      (const f16*)x, w, scales, zeros, perm, (f16*)y, N, K, gs, gg, xf)
@@ -873,6 +928,9 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
   } else if (perm) {
     if (zero_u8) PMI_GEMV_LAUNCH(1, true);
     else PMI_GEMV_LAUNCH(1, false);
+  } else if (x_lds) {
+    if (zero_u8) PMI_GEMV_LAUNCH(7, true);
+    else PMI_GEMV_LAUNCH(7, false);
   } else {
     if (zero_u8) PMI_GEMV_LAUNCH(0, true);
     else PMI_GEMV_LAUNCH(0, false);
@@ -927,23 +985,6 @@ hipError_t launch_mt(const GemvConfig& c, const void* x, const uint8_t* w, const
   return launch_ud<MT, 1>(c, x, w, scales, zeros, zero_u8, perm, y, N, K, gs, xf, stream);
 }
 
-int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  return (s && *s) ? atoi(s) : dflt;
-}
-
-int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      cus = n;
-    else
-      cus = 256;
-  }
-  return cus;
-}
 
 constexpr int kMaxPartBytes = 32 * 1024;  // LDS for the per-row partials
 
