@@ -1006,7 +1006,12 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   // (10.2 us against 11.4-11.7 for four rows at one). Long rows (three or more
   // slice waves, e.g. K = 14336): four rows, one workgroup per CU (8.0 us).
   // Otherwise by rows per CU: >= 48 (N = 14336 and 28672) pairs at one per CU
-  // (7.9 and 12.7-13.0 us; three per CU gave 13.8-14.3 us at N = 28672),
+  // (7.9 and 12.7-13.0 us; three per CU gave 13.8-14.3 us at N = 28672);
+  // plain activations (with the host-side quotients and, where it applies, the
+  // activation staging of mode 7) instead take four-row batches at >= 96
+  // (N = 28672: median 12.11-12.30 against 12.32-12.36 us, three A/B rounds)
+  // and single rows at two per CU below (N = 14336: 7.51-7.55 against
+  // 7.62-7.68 us),
   // >= 20 (N = 6144) pairs at three per CU (5.0 us against 5.3-5.5 for single
   // rows at two). Fewer rows (q/o, k/v): one batch per wave, of the most rows
   // that still give every CU a workgroup (N = 4096: four rows, 4.25 us;
@@ -1033,6 +1038,8 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   // (Qwen down 3584 x 18944: 13.8 against 18.1 us at two per CU)
   if (mt == 1 && c.slices_per_wave == 2) { c.rows_per_wave = 1; wpc = xmode == 4 ? 1 : 2; }
   else if (mt == 1 && c.slice_waves >= 3) { c.rows_per_wave = 4; wpc = 1; }
+  else if (mt == 1 && rows_per_cu >= 96 && xmode == 0) { c.rows_per_wave = 4; wpc = 1; }
+  else if (mt == 1 && rows_per_cu >= 48 && xmode == 0) { c.rows_per_wave = 1; wpc = 2; }
   else if (mt == 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 1; }
   // with the RMSNorm prologue (mode 3) every workgroup first reduces the whole
   // row: single rows at two per CU (fused q/k/v in the decoder: 8.0 against
