@@ -71,10 +71,16 @@ class Buf:
     """Device buffers of one INT4 launch in the kernels' format: kernel-layout
     codes u8 [N, K/2], fp32 scales [N, G], u8 zero points [N, G]; for the MFMA
     GEMM legs also their group-major copies (built once, outside graph capture,
-    as a module does per layer)."""
+    as a module does per layer); with act_order the permutation and its 16-bit
+    copy (pack.perm_u16, built once per layer as the module does)."""
 
     def __init__(self, name, w, s, z, perm=None):
         self.name, self.w, self.s, self.z, self.perm = name, w, s, z, perm
+        self.perm16 = None
+        if perm is not None:
+            import pare_amd as P
+
+            self.perm16 = P.perm_u16(perm)
         self.N, self.K = w.shape[0], w.shape[1] * 2
         self._gm = None
         self._tiled = None
@@ -156,6 +162,7 @@ def launch(L, buf, x, y, M, stream):
     rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, buf.w.data_ptr(), buf.s.data_ptr(),
                             buf.z.data_ptr(), _lib.PMI_U8,
                             buf.perm.data_ptr() if buf.perm is not None else None,
+                            buf.perm16.data_ptr() if buf.perm16 is not None else None,
                             s_gm.data_ptr() if s_gm is not None else None,
                             z_gm.data_ptr() if z_gm is not None else None,
                             buf._tiled.data_ptr() if buf._tiled is not None else None, y.data_ptr(),
@@ -717,7 +724,7 @@ def main():
             for f in fused:
                 b = f[2]
                 rc = L.pmi_matmul_w4a16(xb.data_ptr(), _lib.PMI_BF16, b.w.data_ptr(), b.s.data_ptr(),
-                                        b.z.data_ptr(), _lib.PMI_U8, None, None, None, None,
+                                        b.z.data_ptr(), _lib.PMI_U8, None, None, None, None, None,
                                         yb.data_ptr(), _lib.PMI_BF16, 1, b.N, b.K, GS,
                                         WORKSPACE[0].data_ptr(), WORKSPACE[0].numel(), s)
                 assert rc == 0, _lib.last_error()
@@ -768,7 +775,7 @@ def main():
             b = single[i % n_layers][4 + (i // n_layers) % 2]
             s_gm, z_gm = b.gm()
             rc = L.pmi_matmul_w4a16(xb16.data_ptr(), _lib.PMI_BF16, b.w.data_ptr(), b.s.data_ptr(),
-                                    b.z.data_ptr(), _lib.PMI_U8, None, s_gm.data_ptr(), z_gm.data_ptr(),
+                                    b.z.data_ptr(), _lib.PMI_U8, None, None, s_gm.data_ptr(), z_gm.data_ptr(),
                                     b.tiled().data_ptr(), yb16.data_ptr(), _lib.PMI_BF16, 16, b.N, b.K, GS,
                                     WORKSPACE[0].data_ptr(), WORKSPACE[0].numel(), s)
             assert rc == 0, _lib.last_error()

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PMI_ABI_VERSION 15
+#define PMI_ABI_VERSION 16
 
 #if defined(__GNUC__)
 #define PMI_API __attribute__((visibility("default")))
@@ -86,6 +86,16 @@ PMI_API int pmi_repack_int4_for_kernel(const uint8_t* packed, uint8_t* out, cons
  * Replaces: the per-call zeros.float() of _to_2d   pare/kernels/matmul_int4.py:219-228 */
 PMI_API int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count,
                     int64_t count, void* stream);
+
+/* act_order permutation int32 [K] -> its 16-bit copy perm16 uint16 [K]
+ * (16-byte aligned, K <= 65536), for pmi_matmul_w4a16's perm16 argument.
+ * Entries outside [0, K) become 0, as the kernels clamp them at use; their
+ * number is added to *bad_count (device int32, nullable). Built once per layer.
+ * No reference counterpart: a derived per-layer copy of the act_order
+ * permutation (from g_idx, pare/schemes/gptq.py:196-201,258-261), like the
+ * kernel-layout weight the reference caches (pare/layers/linear.py:148-151). */
+PMI_API int pmi_perm_u16(const int32_t* perm, uint16_t* perm16, int32_t* bad_count, int64_t K,
+                         void* stream);
 
 /* AWQ-GEMM checkpoint tensors -> the buffers above, one device pass each.
  * qweight int32 [K, N/8] and qzeros int32 [G, N/8] hold eight 4-bit codes per
@@ -155,6 +165,10 @@ PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N,
  * zeros: PMI_F32 or PMI_U8 [N,G]; perm (nullable, int32 [K]): act_order
  * gather, X is read as X[:, perm[j]] for weight column j (w must then be
  * repacked with the same perm); y: fp16 [M,N].
+ * perm16 (nullable; only with perm): the pmi_perm_u16 copy of perm (uint16
+ * [K], 16-byte aligned, K <= 65536). The GEMV's act_order launches that stage
+ * X in LDS read it instead of perm, half the bytes every workgroup reads
+ * before its first gather; same results. Every other kernel reads perm.
  * scales_gm, zeros_gm (nullable, both or neither): the pmi_sz_group_major
  * copies of scales and zeros; the MFMA GEMM reads them (one contiguous run per
  * group) instead of gathering [N,G] rows when N % 4 == 0. The other kernels
@@ -178,7 +192,7 @@ PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N,
  *           pare/kernels/matmul_int4.py:183-243 (kernel :66-176) */
 PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_dtype, const int32_t* perm,
-                     const float* scales_gm, const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
+                     const uint16_t* perm16, const float* scales_gm, const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream);
 
@@ -198,7 +212,8 @@ PMI_API int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const
  *           matmul_w4a16  pare/kernels/matmul_int4.py:183-243, for the callers above. */
 PMI_API int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w,
                                      const float* scales, const void* zeros, int zero_dtype,
-                                     const int32_t* perm, const float* scales_gm,
+                                     const int32_t* perm, const uint16_t* perm16,
+                                     const float* scales_gm,
                                      const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
                                      int y_dtype, int64_t M,
                                      int64_t N, int64_t K, int64_t group_size, void* stream);

@@ -17,7 +17,7 @@ from .gptq import HessianAccumulator, gptq_quantize, quantize_linear_gptq
 from .kernels import kernel_available, kernel_choice, matmul_w4a16, matmul_w4a16_bf16, triton_available
 from .linear import FusedQuantizedLinear, QuantizedLinear
 from .model_io import load_quantized, save_quantized
-from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
+from .pack import (dequantize_int4, perm_from_g_idx, perm_u16, repack_int4_for_kernel, sz_group_major,
                    tile_w4a16, tiled_supported, zeros_to_u8)
 from .quant import rtn_quantize
 
@@ -25,7 +25,8 @@ __all__ = [
     "FusedQuantizedLinear", "QuantConfig", "QuantDtype", "QuantizedLinear", "dequantize_int4",
     "export_awq", "gptq_quantize", "HessianAccumulator", "kernel_available", "load_awq",
     "quantize_linear_gptq",
-    "kernel_choice", "matmul_w4a16", "matmul_w4a16_bf16", "perm_from_g_idx", "repack_int4_for_kernel",
+    "kernel_choice", "matmul_w4a16", "matmul_w4a16_bf16", "perm_from_g_idx", "perm_u16",
+    "repack_int4_for_kernel",
     "load_quantized", "rtn_quantize", "save_quantized", "sz_group_major", "tile_w4a16",
     "tiled_supported", "triton_available", "zeros_to_u8",
 ]

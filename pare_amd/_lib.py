@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libpare_amd.so"
 
 # PMI_ABI_VERSION of include/pare_amd.h that these bindings follow.
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 PMI_OK = 0
 PMI_ERR_INVALID = -1
@@ -42,6 +42,7 @@ SIGNATURES = {
     "pmi_device_supported": (_i, [_i]),
     "pmi_repack_int4_for_kernel": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "pmi_zeros_to_u8": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "pmi_perm_u16": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "pmi_sz_group_major": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i64, _i64, _vp]),
     "pmi_matmul_w4a16_glu": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i64, _vp]),
     "pmi_matmul_w4a16_rmsnorm": (_i, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i, _vp,
@@ -55,9 +56,9 @@ SIGNATURES = {
                                      _vp]),
     "pmi_tiled_bytes": (ctypes.c_size_t, [_i64, _i64]),
     "pmi_tile_w4a16": (_i, [_vp, _vp, _i64, _i64, _i64, _vp]),
-    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i64, _i64,
+    "pmi_matmul_w4a16": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i64, _i64,
                              _i64, _i64, _vp, ctypes.c_size_t, _vp]),
-    "pmi_matmul_w4a16_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i64,
+    "pmi_matmul_w4a16_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i64,
                                       _i64, _i64, _i64, _vp]),
     "pmi_matmul_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i]),
     "pmi_dequant_w4a16": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _vp]),

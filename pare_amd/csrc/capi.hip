@@ -104,6 +104,18 @@ int pmi_zeros_to_u8(const float* zeros, uint8_t* zeros_u8, int32_t* bad_count, i
                   fn);
 }
 
+int pmi_perm_u16(const int32_t* perm, uint16_t* perm16, int32_t* bad_count, int64_t K,
+                 void* stream) {
+  const char* fn = "pmi_perm_u16";
+  if (K < 0 || K > 65536)
+    return fail(PMI_ERR_INVALID, "%s: need 0 <= K <= 65536 (K=%lld)", fn, (long long)K);
+  if (K == 0) return ok();
+  if (!perm || !perm16) return fail(PMI_ERR_INVALID, "%s: null buffer", fn);
+  if (!aligned(perm, 4)) return fail(PMI_ERR_INVALID, "%s: perm must be 4-byte aligned", fn);
+  if (!aligned(perm16, 16)) return fail(PMI_ERR_INVALID, "%s: perm16 must be 16-byte aligned", fn);
+  return from_hip(pmi::launch_perm_u16(perm, perm16, bad_count, K, (hipStream_t)stream), fn);
+}
+
 namespace {
 int check_awq(int64_t N, int64_t K, int64_t gs, const char* fn) {
   if (int rc = check_shape(N, K, gs, fn)) return rc;
@@ -518,7 +530,7 @@ int pmi_sz_group_major(const float* scales, const void* zeros, int zero_dtype, f
 
 int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                      const void* zeros, int zero_dtype, const int32_t* perm,
-                     const float* scales_gm, const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
+                     const uint16_t* perm16, const float* scales_gm, const uint8_t* zeros_gm, const uint8_t* w_tiled, void* y,
                      int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                      void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "pmi_matmul_w4a16";
@@ -539,6 +551,9 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     return fail(PMI_ERR_INVALID, "%s: fp32 zeros must be 4-byte aligned", fn);
   if (!aligned(y, 2)) return fail(PMI_ERR_INVALID, "%s: y must be 2-byte aligned", fn);
   if (perm && !aligned(perm, 4)) return fail(PMI_ERR_INVALID, "%s: perm must be 4-byte aligned", fn);
+  if (perm16 && !perm) return fail(PMI_ERR_INVALID, "%s: perm16 is given with perm", fn);
+  if (perm16 && (K > 65536 || !aligned(perm16, 16)))
+    return fail(PMI_ERR_INVALID, "%s: perm16 needs K <= 65536 and 16-byte alignment", fn);
   if (!scales_gm != !zeros_gm)
     return fail(PMI_ERR_INVALID, "%s: scales_gm and zeros_gm are given together or not at all", fn);
   if (scales_gm && (!aligned(scales_gm, 4) || !aligned(zeros_gm, 4)))
@@ -693,23 +708,26 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
   // stages X in LDS and gathers X[:, perm] from there when the rows fit
   // (64 KiB); otherwise X[:, perm] is gathered once into the workspace by a
   // launch of its own, or, without room in the workspace, every lane gathers
-  // its columns from global memory.
+  // its columns from global memory. The LDS gather reads the 16-bit copy of
+  // the permutation when the caller gives one (half the bytes every
+  // workgroup reads before its first gather).
   const uint16_t* xp = (const uint16_t*)x;
   uint16_t* yp = (uint16_t*)y;
   pmi::GemvXform perm_xf;
-  perm_xf.mode = 4;
+  perm_xf.mode = perm16 ? 8 : 4;
   const bool perm_lds = perm && pmi::gemv_perm_lds_ok(M, N, K);
+  const int32_t* gemv_perm = perm_lds && perm16 ? reinterpret_cast<const int32_t*>(perm16) : perm;
   if (perm && !perm_lds && workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
     uint16_t* xg = (uint16_t*)((uint8_t*)workspace + pmi::kWsCounterBytes);
     hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
     if (e != hipSuccess) return from_hip(e, fn);
     xp = xg;
-    perm = nullptr;
+    gemv_perm = nullptr;
   }
   for (int64_t m = 0; m < M; m += 4) {
     const int64_t mt = M - m < 4 ? M - m : 4;
-    hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, perm, yp + m * N, mt, N, K,
-                                    group_size, s, perm_lds ? &perm_xf : nullptr);
+    hipError_t e = pmi::launch_gemv(xp + m * K, w, scales, zeros, zu8, gemv_perm, yp + m * N, mt, N,
+                                    K, group_size, s, perm_lds ? &perm_xf : nullptr);
     if (e != hipSuccess) return from_hip(e, fn);
   }
   return ok();
@@ -774,7 +792,7 @@ extern "C" {
 
 int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w, const float* scales,
                              const void* zeros, int zero_dtype, const int32_t* perm,
-                             const float* scales_gm, const uint8_t* zeros_gm,
+                             const uint16_t* perm16, const float* scales_gm, const uint8_t* zeros_gm,
                              const uint8_t* w_tiled, void* y,
                              int y_dtype, int64_t M, int64_t N, int64_t K, int64_t group_size,
                              void* stream) {
@@ -792,7 +810,7 @@ int pmi_matmul_w4a16_noalloc(const void* x, int x_dtype, const uint8_t* w, const
   if (need) {
     if (int rc = scratch_ptr(&ws, (hipStream_t)stream, fn)) return rc;
   }
-  const int rc = pmi_matmul_w4a16(x, x_dtype, w, scales, zeros, zero_dtype, perm, scales_gm,
+  const int rc = pmi_matmul_w4a16(x, x_dtype, w, scales, zeros, zero_dtype, perm, perm16, scales_gm,
                                   zeros_gm, w_tiled, y, y_dtype, M, N, K, group_size, ws,
                                   need ? kScratchBytes : 0, stream);
   if (rc) {

@@ -107,8 +107,10 @@ size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gs, bool ha
 //           gathered by the caller first);
 //   mode 4: act_order, x[:, perm] gathered from a copy of x staged in LDS by
 //           each workgroup (needs gemv_perm_lds_fits), instead of every lane
-//           gathering from global memory.
-constexpr int kGemvLdsChunks = 8;  // 16-byte activation chunks staged per thread (mode 4)
+//           gathering from global memory;
+//   mode 8: mode 4 with the 16-bit copy of the permutation: the perm argument
+//           then points at uint16 [K] (16-byte aligned, K <= 65536).
+constexpr int kGemvLdsChunks = 8;  // 16-byte activation chunks staged per thread (modes 4, 8)
 inline bool gemv_perm_lds_fits(int64_t mt, int64_t K, int64_t threads) {
   return K % 8 == 0 && mt * K * 2 <= 64 * 1024 && mt * K / 8 <= kGemvLdsChunks * threads;
 }
@@ -188,6 +190,10 @@ hipError_t launch_repack(const uint8_t* packed, uint8_t* out, const int32_t* per
 
 hipError_t launch_zeros_to_u8(const float* zeros, uint8_t* out, int32_t* bad, int64_t count,
                               hipStream_t stream);
+
+// int32 permutation [K] -> uint16 [K] (K <= 65536), entries outside [0, K) as 0.
+hipError_t launch_perm_u16(const int32_t* perm, uint16_t* out, int32_t* bad, int64_t K,
+                           hipStream_t stream);
 
 // AWQ-GEMM int32 layout <-> storage layout + fp32 [N,G] scales and zeros.
 hipError_t launch_awq_to_storage(const int32_t* qweight, const int32_t* qzeros, const void* scales,

@@ -95,7 +95,7 @@ PMI_DEV void load_x_raw(const f16* __restrict__ xrow, const int32_t* __restrict_
   }
 }
 
-// act_order through LDS (XM 4): the permuted column indices of this lane's
+// act_order through LDS (XM 4, 8): the permuted column indices of this lane's
 // chunk (k_lo..k_lo+15, k_hi..k_hi+15), clamped into [0, K); the activations
 // themselves are staged in LDS by the whole workgroup and gathered from there.
 PMI_DEV void load_perm(const int32_t* __restrict__ perm, int k_lo, int k_hi, int K, int (&pl)[16],
@@ -104,6 +104,26 @@ PMI_DEV void load_perm(const int32_t* __restrict__ perm, int k_lo, int k_hi, int
   for (int i = 0; i < 16; ++i) {
     pl[i] = perm_col(perm, k_lo + i, K);
     ph[i] = perm_col(perm, k_hi + i, K);
+  }
+}
+
+// The same from the 16-bit copy of the permutation (XM 8): two 16-byte loads
+// per 16 columns instead of four (k_lo and k_hi are multiples of 16 and the
+// host checks the table's 16-byte alignment), entries past K clamped to 0 as
+// perm_col clamps them.
+PMI_DEV void load_perm16(const uint16_t* __restrict__ p16, int k_lo, int k_hi, int K,
+                         int (&pl)[16], int (&ph)[16]) {
+  const u32x4* ql = reinterpret_cast<const u32x4*>(p16 + k_lo);
+  const u32x4* qh = reinterpret_cast<const u32x4*>(p16 + k_hi);
+  const u32x4 l0 = ql[0], l1 = ql[1], h0 = qh[0], h1 = qh[1];
+  const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+  const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int a = (int)((lw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
+    const int b = (int)((hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
+    pl[i] = a < K ? a : 0;
+    ph[i] = b < K ? b : 0;
   }
 }
 
@@ -414,7 +434,9 @@ PMI_DEV void store_y(f16* p, float v) {
 
 // XM selects the activation source: 0 x [M, K]; 1 x[:, perm] (act_order),
 // gathered by every lane from global memory; 4 the same, x staged in LDS once
-// per workgroup (16-byte loads) and gathered from there;
+// per workgroup (16-byte loads) and gathered from there; 8 as 4 with the
+// 16-bit copy of the permutation (perm then points at uint16 [K]), which
+// halves the table every workgroup reads before its first gather;
 // 2 the fused gate/up output [M, 2K], consumed as silu(gate) * up;
 // 3 RMSNorm(x + r) * w of the residual stream (xf.r nullable), with
 // h = x + r written to xf.h_out by workgroup 0; 5 RMSNorm(x) * w of a
@@ -477,8 +499,9 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   constexpr int kNS = XM == 3 || XM == 5 ? SPW : 1;
   uint32_t ua[kXS][kXM][8], ub[kXS][kXM][8];  // up (XM 2) or residual (XM 3)
   uint32_t wa[kNS][8], wb[kNS][8];            // norm weight (XM 3, 5)
-  constexpr int kPS = XM == 4 ? SPW : 1;
-  int pl[kPS][16], ph[kPS][16];                // permuted columns (XM 4)
+  constexpr bool kPG = XM == 4 || XM == 8;    // act_order gathered from LDS
+  constexpr int kPS = kPG ? SPW : 1;
+  int pl[kPS][16], ph[kPS][16];                // permuted columns (XM 4, 8)
   int klo[SPW];
 #pragma unroll
   for (int sp = 0; sp < SPW; ++sp) {
@@ -508,16 +531,19 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                           ub[sp][m]);
       } else if constexpr (XM == 4) {
         if (m == 0) load_perm(perm, k_lo, k_lo + hgs, K, pl[sp], ph[sp]);
+      } else if constexpr (XM == 8) {
+        if (m == 0)
+          load_perm16(reinterpret_cast<const uint16_t*>(perm), k_lo, k_lo + hgs, K, pl[sp], ph[sp]);
       } else if constexpr (XM != 7) {
         load_x_raw<XM == 1>(x + (int64_t)m * K, perm, k_lo, k_lo + hgs, K, xa[sp][m], xb[sp][m]);
       }
     }
   }
-  // XM 4, 7: the MT activation rows ([MT, K], contiguous) in 16-byte chunks,
+  // XM 4, 7, 8: the MT activation rows ([MT, K], contiguous) in 16-byte chunks,
   // at most kXCh per thread (the host checks MT * K / 8 <= kXCh * blockDim.x),
   // loaded here and written to LDS after the first weight batch is issued.
-  constexpr bool kXL = XM == 4 || XM == 7;
-  constexpr int kXCh = XM == 4 ? kGemvLdsChunks : XM == 7 ? kGemvXLdsChunks : 1;
+  constexpr bool kXL = kPG || XM == 7;
+  constexpr int kXCh = kPG ? kGemvLdsChunks : XM == 7 ? kGemvXLdsChunks : 1;
   u32x4 xst[kXCh];
   const int n_xch = MT * K / 8;
   f16* lds_x = reinterpret_cast<f16*>(
@@ -571,7 +597,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   uint32_t xp[SPW][MT][16];
   float sx[SPW][MT];
   // Pairs the activations with the nibble order and sums each lane's 32.
-  // XM 4: stage the activations in LDS, then gather this lane's columns;
+  // XM 4, 8: stage the activations in LDS, then gather this lane's columns;
   // XM 7: stage them in LDS, then read this lane's two 16-column runs
   auto stage_x = [&]() {
     if constexpr (kXL) {
@@ -595,7 +621,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         for (int m = 0; m < MT; ++m)
           load_x_raw<false>(lds_x + m * K, perm, klo[sp], klo[sp] + hgs, K, xa[sp][m], xb[sp][m]);
     }
-    if constexpr (XM == 4) {
+    if constexpr (kPG) {
       const uint16_t* xs = reinterpret_cast<const uint16_t*>(lds_x);
 #pragma unroll
       for (int sp = 0; sp < SPW; ++sp)
@@ -872,14 +898,14 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
   const dim3 block(64 * c.slice_waves * c.row_waves);
   GemvGeom gg;
   if (!gemv_geom(c, U, K, gs, gg)) return hipErrorInvalidValue;
-  // XM 4 (xf.mode 4): the activation rows staged in LDS after the partials;
+  // XM 4 and 8 (xf.mode 4, 8): the activation rows staged in LDS after the partials;
   // plain activations (XM 7 for 0) likewise where several row waves would
   // each load the same slices, the rows fit one chunk per thread, and either
   // a ring or several workgroups per CU multiply those loads (A/B on MI355X,
   // us: fused q/k/v, three workgroups per CU, 5.01 -> 4.75; gate 7.75 ->
   // 7.67; fused gate/up 12.5 -> 12.45). One workgroup per CU with one batch
   // per wave (q/o, k/v) lost 0.1-0.2 to the barrier and keeps its registers.
-  const bool perm_lds = perm && xf.mode == 4;
+  const bool perm_lds = perm && (xf.mode == 4 || xf.mode == 8);
   if (perm_lds && !gemv_perm_lds_fits(MT, K, (int)block.x)) return hipErrorInvalidValue;
   static const bool env_xlds = env_int("PMI_GEMV_XLDS", 1) != 0;  // benchmark sweeps only
   const bool x_lds = env_xlds && !perm && xf.mode == 0 && c.row_waves > 1 &&
@@ -922,6 +948,9 @@ hipError_t launch_cfg(const GemvConfig& c, const void* x, const uint8_t* w, cons
     if (perm) return hipErrorInvalidValue;
     if (zero_u8) PMI_GEMV_LAUNCH(6, true);
     else PMI_GEMV_LAUNCH(6, false);
+  } else if (perm_lds && xf.mode == 8) {
+    if (zero_u8) PMI_GEMV_LAUNCH(8, true);
+    else PMI_GEMV_LAUNCH(8, false);
   } else if (perm_lds) {
     if (zero_u8) PMI_GEMV_LAUNCH(4, true);
     else PMI_GEMV_LAUNCH(4, false);
@@ -1094,8 +1123,10 @@ hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, con
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream, const GemvXform* xform) {
   const GemvXform xf = xform ? *xform : GemvXform{};
-  // bf16 activations (mode 6) take the plain tuning
-  const int tune_mode = xf.mode == 6 ? 0 : (perm || xf.mode != 4 ? xf.mode : 0);
+  // bf16 activations (mode 6) take the plain tuning, the 16-bit permutation
+  // (mode 8) that of mode 4
+  const int tune_mode =
+      xf.mode == 6 ? 0 : xf.mode == 8 ? (perm ? 4 : 0) : (perm || xf.mode != 4 ? xf.mode : 0);
   const GemvConfig c = gemv_config(M, N, K, tune_mode);
   const int n = (int)N, k = (int)K, g = (int)gs;
   switch (M) {

@@ -65,6 +65,22 @@ __global__ void zeros_to_u8_kernel(const float* __restrict__ zeros, uint8_t* __r
   if (bad && local_bad) atomicAdd(bad, local_bad);
 }
 
+// int32 act_order permutation -> its 16-bit copy (K <= 65536) for the GEMV's
+// LDS gather. Entries outside [0, K) become 0, as the kernels clamp them at
+// use, and are counted into *bad (nullable).
+__global__ void perm_u16_kernel(const int32_t* __restrict__ perm, uint16_t* __restrict__ out,
+                                int32_t* __restrict__ bad, int64_t K) {
+  int local_bad = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < K;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t p = perm[i];
+    const bool ok = p >= 0 && (int64_t)p < K;
+    local_bad += ok ? 0 : 1;
+    out[i] = ok ? (uint16_t)p : (uint16_t)0;
+  }
+  if (bad && local_bad) atomicAdd(bad, local_bad);
+}
+
 // [N, G] -> [G, N] copies of the scales and zero points (zeros to u8, values
 // that are not integers in [0, 15] counted like zeros_to_u8_kernel). One
 // thread per output element: writes are coalesced, reads strided; it runs
@@ -392,6 +408,13 @@ hipError_t launch_zeros_to_u8(const float* zeros, uint8_t* out, int32_t* bad, in
                               hipStream_t stream) {
   hipLaunchKernelGGL(zeros_to_u8_kernel, dim3(grid_for(count)), dim3(kBlock), 0, stream, zeros,
                      out, bad, count);
+  return hipGetLastError();
+}
+
+hipError_t launch_perm_u16(const int32_t* perm, uint16_t* out, int32_t* bad, int64_t K,
+                           hipStream_t stream) {
+  hipLaunchKernelGGL(perm_u16_kernel, dim3(grid_for(K)), dim3(kBlock), 0, stream, perm, out, bad,
+                     K);
   return hipGetLastError();
 }
 

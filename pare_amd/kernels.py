@@ -119,6 +119,7 @@ def matmul_w4a16(
     group_size: int,
     *,
     perm: torch.Tensor | None = None,
+    perm16: torch.Tensor | None = None,
     sz_gm: tuple[torch.Tensor, torch.Tensor] | None = None,
     w_tiled: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
@@ -132,7 +133,9 @@ def matmul_w4a16(
       zeros:         same shape as scales; fp32 integer values or uint8.
       group_size:    quantisation group size; the K-tile of the kernel layout.
     Extensions: ``perm`` (int32 [K]) for act_order layers whose weights were
-    repacked with the same permutation; ``sz_gm``, the group-major copies of
+    repacked with the same permutation, and ``perm16``, its ``pack.perm_u16``
+    copy, which the GEMV's act_order gather reads instead (same results);
+    ``sz_gm``, the group-major copies of
     scales and zeros from ``pack.sz_group_major`` (fp32 and uint8 [G, N]), which
     the MFMA GEMM reads as contiguous runs; ``w_tiled``, the ``pack.tile_w4a16``
     copy of the weights, which (with ``sz_gm``) lets 3..32 activation rows run
@@ -145,7 +148,7 @@ def matmul_w4a16(
         raise RuntimeError("matmul_w4a16 requires HIP (cuda) tensors.")
     assert x.is_contiguous(), "x must be contiguous"
     assert x.dtype == torch.float16, f"x must be float16, got {x.dtype}"
-    return _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out)
+    return _matmul(x, packed_weight, scales, zeros, group_size, perm, perm16, sz_gm, w_tiled, out)
 
 
 def matmul_w4a16_bf16(
@@ -156,6 +159,7 @@ def matmul_w4a16_bf16(
     group_size: int,
     *,
     perm: torch.Tensor | None = None,
+    perm16: torch.Tensor | None = None,
     sz_gm: tuple[torch.Tensor, torch.Tensor] | None = None,
     w_tiled: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
@@ -173,10 +177,10 @@ def matmul_w4a16_bf16(
         raise RuntimeError("matmul_w4a16_bf16 requires HIP (cuda) tensors.")
     assert x.is_contiguous(), "x must be contiguous"
     assert x.dtype == torch.bfloat16, f"x must be bfloat16, got {x.dtype}"
-    return _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out)
+    return _matmul(x, packed_weight, scales, zeros, group_size, perm, perm16, sz_gm, w_tiled, out)
 
 
-def _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, out):
+def _matmul(x, packed_weight, scales, zeros, group_size, perm, perm16, sz_gm, w_tiled, out):
     """The shared argument checks and the pmi_matmul_w4a16 call (x fp16 or
     bf16, y of the same dtype)."""
     L = _lib.lib()
@@ -202,6 +206,11 @@ def _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, o
         assert perm.dtype == torch.int32 and perm.numel() == K and perm.device == dev, \
             "perm must be an int32 [K] tensor on x's device"
         perm = perm.contiguous()
+    if perm16 is not None:
+        assert perm is not None, "perm16 is given with perm"
+        assert perm16.dtype == torch.int16 and perm16.numel() == K and perm16.device == dev \
+            and perm16.is_contiguous(), "perm16 must be a contiguous int16 [K] tensor on x's device"
+        perm16 = _aligned16(perm16)
     s_gm = z_gm = None
     if sz_gm is not None:
         s_gm, z_gm = sz_gm
@@ -229,6 +238,7 @@ def _matmul(x, packed_weight, scales, zeros, group_size, perm, sz_gm, w_tiled, o
         _lib.check(L.pmi_matmul_w4a16(
             xa.data_ptr(), code, w.data_ptr(), s2.data_ptr(), z2.data_ptr(), zdt,
             perm.data_ptr() if perm is not None else None,
+            perm16.data_ptr() if perm16 is not None else None,
             s_gm.data_ptr() if s_gm is not None else None,
             z_gm.data_ptr() if z_gm is not None else None,
             w_tiled.data_ptr() if w_tiled is not None else None, out.data_ptr(), code,

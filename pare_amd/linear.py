@@ -22,9 +22,8 @@ import torch.nn.functional as F
 
 from .config import QuantConfig, is_int4, kernel_group_size
 from .kernels import kernel_choice, matmul_w4a16, matmul_w4a16_bf16
-from .pack import (dequantize_int4, perm_from_g_idx, repack_int4_for_kernel, sz_group_major,
-                   tile_w4a16, tiled_supported,
-                   zeros_to_u8)
+from .pack import (dequantize_int4, perm_from_g_idx, perm_u16, repack_int4_for_kernel,
+                   sz_group_major, tile_w4a16, tiled_supported, zeros_to_u8)
 
 
 class QuantizedLinear(nn.Module):
@@ -127,6 +126,8 @@ class QuantizedLinear(nn.Module):
             w_kernel = repack_int4_for_kernel(self.packed_weight, gs, perm=perm)
         self._packed_weight_kernel = w_kernel
         self._packed_weight_tiled = None
+        # the 16-bit copy the GEMV's act_order gather reads (None past K = 65536)
+        self._perm16 = perm_u16(perm) if perm is not None else None
         zero_u8 = zeros_to_u8(self.zero)
         self._kernel_cache = (self._stamp(), zero_u8, perm, sz_group_major(self.scale, zero_u8))
 
@@ -179,14 +180,14 @@ class QuantizedLinear(nn.Module):
             xb = x.reshape(-1, self.in_features).contiguous()
             w_t = None if perm is not None else self._tiled_buffer(w_k, xb.shape[0])
             y = matmul_w4a16_bf16(xb, w_k, self.scale, zero_u8, self._group_size(), perm=perm,
-                                  sz_gm=sz_gm, w_tiled=w_t)
+                                  perm16=self._perm16, sz_gm=sz_gm, w_tiled=w_t)
             if self.bias is not None:
                 y = y + self.bias
             return y.reshape(*orig_shape[:-1], self.out_features)
         x_2d = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
         w_t = self._tiled_buffer(w_k, x_2d.shape[0], perm)
-        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm, sz_gm=sz_gm,
-                         w_tiled=w_t)
+        y = matmul_w4a16(x_2d, w_k, self.scale, zero_u8, self._group_size(), perm=perm,
+                         perm16=self._perm16, sz_gm=sz_gm, w_tiled=w_t)
         y = y.to(x.dtype)
         if self.bias is not None:
             y = y + self.bias

@@ -161,6 +161,28 @@ def dequantize_int4(packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tenso
     return out
 
 
+def perm_u16(perm: torch.Tensor) -> torch.Tensor | None:
+    """The 16-bit copy of an act_order permutation (int16 [K] holding the
+    uint16 values) for ``matmul_w4a16(..., perm16=...)``, built once per layer;
+    None when K > 65536 (no 16-bit copy exists). Raises ValueError unless every
+    entry lies in [0, K)."""
+    L = _lib.lib()
+    _require_cuda(perm, "perm_u16")
+    assert perm.dtype == torch.int32 and perm.dim() == 1, "perm must be an int32 [K] tensor"
+    K = perm.numel()
+    if K > 65536:
+        return None
+    p = perm.contiguous()
+    out = torch.empty(K, dtype=torch.int16, device=p.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=p.device)
+    with _DeviceGuard(p.device):
+        _lib.check(L.pmi_perm_u16(p.data_ptr(), out.data_ptr(), bad.data_ptr(), K,
+                                  _stream_handle(p.device)), "pmi_perm_u16")
+    if int(bad.item()) != 0:
+        raise ValueError(f"{int(bad.item())} permutation entries lie outside [0, {K})")
+    return out
+
+
 def perm_from_g_idx(g_idx: torch.Tensor, group_size: int) -> torch.Tensor:
     """Column order that makes act_order groups contiguous: perm with
     g_idx[perm[j]] == j // group_size. Requires exactly group_size columns per

@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version(L):
-    assert L.pmi_abi_version() == _lib.ABI_VERSION == 15
+    assert L.pmi_abi_version() == _lib.ABI_VERSION == 16
 
 
 def test_kernel_choice(L):
@@ -173,9 +173,9 @@ FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by invalid
 
 
 def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.PMI_F32,
-        perm=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16, s_gm=None, z_gm=None):
-    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, s_gm, z_gm, None, y, ydt, M, N, K, gs,
-                              None, 0, None)
+        perm=None, perm16=None, y=FAKE, xdt=_lib.PMI_F16, ydt=_lib.PMI_F16, s_gm=None, z_gm=None):
+    return L.pmi_matmul_w4a16(x, xdt, w, s, z, zdt, perm, perm16, s_gm, z_gm, None, y, ydt, M, N,
+                              K, gs, None, 0, None)
 
 
 @pytest.mark.parametrize("kw,code,msg", [
@@ -193,6 +193,9 @@ def _mm(L, M=1, N=256, K=256, gs=128, x=FAKE, w=FAKE, s=FAKE, z=FAKE, zdt=_lib.P
     (dict(s_gm=FAKE), _lib.PMI_ERR_INVALID, "together"),
     (dict(z_gm=FAKE), _lib.PMI_ERR_INVALID, "together"),
     (dict(s_gm=FAKE + 2, z_gm=FAKE), _lib.PMI_ERR_INVALID, "4-byte aligned"),
+    (dict(perm16=FAKE), _lib.PMI_ERR_INVALID, "perm16 is given with perm"),
+    (dict(perm=FAKE, perm16=FAKE + 8), _lib.PMI_ERR_INVALID, "16-byte alignment"),
+    (dict(perm=FAKE, perm16=FAKE, K=65536 + 128), _lib.PMI_ERR_INVALID, "K <= 65536"),
 ])
 def test_matmul_validation(L, kw, code, msg):
     rc = _mm(L, **kw)
@@ -214,6 +217,18 @@ def test_sz_group_major_validation(L):
     rc = L.pmi_sz_group_major(FAKE, None, _lib.PMI_U8, FAKE, FAKE, None, 4, 2, None)
     assert rc == _lib.PMI_ERR_INVALID and "null" in _lib.last_error()
     assert L.pmi_sz_group_major(None, None, _lib.PMI_U8, None, None, None, 0, 2, None) == _lib.PMI_OK
+
+
+def test_perm_u16_validation(L):
+    rc = L.pmi_perm_u16(FAKE, FAKE, None, 65537, None)
+    assert rc == _lib.PMI_ERR_INVALID and "K <= 65536" in _lib.last_error()
+    rc = L.pmi_perm_u16(FAKE, FAKE + 8, None, 256, None)
+    assert rc == _lib.PMI_ERR_INVALID and "16-byte aligned" in _lib.last_error()
+    rc = L.pmi_perm_u16(FAKE + 2, FAKE, None, 256, None)
+    assert rc == _lib.PMI_ERR_INVALID and "4-byte aligned" in _lib.last_error()
+    rc = L.pmi_perm_u16(None, FAKE, None, 256, None)
+    assert rc == _lib.PMI_ERR_INVALID and "null" in _lib.last_error()
+    assert L.pmi_perm_u16(None, None, None, 0, None) == _lib.PMI_OK
 
 
 def test_repack_validation(L):

@@ -465,6 +465,69 @@ def test_gemv_act_order_lds_gather_equals_pregathered(M, N, K):
     _check_out(y, ref, f"act_order gemv lds M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 3584, 3584), (2, 3584, 3584), (3, 512, 3584),
+                                   (4, 4096, 8192), (1, 3584, 18944), (1, 512, 3584),
+                                   (1, 256, 32768)])
+def test_gemv_act_order_perm16_equals_int32(M, N, K):
+    """The GEMV's LDS gather reading the 16-bit copy of the permutation
+    (pack.perm_u16): the same columns as through the int32 table, so identical
+    bits, and within tolerance of the oracle. K = 32768 is the longest row the
+    one-row gather stages (64 KiB)."""
+    gs = 128
+    rng = np.random.default_rng(M + N + K + 1)
+    w = _w(N, K, M + 17)
+    packed, s, z, g = O.rtn_quantize_act_order(w, rng.permutation(K), gs)
+    x = _x(M, K, 13).to(DEV)
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    p16 = P.perm_u16(pm)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=pm)
+    print(f"[case] act_order gemv perm16 M={M} N={N} K={K}", flush=True)
+    with force_kernel("gemv"):
+        y32 = P.matmul_w4a16(x, wk, _cuda(s), _cuda(z), gs, perm=pm)
+        y16 = P.matmul_w4a16(x, wk, _cuda(s), _cuda(z), gs, perm=pm, perm16=p16)
+    torch.cuda.synchronize()
+    assert torch.equal(y16.view(torch.int16), y32.view(torch.int16))
+    ref = O.linear_fp32(x.float().cpu().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
+    _check_out(y16, ref, f"act_order gemv perm16 M={M} N={N} K={K}")
+
+
+def test_perm_u16_copy_and_clamp():
+    """pmi_perm_u16 copies every entry of a permutation into 16 bits (values up
+    to 65535 at K = 65536), and entries outside [0, K) become 0 and are counted,
+    the clamp the kernels apply to the int32 table at use: a malformed table
+    gives the same GEMV bits through either copy. K > 65536 has no copy."""
+    K = 65536
+    perm = torch.randperm(K, generator=torch.Generator(device=DEV).manual_seed(3),
+                          device=DEV).to(torch.int32)
+    p16 = P.perm_u16(perm)
+    assert torch.equal(p16.cpu().view(torch.uint16).to(torch.int32), perm.cpu())
+    assert P.perm_u16(torch.arange(K + 128, dtype=torch.int32, device=DEV)) is None
+    with pytest.raises(ValueError, match="outside"):
+        P.perm_u16(torch.tensor([0, 1, 5, 2], dtype=torch.int32, device=DEV))
+    # a malformed table through the C ABI: clamped and counted, same GEMV bits
+    N, K, gs = 512, 3584, 128
+    bad = torch.randperm(K, generator=torch.Generator(device=DEV).manual_seed(4),
+                         device=DEV).to(torch.int32)
+    bad[5], bad[700], bad[3000] = -1, K, K + 9
+    out = torch.empty(K, dtype=torch.int16, device=DEV)
+    cnt = torch.zeros(1, dtype=torch.int32, device=DEV)
+    L = _lib.lib()
+    assert L.pmi_perm_u16(bad.data_ptr(), out.data_ptr(), cnt.data_ptr(), K,
+                          torch.cuda.current_stream().cuda_stream) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 3
+    assert torch.equal(out.cpu().view(torch.uint16).to(torch.int32),
+                       torch.where((bad >= 0) & (bad < K), bad, 0).cpu())
+    packed, s, z = O.rtn_quantize(_w(N, K, 21), gs)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs)
+    x = _x(1, K, 22).to(DEV)
+    with force_kernel("gemv"):
+        y32 = P.matmul_w4a16(x, wk, _cuda(s), _cuda(z), gs, perm=bad)
+        y16 = P.matmul_w4a16(x, wk, _cuda(s), _cuda(z), gs, perm=bad, perm16=out)
+    torch.cuda.synchronize()
+    assert torch.equal(y16.view(torch.int16), y32.view(torch.int16))
+
+
 @pytest.mark.parametrize("M", [1, 3, 6])
 def test_gemv_act_order_gathered_equals_in_kernel_gather(M):
     """With a workspace the GEMV reads X[:, perm] gathered once; without one each
@@ -492,7 +555,7 @@ def test_gemv_act_order_gathered_equals_in_kernel_gather(M):
             y = torch.empty(M, N, dtype=torch.float16, device=DEV)
             rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
                                     zu8.data_ptr(), _lib.PMI_U8, pm.data_ptr(), None, None, None,
-                                    y.data_ptr(), _lib.PMI_F16, M, N, K, gs, wsp, nb, stream)
+                                    None, y.data_ptr(), _lib.PMI_F16, M, N, K, gs, wsp, nb, stream)
             assert rc == 0, _lib.last_error()
             outs.append(y)
     torch.cuda.synchronize()
@@ -554,7 +617,7 @@ def test_gemm_workspace_reused_across_shapes():
                 rc = L.pmi_matmul_w4a16(xd.data_ptr(), _lib.PMI_F16, wk.data_ptr(), sd.data_ptr(),
                                         zd.data_ptr(), _lib.PMI_U8,
                                         pm.data_ptr() if pm is not None else None, None, None, None,
-                                        y.data_ptr(), _lib.PMI_F16, M, N, K, gs, ws.data_ptr(),
+                                        None, y.data_ptr(), _lib.PMI_F16, M, N, K, gs, ws.data_ptr(),
                                         ws.numel(), stream)
             assert rc == 0, _lib.last_error()
             torch.cuda.synchronize()

@@ -133,7 +133,7 @@ def _abi_no_workspace(x, wk, s, zu8, sz, wt, perm, gs):
     y = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
     L = _lib.lib()
     rc = L.pmi_matmul_w4a16(x.data_ptr(), _lib.PMI_F16, wk.data_ptr(), s.data_ptr(), zu8.data_ptr(),
-                            _lib.PMI_U8, perm.data_ptr() if perm is not None else None,
+                            _lib.PMI_U8, perm.data_ptr() if perm is not None else None, None,
                             sz[0].data_ptr(), sz[1].data_ptr(), wt.data_ptr(), y.data_ptr(),
                             _lib.PMI_F16, M, N, K, gs, None, 0,
                             torch.cuda.current_stream().cuda_stream)

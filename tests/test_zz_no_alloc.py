@@ -51,8 +51,10 @@ def _call(fn, x, layer, N, K, ws=None, tiled=None):
     L = _lib.lib()
     stream = torch.cuda.current_stream().cuda_stream
     s_gm, z_gm, w_t = (t.data_ptr() for t in tiled) if tiled is not None else (None, None, None)
+    p16 = P.perm_u16(perm) if perm is not None else None  # the act_order GEMV reads it
     common = (x.data_ptr(), _lib.PMI_F16, wk.data_ptr(), s.data_ptr(), z.data_ptr(), _lib.PMI_U8,
-              perm.data_ptr() if perm is not None else None, s_gm, z_gm, w_t, y.data_ptr(),
+              perm.data_ptr() if perm is not None else None,
+              p16.data_ptr() if p16 is not None else None, s_gm, z_gm, w_t, y.data_ptr(),
               _lib.PMI_F16, M, N, K, GS)
     if fn == "noalloc":
         rc = L.pmi_matmul_w4a16_noalloc(*common, stream)
@@ -115,8 +117,8 @@ def test_noalloc_rejects_oversized_scratch():
     assert L.pmi_matmul_workspace_bytes(M, N, K, GS, 1) > (16 << 20)
     dummy = torch.zeros(16, dtype=torch.uint8, device=DEV)
     p = dummy.data_ptr()
-    rc = L.pmi_matmul_w4a16_noalloc(p, _lib.PMI_F16, p, p, p, _lib.PMI_U8, p, None, None, None, p,
-                                    _lib.PMI_F16, M, N, K, GS,
+    rc = L.pmi_matmul_w4a16_noalloc(p, _lib.PMI_F16, p, p, p, _lib.PMI_U8, p, None, None, None,
+                                    None, p, _lib.PMI_F16, M, N, K, GS,
                                     torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.PMI_ERR_UNSUPPORTED
     assert "scratch" in _lib.last_error() and "16777216" in _lib.last_error()
