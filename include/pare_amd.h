@@ -167,8 +167,9 @@ PMI_API int pmi_tile_w4a16(const uint8_t* w_kernel, uint8_t* w_tiled, int64_t N,
  * repacked with the same perm); y: fp16 [M,N].
  * perm16 (nullable; only with perm): the pmi_perm_u16 copy of perm (uint16
  * [K], 16-byte aligned, K <= 65536). The GEMV's act_order launches that stage
- * X in LDS read it instead of perm, half the bytes every workgroup reads
- * before its first gather; same results. Every other kernel reads perm.
+ * X in LDS, and the tiled GEMM's in-kernel gather (up to 16 rows), read it
+ * instead of perm: half the table bytes every workgroup reads before its
+ * first gather; same results. Every other kernel reads perm.
  * scales_gm, zeros_gm (nullable, both or neither): the pmi_sz_group_major
  * copies of scales and zeros; the MFMA GEMM reads them (one contiguous run per
  * group) instead of gathering [N,G] rows when N % 4 == 0. The other kernels

@@ -582,8 +582,8 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
                   "zeros_gm, no perm, y 8-byte aligned, group_size %% 128 == 0 and 16-row blocks", fn);
     if (bf_tiled && (forced == 5 || (!forced && pmi_matmul_kernel_choice(M, N, K, group_size,
                                                                          PMI_CHOICE_TILED) == 5)))
-      return from_hip(pmi::launch_tgemm(x, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N, K, group_size,
-                                        nullptr, 0, 0, s, true),
+      return from_hip(pmi::launch_tgemm(x, nullptr, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N,
+                                        K, group_size, nullptr, 0, 0, s, true),
                       fn);
     const uint16_t* xp = (const uint16_t*)x;
     if (perm) {
@@ -644,15 +644,15 @@ int pmi_matmul_w4a16(const void* x, int x_dtype, const uint8_t* w, const float* 
     // (the split-K partial tiles follow the counters, or the gathered X)
     void* ws = workspace_bytes >= pmi::kWsCounterBytes ? workspace : nullptr;
     if (!perm || pmi::tgemm_gather_supported(M, K))
-      return from_hip(pmi::launch_tgemm(x, perm, w_tiled, scales_gm, zeros_gm, y, M, N, K,
+      return from_hip(pmi::launch_tgemm(x, perm, perm16, w_tiled, scales_gm, zeros_gm, y, M, N, K,
                                         group_size, ws, workspace_bytes, pmi::kWsCounterBytes, s),
                       fn);
     if (workspace_bytes >= pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K)) {
       void* xg = (uint8_t*)workspace + pmi::kWsCounterBytes;
       hipError_t e = pmi::launch_gather_cols(x, perm, xg, M, K, s);
       if (e != hipSuccess) return from_hip(e, fn);
-      return from_hip(pmi::launch_tgemm(xg, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N, K,
-                                        group_size, ws, workspace_bytes,
+      return from_hip(pmi::launch_tgemm(xg, nullptr, nullptr, w_tiled, scales_gm, zeros_gm, y, M, N,
+                                        K, group_size, ws, workspace_bytes,
                                         pmi::kWsCounterBytes + pmi::ws_perm_bytes(M, K), s),
                       fn);
     }

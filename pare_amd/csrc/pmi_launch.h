@@ -256,14 +256,16 @@ BgemmConfig bgemm_config(int64_t M, int64_t N, int64_t K, int64_t gs);
 hipError_t launch_bgemm(const void* x, const uint8_t* w_tiled, const float* scales_gm,
                         const uint8_t* zeros_gm, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
                         hipStream_t stream);
-// perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null.
+// perm: act_order columns, gathered in the kernel (tgemm_gather_supported), or null;
+// perm16 (nullable, with perm): its 16-bit copy, which the gather then reads instead.
 // workspace: counters (zero between calls) at its start and the split-K partial
 // tiles at part_offset; null or too small for them, the kernel runs unsplit.
 // bf16: x and y bf16 (tgemm_bf16_supported, no perm; always one K range).
-hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
-                        const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
-                        int64_t N, int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
-                        size_t part_offset, hipStream_t stream, bool bf16 = false);
+hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint16_t* perm16,
+                        const uint8_t* w_tiled, const float* scales_gm, const uint8_t* zeros_gm,
+                        void* y, int64_t M, int64_t N, int64_t K, int64_t gs, void* workspace,
+                        size_t ws_bytes, size_t part_offset, hipStream_t stream,
+                        bool bf16 = false);
 bool tgemm_bf16_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 // silu(gate) * up from a fused gate/up weight whose rows are interleaved in
 // groups of four (rows 4n + {0, 1} of a 64-row panel p: gate rows 32 p + 2 n +

@@ -48,7 +48,8 @@
 // 2 perm[c], out-of-range entries read column 0) into LDS once, before its
 // loop; each lane then gathers its 8 columns per k-step with 2-byte LDS reads,
 // one step ahead of the MFMAs. A workgroup reads X once either way, so the
-// gather adds the 4K-byte table to its L2 traffic and no launch.
+// gather adds the 4K-byte table to its L2 traffic and no launch; 2K bytes with
+// the 16-bit copy of the permutation (GATHER 2; GATHER 1 reads the int32 one).
 //
 // Residual add + RMSNorm (NORM, up to 4 rows, K <= 4096). Every workgroup
 // reads the rows of x and of the residual ahead of its first weight loads,
@@ -90,7 +91,7 @@ constexpr int kXGPermIt = 8;         // perm-table entries per thread / 4 (K <= 
 
 struct TgemmArgs {
   const f16* x;
-  const int32_t* perm;  // act_order columns (GATHER), else null
+  const int32_t* perm;  // act_order columns (GATHER 1), their uint16 copy (GATHER 2), else null
   const uint8_t* wt;    // tiled weights
   const float* s_gm;    // fp32 [G, N]
   const uint8_t* z_gm;  // u8 [G, N]
@@ -119,6 +120,7 @@ struct TgemmArgs {
   uint32_t upg_magic;   // units per group (gs >= 128: gs / 128, else 1), 16-bit form
   uint32_t span_magic;  // grid_m > 1: 8 grid_m, 32-bit form
   uint32_t split_magic; // splits > 1: splits, 32-bit form
+  int perm_u16;         // host dispatch: perm points at the 16-bit copy (GATHER 2)
 };
 
 // Fills the derived fields of `a`; false when a quotient would leave the range
@@ -231,7 +233,7 @@ __device__ __forceinline__ bool combine_splits(const TgemmArgs& a, int wg, int s
 // element: its products x (-(128 + z)) are exact in fp32, so the group's sum
 // is sum x (q - z) up to the fp32 rounding of the accumulation; the fold and
 // the combine are those of fp16, and y is rounded to bf16 (nearest even).
-template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT = false, bool NORM = false,
+template <int MT, int NTW, int GPU, int GATHER, bool RNG, bool SPLIT = false, bool NORM = false,
           bool BF = false>
 __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_tgemm_kernel(TgemmArgs a) {
   static_assert(!GATHER || MT == 1, "the act_order gather is built for up to 16 rows");
@@ -390,7 +392,8 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
     // GATHER: X rows in 1 KiB copies (K % 512 == 0), dealt to the waves, and
     // the perm table through registers (clamped, scaled to byte offsets; the
     // table is written after the ring's first weight loads are issued, so
-    // that the latencies overlap)
+    // that the latencies overlap). From the 16-bit copy of the permutation
+    // each 16-byte load holds 8 entries instead of 4: half the loads.
     u32x4 pv[GATHER ? kXGPermIt : 1];
     auto stage_issue = [&]() {
       if constexpr (GATHER) {
@@ -401,12 +404,22 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
           copy_to_lds<16>(rx, lds + m * xstride + q * 1024, 16 * l,
                           __builtin_amdgcn_readfirstlane(m * K * 2 + q * 1024));
         }
-        const __amdgpu_buffer_rsrc_t rp = rsrc(a.perm, (int64_t)K * 4);
+        if constexpr (GATHER == 2) {
+          const __amdgpu_buffer_rsrc_t rp = rsrc(a.perm, (int64_t)K * 2);
 #pragma unroll
-        for (int i = 0; i < kXGPermIt; ++i) {
-          const int e = tid + i * kKW * 64;  // entries 4 e .. 4 e + 3
-          pv[i] = 4 * e < K ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 16 * e, 0, 0))
-                            : u32x4{0u, 0u, 0u, 0u};
+          for (int i = 0; i < kXGPermIt / 2; ++i) {
+            const int e = tid + i * kKW * 64;  // entries 8 e .. 8 e + 7
+            pv[i] = 8 * e < K ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 16 * e, 0, 0))
+                              : u32x4{0u, 0u, 0u, 0u};
+          }
+        } else {
+          const __amdgpu_buffer_rsrc_t rp = rsrc(a.perm, (int64_t)K * 4);
+#pragma unroll
+          for (int i = 0; i < kXGPermIt; ++i) {
+            const int e = tid + i * kKW * 64;  // entries 4 e .. 4 e + 3
+            pv[i] = 4 * e < K ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 16 * e, 0, 0))
+                              : u32x4{0u, 0u, 0u, 0u};
+          }
         }
       }
     };
@@ -633,14 +646,34 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (GATHER) {
+      if constexpr (GATHER == 2) {
 #pragma unroll
-      for (int i = 0; i < kXGPermIt; ++i) {
-        const int e = tid + i * kKW * 64;  // entries 4 e .. 4 e + 3
-        if (4 * e < K) {
-          u32x4 o;
+        for (int i = 0; i < kXGPermIt / 2; ++i) {
+          const int e = tid + i * kKW * 64;  // entries 8 e .. 8 e + 7 (K % 8 == 0)
+          if (8 * e < K) {
+            u32x4 o0, o1;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) o[c] = pv[i][c] < (uint32_t)K ? 2u * pv[i][c] : 0u;
-          *reinterpret_cast<u32x4*>(lds + xtab + 16 * e) = o;
+            for (int c = 0; c < 4; ++c) {
+              const uint32_t lo = pv[i][c] & 0xFFFFu, hi = pv[i][c] >> 16;
+              const uint32_t olo = lo < (uint32_t)K ? 2u * lo : 0u;
+              const uint32_t ohi = hi < (uint32_t)K ? 2u * hi : 0u;
+              if (c < 2) { o0[2 * c] = olo; o0[2 * c + 1] = ohi; }
+              else { o1[2 * c - 4] = olo; o1[2 * c - 3] = ohi; }
+            }
+            *reinterpret_cast<u32x4*>(lds + xtab + 32 * e) = o0;
+            *reinterpret_cast<u32x4*>(lds + xtab + 32 * e + 16) = o1;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kXGPermIt; ++i) {
+          const int e = tid + i * kKW * 64;  // entries 4 e .. 4 e + 3
+          if (4 * e < K) {
+            u32x4 o;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c] = pv[i][c] < (uint32_t)K ? 2u * pv[i][c] : 0u;
+            *reinterpret_cast<u32x4*>(lds + xtab + 16 * e) = o;
+          }
         }
       }
       // this wave's X copies have landed (only the ring's loads may still be
@@ -774,7 +807,7 @@ __global__ __launch_bounds__((kKW + (MT == 1 ? 0 : kProd)) * 64, 1) void w4a16_t
 
 // Launches one kernel variant; GATHER variants get their dynamic LDS beyond
 // the 64 KiB default allowed once per variant and device.
-template <int MT, int NTW, int GPU, bool GATHER, bool RNG, bool SPLIT>
+template <int MT, int NTW, int GPU, int GATHER, bool RNG, bool SPLIT>
 hipError_t launch_variant(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stream) {
   const dim3 block((kKW + (MT == 1 ? 0 : kProd)) * 64);
   size_t lds = 0;
@@ -818,11 +851,13 @@ hipError_t launch_cfg(const TgemmConfig& c, const TgemmArgs& a, hipStream_t stre
     // K split: one tile per workgroup at every group size, 2 or 4 at gs >= 128
     if constexpr (!RNG && (NTW == 1 || GPU == 1)) {
       if (a.splits > 1) {
-        if (a.perm) return launch_variant<1, NTW, GPU, true, false, true>(c, a, stream);
+        if (a.perm && a.perm_u16) return launch_variant<1, NTW, GPU, 2, false, true>(c, a, stream);
+        if (a.perm) return launch_variant<1, NTW, GPU, 1, false, true>(c, a, stream);
         return launch_variant<1, NTW, GPU, false, false, true>(c, a, stream);
       }
     }
-    if (a.perm) return launch_variant<1, NTW, GPU, true, RNG, false>(c, a, stream);
+    if (a.perm && a.perm_u16) return launch_variant<1, NTW, GPU, 2, RNG, false>(c, a, stream);
+    if (a.perm) return launch_variant<1, NTW, GPU, 1, RNG, false>(c, a, stream);
   }
   return launch_variant<MT, NTW, GPU, false, RNG, false>(c, a, stream);
 }
@@ -979,10 +1014,10 @@ bool tgemm_gather_supported(int64_t M, int64_t K) {
   return M >= 1 && M <= 16 && K <= 4 * 64 * kXGPermIt * 4 && M * (2 * K + 16) + 4 * K <= kXGLds;
 }
 
-hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_tiled,
-                        const float* scales_gm, const uint8_t* zeros_gm, void* y, int64_t M,
-                        int64_t N, int64_t K, int64_t gs, void* workspace, size_t ws_bytes,
-                        size_t part_offset, hipStream_t stream, bool bf16) {
+hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint16_t* perm16,
+                        const uint8_t* w_tiled, const float* scales_gm, const uint8_t* zeros_gm,
+                        void* y, int64_t M, int64_t N, int64_t K, int64_t gs, void* workspace,
+                        size_t ws_bytes, size_t part_offset, hipStream_t stream, bool bf16) {
   if (perm && !tgemm_gather_supported(M, K)) return hipErrorInvalidValue;
   if (bf16 && (perm || !tgemm_bf16_supported(M, N, K, gs))) return hipErrorInvalidValue;
   TgemmConfig c = tgemm_config(M, N, K, gs, perm != nullptr);
@@ -997,7 +1032,8 @@ hipError_t launch_tgemm(const void* x, const int32_t* perm, const uint8_t* w_til
   }
   TgemmArgs a;
   a.x = (const f16*)x;
-  a.perm = perm;
+  a.perm = perm && perm16 ? reinterpret_cast<const int32_t*>(perm16) : perm;
+  a.perm_u16 = perm && perm16 ? 1 : 0;
   a.wt = w_tiled;
   a.s_gm = scales_gm;
   a.z_gm = zeros_gm;
@@ -1045,6 +1081,7 @@ hipError_t launch_tgemm_glu(const void* x, const uint8_t* w_tiled, const float* 
   TgemmArgs a;
   a.x = (const f16*)x;
   a.perm = nullptr;
+  a.perm_u16 = 0;
   a.wt = w_tiled;
   a.s_gm = scales_gm;
   a.z_gm = zeros_gm;
@@ -1084,6 +1121,7 @@ hipError_t launch_tgemm_norm(const void* x, const void* r, const void* norm_w, f
   TgemmArgs a;
   a.x = (const f16*)x;
   a.perm = nullptr;
+  a.perm_u16 = 0;
   a.wt = w_tiled;
   a.s_gm = scales_gm;
   a.z_gm = zeros_gm;

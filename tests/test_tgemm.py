@@ -367,6 +367,37 @@ def test_tgemm_tile_ranges(M, N, K, act_order):
     _tgemm_case(M, N, K, 128, seed=N % 101 + M, act_order=act_order, no_workspace=True)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(16, 3584, 3584), (16, 512, 3584), (8, 18944, 3584),
+                                   (4, 1024, 4096), (1, 2048, 8192), (13, 4096, 2048)])
+def test_tgemm_gather_perm16_equals_int32(M, N, K):
+    """The in-kernel act_order gather reading the 16-bit copy of the permutation
+    (pack.perm_u16) instead of the int32 table: plain, K-split (k_v) and
+    tile-range (18944 rows) launches give identical bits, within tolerance of the
+    oracle."""
+    gs, seed = 128, N % 89 + M
+    g0 = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g0) * 0.02).numpy().astype(np.float32)
+    packed, s, z, g_idx = O.rtn_quantize_act_order(w, np.random.default_rng(seed).permutation(K), gs)
+    perm = P.perm_from_g_idx(_cuda(g_idx), gs)
+    p16 = P.perm_u16(perm)
+    wk = P.repack_int4_for_kernel(_cuda(packed), gs, perm=perm)
+    zu8 = P.zeros_to_u8(_cuda(z))
+    sz = P.sz_group_major(_cuda(s), zu8)
+    wt = P.tile_w4a16(wk, gs)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(seed + 1)).to(torch.float16)
+    print(f"[case] tgemm gather perm16 M={M} N={N} K={K}", flush=True)
+    with force_kernel("tgemm"):
+        y32 = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt, perm=perm)
+        y16 = P.matmul_w4a16(x.to(DEV), wk, _cuda(s), zu8, gs, sz_gm=sz, w_tiled=wt, perm=perm,
+                             perm16=p16)
+    torch.cuda.synchronize()
+    assert torch.equal(y16.view(torch.int16), y32.view(torch.int16))
+    ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g_idx))
+    err = np.abs(y16.float().cpu().numpy() - ref)
+    assert (err <= ATOL + RTOL * np.abs(ref)).all(), f"max_abs={err.max():.4e}"
+
+
 # ---- the big-tile variant (kernel 6): many activation rows ------------------------
 
 BGEMM_CASES = [
