@@ -53,8 +53,8 @@ struct SkinnyConfig {
 int device_cu_count();
 
 // xmode: the activation transform (GemvXform::mode). Modes whose per-workgroup
-// prologue reads all of X once (4: act_order staged in LDS, 3: RMSNorm over
-// the row) take fewer, larger workgroups on some shapes.
+// prologue reads all of X once (4 and 8: act_order staged in LDS, 3: RMSNorm
+// over the row) take fewer, larger workgroups on some shapes.
 GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode = 0);
 bool skinny_supported(int64_t M, int64_t N, int64_t K, int64_t gs);
 SkinnyConfig skinny_config(int64_t M, int64_t N, int64_t K, int64_t gs);

@@ -1064,8 +1064,14 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   bool one_batch = false;
   // act_order gather (mode 4) on such rows: one per CU, since every workgroup
   // reads the activations (2K bytes) and the permutation (4K) from L2 once
-  // (Qwen down 3584 x 18944: 13.8 against 18.1 us at two per CU)
-  if (mt == 1 && c.slices_per_wave == 2) { c.rows_per_wave = 1; wpc = xmode == 4 ? 1 : 2; }
+  // (Qwen down 3584 x 18944: 13.8 against 18.1 us at two per CU); with the
+  // 16-bit permutation (mode 8, 2K bytes) two per CU up to K = 20480 (3584 x
+  // 18944: 11.58-11.68 against 11.70-11.72 us; 4096 x 18944: 12.30-12.34
+  // against 12.78-12.81), one beyond (3584 x 32768: 15.0 against 15.3-15.4)
+  if (mt == 1 && c.slices_per_wave == 2) {
+    c.rows_per_wave = 1;
+    wpc = xmode == 4 || (xmode == 8 && K > 20480) ? 1 : 2;
+  }
   else if (mt == 1 && c.slice_waves >= 3) { c.rows_per_wave = 4; wpc = 1; }
   else if (mt == 1 && rows_per_cu >= 96 && xmode == 0) { c.rows_per_wave = 4; wpc = 1; }
   else if (mt == 1 && rows_per_cu >= 48 && xmode == 0) { c.rows_per_wave = 1; wpc = 2; }
@@ -1080,7 +1086,7 @@ GemvConfig gemv_config(int64_t M, int64_t N, int64_t K, int xmode) {
   // ring instead of a wave's only batch (6.2 against 7.3 us)
   else if (mt == 1 && rows_per_cu >= 20) {
     c.rows_per_wave = 2;
-    wpc = xmode == 4 || xmode == 5 ? 1 : 3;
+    wpc = xmode == 4 || xmode == 8 || xmode == 5 ? 1 : 3;
   }
   else if (mt > 1 && rows_per_cu >= 48) { c.rows_per_wave = 2; wpc = 2; }
   else one_batch = true;
@@ -1123,10 +1129,9 @@ hipError_t launch_gemv(const void* x, const uint8_t* w, const float* scales, con
                        int zero_u8, const int32_t* perm, void* y, int64_t M, int64_t N,
                        int64_t K, int64_t gs, hipStream_t stream, const GemvXform* xform) {
   const GemvXform xf = xform ? *xform : GemvXform{};
-  // bf16 activations (mode 6) take the plain tuning, the 16-bit permutation
-  // (mode 8) that of mode 4
+  // bf16 activations (mode 6) take the plain tuning
   const int tune_mode =
-      xf.mode == 6 ? 0 : xf.mode == 8 ? (perm ? 4 : 0) : (perm || xf.mode != 4 ? xf.mode : 0);
+      xf.mode == 6 ? 0 : (perm || (xf.mode != 4 && xf.mode != 8) ? xf.mode : 0);
   const GemvConfig c = gemv_config(M, N, K, tune_mode);
   const int n = (int)N, k = (int)K, g = (int)gs;
   switch (M) {
