@@ -429,6 +429,40 @@ def reference_shapes(dev, stream):
     return rows
 
 
+def qwen_act_order(L, dev, stream, g):
+    """Config 4: the Qwen2.5-7B act_order layers at M = 1 and 16. Per shape, in
+    QWEN order: a graph of launches over enough weight copies to pass the MALL,
+    at M = 1 then at M = 16, each replayed once untimed and five times timed."""
+    import torch
+
+    qwen = {}
+    for qi, (name, N, K) in enumerate(QWEN):
+        wbytes = N * K // 2
+        n_copies = int(min(48, max(8, -(-600_000_000 // wbytes))))  # > 512 MB: beyond the MALL
+        bufs = [make_act_order_layer(N, K, 7000 + 100 * qi + c, dev) for c in range(n_copies)]
+        for b in bufs:
+            b.gm()
+            b.tiled()
+        xq = torch.randn(16, K, generator=g, device=dev).to(torch.float16)
+        yq = torch.empty(16, N, dtype=torch.float16, device=dev)
+        torch.cuda.synchronize()
+        row = {"N": N, "K": K, "copies": n_copies}
+        for M in (1, 16):
+            gq = capture(lambda s, M=M: [launch(L, b, xq, yq, M, s) for b in bufs], stream)
+            gq.replay()
+            us = time_graph(gq, 5, stream) * 1e3 / n_copies
+            byt = layer_bytes(N, K, M) + 4 * K
+            row[f"M{M}"] = {"us": round(us, 2), "GB/s": round(byt / (us * 1e-6) / 1e9, 1),
+                            "TFLOP/s": round(2 * M * N * K / (us * 1e-6) / 1e12, 2),
+                            "kernel": kernel_of(bufs[0], M)}
+            log(f"  qwen act_order {name:8s} {N:6d}x{K:6d} M={M:2d}: {row[f'M{M}']}")
+            del gq
+        qwen[name] = row
+        del bufs
+        torch.cuda.empty_cache()
+    return qwen
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -438,7 +472,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--kernel-only",
                     choices=["gate_up_m1", "gate_m64", "gate", "sweep", "narrow", "read_floor", "copy",
-                             "e2e_bs1", "e2e_bs4", "prefill"],
+                             "e2e_bs1", "e2e_bs4", "prefill", "qwen"],
                     default=None,
                     help="run only one kernel loop (for rocprofv3 counter passes): gate_up_m1 "
                          "the fused gate/up GEMV; gate the gate_proj launches at --m rows "
@@ -447,7 +481,8 @@ def main():
                          "the plain read of the gate/up weights; "
                          "e2e_bs1 / e2e_bs4: the end-to-end decoder at batch 1 / 4, 32 tokens; "
                          "prefill: the reference's 4096x4096 layer at M = 2048 (the big-tile GEMM), "
-                         "8 weight copies, graph replays")
+                         "8 weight copies, graph replays; qwen: the Qwen2.5-7B act_order layers "
+                         "(config 4) at M = 1 and 16, graph replays, as the JSON line's leg")
     ap.add_argument("--m", type=int, default=64, help="activation rows of --kernel-only gate")
     ap.add_argument("--graph", action="store_true",
                     help="--kernel-only gate_up_m1 / gate / gate_m64 / read_floor: capture one pass "
@@ -609,6 +644,10 @@ def main():
                 log(f"narrow {names} M={M}: 320 launches, kernel "
                     f"{P.kernel_choice(M, N, 4096, GS, tiled=True)}, "
                     f"{P.kernels.tgemm_splits(M, N, 4096, GS)} K range(s)")
+        return
+
+    if args.kernel_only == "qwen":
+        qwen_act_order(L, dev, stream, torch.Generator(device=dev).manual_seed(1))
         return
 
     if args.kernel_only:
@@ -793,31 +832,7 @@ def main():
     detail["reference_shapes_4096x4096"] = reference_shapes(dev, stream)
 
     # --- Qwen2.5-7B act_order layers at M = 1 and 16 (config 4) ---------------
-    qwen = {}
-    for qi, (name, N, K) in enumerate(QWEN):
-        wbytes = N * K // 2
-        n_copies = int(min(48, max(8, -(-600_000_000 // wbytes))))  # > 512 MB: beyond the MALL
-        bufs = [make_act_order_layer(N, K, 7000 + 100 * qi + c, dev) for c in range(n_copies)]
-        for b in bufs:
-            b.gm()
-            b.tiled()
-        xq = torch.randn(16, K, generator=g, device=dev).to(torch.float16)
-        yq = torch.empty(16, N, dtype=torch.float16, device=dev)
-        torch.cuda.synchronize()
-        row = {"N": N, "K": K, "copies": n_copies}
-        for M in (1, 16):
-            gq = capture(lambda s, M=M: [launch(L, b, xq, yq, M, s) for b in bufs], stream)
-            gq.replay()
-            us = time_graph(gq, 5, stream) * 1e3 / n_copies
-            byt = layer_bytes(N, K, M) + 4 * K
-            row[f"M{M}"] = {"us": round(us, 2), "GB/s": round(byt / (us * 1e-6) / 1e9, 1),
-                            "TFLOP/s": round(2 * M * N * K / (us * 1e-6) / 1e12, 2),
-                            "kernel": kernel_of(bufs[0], M)}
-            log(f"  qwen act_order {name:8s} {N:6d}x{K:6d} M={M:2d}: {row[f'M{M}']}")
-            del gq
-        qwen[name] = row
-        del bufs
-        torch.cuda.empty_cache()
+    qwen = qwen_act_order(L, dev, stream, g)
     detail["qwen_act_order"] = qwen
 
     # --- end-to-end decoder (config 5): tok/s at BS 1 and 4 -----------------
