@@ -722,7 +722,10 @@ def test_from_tensors_without_use_kernel_attr():
     assert y.shape == (2, 64)
 
 
-def test_act_order_module():
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_act_order_module(M):
+    """An act_order layer through the module: it builds the permutation from
+    g_idx and its 16-bit copy once, and the forward matches the oracle."""
     rng = np.random.default_rng(8)
     N, K, gs = 96, 512, 128
     w = _w(N, K, 8)
@@ -730,11 +733,13 @@ def test_act_order_module():
     packed, s, z, g = O.rtn_quantize_act_order(w, perm, gs)
     ql = P.QuantizedLinear(_cuda(packed), _cuda(s), _cuda(z), P.QuantConfig(group_size=gs), None,
                            K, N, use_kernel=True, g_idx=_cuda(g))
-    x = _x(4, K, 2)
+    x = _x(M, K, 2)
     with torch.no_grad():
         y = ql(x.to(DEV))
+    pm = P.perm_from_g_idx(_cuda(g), gs)
+    assert torch.equal(ql._perm16.cpu().view(torch.uint16).to(torch.int32), pm.cpu())
     ref = O.linear_fp32(x.float().numpy(), O.dequantize_gidx(O.unpack_int4(packed), s, z, g))
-    _check_out(y, ref, "act_order module")
+    _check_out(y, ref, f"act_order module M={M}")
 
 
 @pytest.mark.parametrize("M", [1, 4, 16, 64])
