@@ -465,15 +465,17 @@ def test_gemv_act_order_lds_gather_equals_pregathered(M, N, K):
     _check_out(y, ref, f"act_order gemv lds M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 3584, 3584), (2, 3584, 3584), (3, 512, 3584),
-                                   (4, 4096, 8192), (1, 3584, 18944), (1, 512, 3584),
-                                   (1, 256, 32768)])
-def test_gemv_act_order_perm16_equals_int32(M, N, K):
+@pytest.mark.parametrize("M,N,K,gs", [(1, 3584, 3584, 128), (2, 3584, 3584, 128),
+                                      (3, 512, 3584, 128), (4, 4096, 8192, 128),
+                                      (1, 3584, 18944, 128), (1, 512, 3584, 128),
+                                      (1, 256, 32768, 128), (1, 512, 4096, 32),
+                                      (2, 1024, 2048, 64), (1, 768, 4096, 256)])
+def test_gemv_act_order_perm16_equals_int32(M, N, K, gs):
     """The GEMV's LDS gather reading the 16-bit copy of the permutation
     (pack.perm_u16): the same columns as through the int32 table, so identical
     bits, and within tolerance of the oracle. K = 32768 is the longest row the
-    one-row gather stages (64 KiB)."""
-    gs = 128
+    one-row gather stages (64 KiB); group sizes 32 to 256 move the lanes' column
+    offsets within a group."""
     rng = np.random.default_rng(M + N + K + 1)
     w = _w(N, K, M + 17)
     packed, s, z, g = O.rtn_quantize_act_order(w, rng.permutation(K), gs)

@@ -368,14 +368,17 @@ def test_tgemm_tile_ranges(M, N, K, act_order):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,K", [(16, 3584, 3584), (16, 512, 3584), (8, 18944, 3584),
-                                   (4, 1024, 4096), (1, 2048, 8192), (13, 4096, 2048)])
-def test_tgemm_gather_perm16_equals_int32(M, N, K):
+@pytest.mark.parametrize("M,N,K,gs", [(16, 3584, 3584, 128), (16, 512, 3584, 128),
+                                      (8, 18944, 3584, 128), (4, 1024, 4096, 128),
+                                      (1, 2048, 8192, 128), (13, 4096, 2048, 128),
+                                      (8, 1024, 2048, 64), (4, 512, 2048, 32),
+                                      (16, 2048, 4096, 256)])
+def test_tgemm_gather_perm16_equals_int32(M, N, K, gs):
     """The in-kernel act_order gather reading the 16-bit copy of the permutation
     (pack.perm_u16) instead of the int32 table: plain, K-split (k_v) and
-    tile-range (18944 rows) launches give identical bits, within tolerance of the
-    oracle."""
-    gs, seed = 128, N % 89 + M
+    tile-range (18944 rows) launches, group sizes 32 to 256, give identical bits,
+    within tolerance of the oracle."""
+    seed = N % 89 + M
     g0 = torch.Generator().manual_seed(seed)
     w = (torch.randn(N, K, generator=g0) * 0.02).numpy().astype(np.float32)
     packed, s, z, g_idx = O.rtn_quantize_act_order(w, np.random.default_rng(seed).permutation(K), gs)
