@@ -267,7 +267,16 @@ PMI_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
 // last row (their results are never written) and inactive lanes read byte
 // offset 0 (their activations are zero). Row offsets are wave-uniform and go
 // in the SGPR offset of the buffer load; lane offsets are fixed per wave.
-template <int U, int SPW, bool ZU8>
+// The weights are read non-temporally (each byte once per launch); SZNT marks
+// the scale and zero-point loads non-temporal too, on plain activations (modes
+// 0 and 7, no residual epilogue). Measured in the decode step of four launches
+// per layer (graphs over 32 distinct layers, two boxes, A/B/C in one process
+// type): 903.7-914.4 us against 919.2-927.2 without the hint, the seven-launch
+// step 1137-1140 against 1158-1162, although the down projection alone is
+// 0.05-0.15 us slower with it; the launch that follows finds more of L2 free.
+// The fused decoder modes keep cached loads (batch-1 decoding 619 against 623
+// tok/s with the hint on them).
+template <int U, int SPW, bool ZU8, bool SZNT = false>
 PMI_DEV void load_batch(Batch<U, SPW, ZU8>& bt, const Rsrc& rs, int first_row, int row_last,
                         int row_bytes, int G, const int (&boff)[SPW], const int (&grp)[SPW]) {
 #pragma unroll
@@ -278,12 +287,13 @@ PMI_DEV void load_batch(Batch<U, SPW, ZU8>& bt, const Rsrc& rs, int first_row, i
       const u32x4 wv = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, boff[sp], n * row_bytes, 2));
       bt.w[sp][u] = wv;
+      constexpr int kAux = SZNT ? 2 : 0;
       bt.s[sp][u] = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(rs.s, grp[sp] * 4, n * G * 4, 0));
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs.s, grp[sp] * 4, n * G * 4, kAux));
       if constexpr (ZU8)
-        bt.z[sp][u] = __builtin_amdgcn_raw_buffer_load_b8(rs.z, grp[sp], n * G, 0);
+        bt.z[sp][u] = __builtin_amdgcn_raw_buffer_load_b8(rs.z, grp[sp], n * G, kAux);
       else
-        bt.z[sp][u] = __builtin_amdgcn_raw_buffer_load_b32(rs.z, grp[sp] * 4, n * G * 4, 0);
+        bt.z[sp][u] = __builtin_amdgcn_raw_buffer_load_b32(rs.z, grp[sp] * 4, n * G * 4, kAux);
     }
   }
 }
@@ -543,6 +553,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
   // at most kXCh per thread (the host checks MT * K / 8 <= kXCh * blockDim.x),
   // loaded here and written to LDS after the first weight batch is issued.
   constexpr bool kXL = kPG || XM == 7;
+  constexpr bool kSZNT = (XM == 0 || XM == 7) && !RES;  // non-temporal scale / zero loads
   constexpr int kXCh = kPG ? kGemvLdsChunks : XM == 7 ? kGemvXLdsChunks : 1;
   u32x4 xst[kXCh];
   const int n_xch = MT * K / 8;
@@ -769,20 +780,20 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     // No ring (the host picks it when every wave has one batch): batches go
     // one after the other, the first load ahead of the activation setup.
     Batch<U, SPW, ZU8> bt;
-    load_batch<U, SPW, ZU8>(bt, rs, my_row0, row_last, row_bytes, G, boff, grp);
+    load_batch<U, SPW, ZU8, kSZNT>(bt, rs, my_row0, row_last, row_bytes, G, boff, grp);
     __builtin_amdgcn_sched_barrier(0);
     stage_x();
     setup_x();
     finish(bt, 0);
     for (int b = 1; b < n_batches; ++b) {
-      load_batch<U, SPW, ZU8>(bt, rs, my_row0 + b * stride, row_last, row_bytes, G, boff, grp);
+      load_batch<U, SPW, ZU8, kSZNT>(bt, rs, my_row0 + b * stride, row_last, row_bytes, G, boff, grp);
       finish(bt, b);
     }
   } else {
     Batch<U, SPW, ZU8> ring[D];
 #pragma unroll
     for (int d = 0; d < D - 1; ++d)
-      load_batch<U, SPW, ZU8>(ring[d], rs, my_row0 + d * stride, row_last, row_bytes, G, boff,
+      load_batch<U, SPW, ZU8, kSZNT>(ring[d], rs, my_row0 + d * stride, row_last, row_bytes, G, boff,
                               grp);
     __builtin_amdgcn_sched_barrier(0);
     stage_x();
@@ -800,7 +811,7 @@ w4a16_gemv_kernel(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     for (; i < n_full; i += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        load_batch<U, SPW, ZU8>(ring[(d + D - 1) % D], rs, my_row0 + (i + d + D - 1) * stride,
+        load_batch<U, SPW, ZU8, kSZNT>(ring[(d + D - 1) % D], rs, my_row0 + (i + d + D - 1) * stride,
                                 row_last, row_bytes, G, boff, grp);
         __builtin_amdgcn_sched_barrier(0);
         finish(ring[d], i + d);
